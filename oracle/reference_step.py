@@ -1,0 +1,344 @@
+"""CPU oracle for the 4-bit AdamW step -- test infrastructure, never shipped.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline leg
+import this module, and only as the checker (or, in the bench, as the timed CPU
+restatement of the reference's own eager update).  The product
+(``adamw4bit_amd``) never imports it.
+
+It restates, with PyTorch CPU tensor operations in the reference's exact operation
+order, the parts of ``adamw4bit`` that the fused HIP step replaces:
+
+* the bounded-chunk update of the optimized backend: ``_step_chunk``
+  (``src/adamw4bit/_optimized.py:206-234``), its moment views
+  (``_moment_buffer.py:89-179``), chunk codec (``_optimized_quantization.py:37-107``)
+  and rounding rules with endpoint guards (``_compiled_quantization.py:30-109``);
+* the per-parameter driver around it: state initialization, step counting, bias
+  corrections, chunk loop and random-draw consumption
+  (``_optimized.py:145-203``, ``adamw.py:281-324``);
+* the default reference step (``adamw.py:472-805``) for the scheme set shared with
+  the optimized path; it differs only in having no endpoint guards in stochastic
+  rounding (``quantization.py:279-377``) and in drawing ``numel`` uniforms when a
+  stochastic moment is initialized (``adamw.py:524-545``).
+
+Because the operations are ATen CPU kernels called in the reference's order, the
+element arithmetic (lerp as a fused multiply-add, true division, the 8-lane by
+4-accumulator order of the per-block sums, bf16/fp16 rounding points) is the
+reference's own.  Random draws come from ``torch.Generator`` CPU streams seeded
+exactly as the reference seeds them, and every draw tensor consumed is recorded so
+a device implementation can be fed the same draws.
+
+Pinning (see ``tests/test_oracle_*.py``): golden trajectories written by
+``tests/golden/make_golden.py`` from the reference itself, the reference's
+known-answer tests (codebooks, nibble order, tie rule, scale floor, zero floor,
+first step equal to ``torch.optim.AdamW``), the EDEN invariant and brute force over
+all 16 levels on small blocks.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional, Tuple
+
+import torch
+
+BLOCK = 128
+CHUNK_NUMEL = 1 << 19  # _optimized.py:33
+QUANT_RNG_OFFSETS = {"m1": 0x1A2B3C4D, "m2": 0x5E6F7789}  # adamw.py:122-125
+
+# Codebooks from the reference's closed forms (quantization.py:201-237, 401-422, 457-497).
+_NF4 = [-1.0000000, -0.6961928, -0.5250731, -0.3949175, -0.2844414, -0.1847734, -0.0910500, 0.0,
+        0.0795803, 0.1609302, 0.2461123, 0.3379152, 0.4407098, 0.5626170, 0.7229568, 1.0000000]
+
+
+def _dynamic_map(signed: bool) -> torch.Tensor:
+    """Dettmers dynamic map with 3 exponent bits and 4 total bits (quantization.py:201-237)."""
+    values: List[float] = []
+    for i in range(3):
+        items = (2 ** i + 1) if signed else (2 ** (i + 1) + 1)
+        edges = torch.linspace(0.1, 1, items)
+        mids = (edges[:-1] + edges[1:]) / 2.0
+        values += ((10 ** (-2 + i)) * mids).tolist()
+        if signed:
+            values += (-(10 ** (-2 + i)) * mids).tolist()
+    values += [0.0, 1.0]
+    values.sort()
+    return torch.tensor(values, dtype=torch.float32)
+
+
+def codebook(mode: str) -> torch.Tensor:
+    if mode.startswith("nf4"):
+        return torch.tensor(_NF4, dtype=torch.float32)
+    if mode.startswith("sdyn4"):
+        return _dynamic_map(True)
+    if mode == "lin4_nz":
+        return torch.linspace(0.0, 1.0, 17, dtype=torch.float32)[1:]
+    if mode.startswith("lin4"):
+        return torch.linspace(0.0, 1.0, 16, dtype=torch.float32)
+    if mode.startswith("dyn4"):
+        return _dynamic_map(False)
+    raise ValueError(f"no 16-level codebook for {mode!r}")
+
+
+RTN_SCHEMES = {"nf4", "sdyn4", "lin4", "lin4_nz", "dyn4", "dyn4_nz"}
+STATE_SR_SCHEMES = {"nf4_sr", "sdyn4_sr", "lin4_sr", "dyn4_sr"}
+UPDATE_SR_SCHEMES = {"lin4_upd_sr_fp32read", "dyn4_upd_sr_fp32read", "dyn4_lookahead_sr",
+                     "dyn4_upd_sr_fp32read_nextbc"}
+NEXT_BIAS_SCHEMES = {"dyn4_lookahead_sr", "dyn4_upd_sr_fp32read_nextbc"}
+M1_SCHEMES = {"fp32", "nf4", "nf4_sr", "sdyn4", "sdyn4_sr"}            # _optimized.py:36
+M2_SCHEMES = {"fp32", "lin4", "lin4_sr", "lin4_nz", "dyn4", "dyn4_sr", "dyn4_nz"} | UPDATE_SR_SCHEMES
+
+
+def is_stochastic(mode: str) -> bool:
+    return mode in STATE_SR_SCHEMES or mode in UPDATE_SR_SCHEMES
+
+
+# ---------------------------------------------------------------------------
+# Codec
+# ---------------------------------------------------------------------------
+
+def decode(packed: torch.Tensor, scales: torch.Tensor, mode: str, numel: int) -> torch.Tensor:
+    """Packed nibbles -> float32 values (``_optimized_quantization.py:91-107``)."""
+    codes = torch.empty(numel, dtype=torch.uint8)
+    codes[0::2] = packed & 0x0F
+    codes[1::2] = packed[: numel // 2] >> 4
+    levels = torch.index_select(codebook(mode), 0, codes.to(torch.int32))
+    return (levels.view(-1, BLOCK) * scales.unsqueeze(1)).view(-1)
+
+
+def _endpoints(x: torch.Tensor, cb: torch.Tensor):
+    """searchsorted-left neighbours (``_compiled_quantization.py:30-38``)."""
+    idx = torch.searchsorted(cb, x, out_int32=True)
+    lower = (idx - 1).clamp(min=0)
+    upper = idx.clamp(max=cb.numel() - 1)
+    return lower, upper, cb[lower.long()], cb[upper.long()]
+
+
+def encode(values: torch.Tensor, mode: str, *, eden: bool = False,
+           draws: Optional[torch.Tensor] = None, bias: float = 1.0, eps: float = 1e-8,
+           guards: bool = True) -> Tuple[torch.Tensor, torch.Tensor]:
+    """float32 values (length a multiple of 128) -> (unpacked uint8 codes, float32 scales).
+
+    ``guards=True`` is the optimized path (``_optimized_quantization.py:46-88`` with the
+    rounding of ``_compiled_quantization.py``); ``guards=False`` is the reference
+    step's strategies (``quantization.py:254-377``, ``:898-971``).
+    """
+    blocked = values.view(-1, BLOCK)
+    scales = blocked.abs().max(dim=1).values.clamp_min(1e-12)
+    x = blocked / scales.unsqueeze(1)
+    cb = codebook(mode)
+    lower, upper, a, b = _endpoints(x, cb)
+    if mode in RTN_SCHEMES:
+        pick_lower = (x - a).abs() < (b - x).abs()
+        codes = torch.where(pick_lower, lower, upper)
+    elif mode in STATE_SR_SCHEMES:
+        assert draws is not None and draws.shape == x.shape
+        width = b - a
+        p = (x - a) / width.clamp_min(1e-12)
+        p = torch.where(width > 0, p, 0.0).clamp(0.0, 1.0)
+        if guards:
+            p = torch.where(x >= b, 1.0, p)
+            p = torch.where(x <= a, 0.0, p)
+        codes = torch.where(draws < p, upper, lower)
+    elif mode in UPDATE_SR_SCHEMES:
+        assert draws is not None and draws.shape == x.shape
+        s = scales.unsqueeze(1)
+        bias_c = max(float(bias), 1e-12)
+
+        def preconditioner(level: torch.Tensor) -> torch.Tensor:
+            v_hat = (s * level / bias_c).clamp_min(0.0)
+            return torch.reciprocal(v_hat.sqrt() + eps)  # ``1.0 / t`` is reciprocal(t) * 1.0
+
+        f_a, f_b, f_x = preconditioner(a), preconditioner(b), preconditioner(x)
+        den = f_a - f_b
+        p = (f_x - f_b) / den.clamp_min(1e-30)
+        p = torch.where((b > a) & (den > 0), p, 1.0).clamp(0.0, 1.0)
+        if guards:
+            p = torch.where(x >= b, 0.0, p)
+            p = torch.where(x <= a, 1.0, p)
+        codes = torch.where(draws < p, lower, upper)
+    else:
+        raise ValueError(f"unsupported scheme {mode!r}")
+    codes = codes.to(torch.uint8)
+    if mode == "dyn4_nz":
+        codes = codes.masked_fill(codes == 0, 1)
+    if eden:
+        levels = torch.index_select(cb, 0, codes.reshape(-1).to(torch.int32)).view_as(x)
+        num = (x * x).sum(dim=1)
+        den = (x * levels).sum(dim=1)
+        scales = scales * (num / den.clamp_min(1e-12))
+    return codes.reshape(-1), scales
+
+
+def pack(codes: torch.Tensor) -> torch.Tensor:
+    out = codes[0::2].clone()
+    out[: codes.numel() // 2] |= codes[1::2] << 4
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Per-parameter state and the step driver
+# ---------------------------------------------------------------------------
+
+@dataclass
+class Hyper:
+    lr: float = 1e-3
+    betas: Tuple[float, float] = (0.9, 0.95)
+    eps: float = 1e-8
+    weight_decay: float = 0.1
+
+
+@dataclass
+class MomentState:
+    scheme: str                      # effective scheme ("fp32" when ineligible)
+    values: Optional[torch.Tensor] = None   # fp32 state
+    codes: Optional[torch.Tensor] = None    # packed uint8 [(n+1)//2]
+    scales: Optional[torch.Tensor] = None   # fp32 [n/128]
+
+
+@dataclass
+class ParamState:
+    step: int = 0
+    m1: Optional[MomentState] = None
+    m2: Optional[MomentState] = None
+
+
+@dataclass
+class DrawLog:
+    """Uniform draws consumed by one write of one moment of one parameter."""
+    param: int
+    moment: str
+    step: int
+    draws: torch.Tensor  # flat float32, one per element
+
+
+def effective_scheme(numel: int, scheme: str) -> str:
+    """TorchAO eligibility (``adamw.py:807-817``)."""
+    if scheme == "fp32" or (numel >= 4096 and numel % BLOCK == 0):
+        return scheme
+    return "fp32"
+
+
+class Oracle:
+    """Multi-parameter optimizer restatement over CPU tensors.
+
+    ``optimized=True`` follows the bounded-chunk backend; ``optimized=False`` the
+    reference step.  ``m1_schemes``/``m2_schemes``/``eden`` are per parameter so
+    mixed-scheme parameter lists (runtime ``nf4_sr`` switches, ablation slices) can
+    be expressed.
+    """
+
+    def __init__(self, params: List[torch.Tensor], hyper: Hyper, m1_schemes: List[str],
+                 m2_schemes: List[str], eden: List[bool], *, seed: Optional[int] = None,
+                 optimized: bool = True, chunk: int = CHUNK_NUMEL, record_draws: bool = False):
+        self.params = params
+        self.hyper = hyper
+        self.m1_schemes = list(m1_schemes)
+        self.m2_schemes = list(m2_schemes)
+        self.eden = list(eden)
+        self.optimized = optimized
+        self.chunk = chunk
+        self.states = [ParamState() for _ in params]
+        self.generators: Dict[str, Optional[torch.Generator]] = {}
+        for moment, offset in QUANT_RNG_OFFSETS.items():
+            if seed is None:
+                self.generators[moment] = None
+            else:
+                gen = torch.Generator()
+                gen.manual_seed((seed + offset) % ((1 << 63) - 1))
+                self.generators[moment] = gen
+        self.record_draws = record_draws
+        self.draw_log: List[DrawLog] = []
+        self.draw_counts = {"m1": 0, "m2": 0}
+
+    # -- random draws -------------------------------------------------------
+    def _draw(self, moment: str, n: int, param: int, step: int, log: bool) -> torch.Tensor:
+        u = torch.rand((n // BLOCK, BLOCK), dtype=torch.float32, generator=self.generators[moment])
+        self.draw_counts[moment] += n
+        if self.record_draws and log:
+            self.draw_log.append(DrawLog(param, moment, step, u.reshape(-1).clone()))
+        return u
+
+    # -- initialization -------------------------------------------------------
+    def _init_moment(self, index: int, moment: str, scheme: str, eden: bool) -> MomentState:
+        p = self.params[index]
+        n = p.numel()
+        if scheme == "fp32":
+            return MomentState("fp32", values=torch.zeros(n, dtype=torch.float32))
+        if self.optimized:
+            # _moment_buffer.py:106-126: encode one zero tile, broadcast its first byte/scale.
+            tile = n if n <= self.chunk else math.lcm(BLOCK, 2)
+        else:
+            tile = n  # adamw.py:524-545 encodes the whole zero tensor
+        draws = self._draw(moment, tile, index, 0, log=False) if is_stochastic(scheme) else None
+        codes, scales = encode(torch.zeros(tile, dtype=torch.float32), scheme, eden=eden,
+                               draws=draws, guards=self.optimized)
+        byte = pack(codes)[:1]
+        return MomentState(scheme, codes=byte.expand((n + 1) // 2).clone(),
+                           scales=scales[:1].expand(n // BLOCK).clone())
+
+    # -- one step -------------------------------------------------------------
+    def step(self, grads: List[torch.Tensor]) -> None:
+        for index, (p, g) in enumerate(zip(self.params, grads)):
+            self._step_param(index, p, g)
+
+    def _step_param(self, index: int, p: torch.Tensor, grad: torch.Tensor) -> None:
+        st = self.states[index]
+        n = p.numel()
+        s1 = effective_scheme(n, self.m1_schemes[index])
+        s2 = effective_scheme(n, self.m2_schemes[index])
+        eden = self.eden[index]
+        if st.step == 0:
+            st.m1 = self._init_moment(index, "m1", s1, False)
+            st.m2 = self._init_moment(index, "m2", s2, eden)
+        else:
+            # A runtime m1 switch (nf4 <-> nf4_sr) keeps the codes and changes only the rule.
+            st.m1.scheme = s1
+        st.step += 1
+        b1, b2 = self.hyper.betas
+        bc1, bc2 = 1 - b1 ** st.step, 1 - b2 ** st.step
+        storage_bc = 1 - b2 ** (st.step + 1) if s2 in NEXT_BIAS_SCHEMES else bc2
+        flat_p = p.view(-1)
+        flat_g = grad.reshape(-1)
+        chunk = self._chunk_size(s1, s2) if self.optimized else n
+        for start in range(0, n, chunk):
+            stop = min(start + chunk, n)
+            self._update_chunk(index, st, flat_p[start:stop], flat_g[start:stop], start, stop,
+                               s1, s2, eden, bc1, bc2, storage_bc)
+
+    def _chunk_size(self, s1: str, s2: str) -> int:
+        sizes = [BLOCK for s in (s1, s2) if s != "fp32"]
+        align = math.lcm(2, *sizes) if sizes else 1
+        return self.chunk // align * align
+
+    def _update_chunk(self, index, st, p, grad, start, stop, s1, s2, eden, bc1, bc2, storage_bc):
+        """``_step_chunk`` (_optimized.py:206-234) on elements [start, stop)."""
+        hp = self.hyper
+        n = stop - start
+        g = grad.to(dtype=torch.float32)
+        m1 = self._read(st.m1, start, stop)
+        m2 = self._read(st.m2, start, stop)
+        m1.lerp_(g, 1 - hp.betas[0])
+        m2.lerp_(g.square(), 1 - hp.betas[1])
+        den = m2.sqrt().div_(math.sqrt(bc2)).add_(hp.eps)
+        p.mul_(1 - hp.lr * hp.weight_decay)
+        p.addcdiv_(m1, den, value=-hp.lr / bc1)
+        draws = self._draw("m1", n, index, st.step, True) if is_stochastic(s1) else None
+        self._write(st.m1, m1, start, stop, eden=False, draws=draws, bias=1.0, eps=1e-8)
+        draws = self._draw("m2", n, index, st.step, True) if is_stochastic(s2) else None
+        self._write(st.m2, m2, start, stop, eden=eden, draws=draws, bias=storage_bc, eps=hp.eps)
+
+    @staticmethod
+    def _read(ms: MomentState, start: int, stop: int) -> torch.Tensor:
+        if ms.scheme == "fp32":
+            return ms.values[start:stop]  # a view: updated in place like MomentBuffer.read
+        return decode(ms.codes[start // 2:(stop + 1) // 2], ms.scales[start // BLOCK:stop // BLOCK],
+                      ms.scheme, stop - start)
+
+    def _write(self, ms: MomentState, value, start, stop, *, eden, draws, bias, eps) -> None:
+        if ms.scheme == "fp32":
+            return  # the read view was updated in place
+        codes, scales = encode(value, ms.scheme, eden=eden, draws=draws, bias=bias, eps=eps,
+                               guards=self.optimized)
+        ms.codes[start // 2:(stop + 1) // 2] = pack(codes)
+        ms.scales[start // BLOCK:stop // BLOCK] = scales
