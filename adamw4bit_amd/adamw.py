@@ -1,0 +1,649 @@
+"""``QuantizedAdamW`` and its 4-bit recipes, stepped by one fused HIP launch per step.
+
+Drop-in for the optimizer API of ``adamw4bit`` (reference ``src/adamw4bit/adamw.py``):
+same constructor arguments and validation (``adamw.py:127-239``), the
+ZIP-SR / ZE-EDEN recipe subclasses (``:869-892``), runtime m1 retargeting
+(``:251-279``), the per-(moment, device) quantization RNG streams keyed by
+``quant_rng_seed`` (``:281-324``) and the packed-code / block-scale
+``state_dict`` layout with its ``_quant_rng_state`` payload (``:326-470``).
+
+``step()`` gathers every parameter with a gradient into a launch table and
+calls ``aw4_fused_step`` once per device: decode -> AdamW -> re-encode for all
+tensors, fp32-state tensors included, in one kernel.  With ``optimized=True`` a
+parameter follows the optimized backend's semantics (``_optimized.py:85-234``:
+exact-level guards in stochastic rounding, one-tile initial draws); parameters
+the backend's preflight would reject, and every parameter when
+``optimized=False``, follow the reference step (``adamw.py:472-805``), which
+differs only in those two points.
+
+Outside this build (raise ``NotImplementedError`` on construction): 8-bit state
+(``linear``/``dynamic``, ``AdamW8bit``), the research m2 variants
+``*_upd_sr``, ``*_upd_sr_store_eden`` and the lookahead proxies, update
+clipping, diagnostics recording and telemetry callbacks.  Parameters must live
+on a HIP device; there is no CPU implementation.
+"""
+
+from __future__ import annotations
+
+import math
+from collections.abc import Mapping
+from typing import Any, Dict, Iterable, Iterator, List, Optional, Tuple
+
+import numpy as np
+import torch
+from torch.optim.optimizer import Optimizer
+
+from . import _lib
+from ._rng import PhiloxStream
+from .quantization import (
+    NEXT_BIAS_SCHEMES,
+    QuantState,
+    ROUND_STATE_SR,
+    ROUND_UPDATE_SR,
+    SCHEMES,
+    default_block_size,
+    initial_code_and_scale,
+    pack_4bit_codes,
+)
+
+_TORCHAO_MIN_QUANT_NUMEL = 4096           # adamw.py:19
+_CHUNK_NUMEL = 1 << 19                    # _optimized.py:33
+_CHUNK_KEY = "max_chunk_numel"            # _optimized.py:34
+_FALLBACK_KEY = "_optimized_full_fallback"  # _optimized.py:35
+# Schemes the optimized backend accepts (_optimized.py:36-41).
+_OPT_M1_SCHEMES = {"fp32", "nf4", "nf4_sr", "sdyn4", "sdyn4_sr"}
+_OPT_M2_SCHEMES = {
+    "fp32", "lin4", "lin4_sr", "lin4_nz", "dyn4", "dyn4_sr", "dyn4_nz",
+    "lin4_upd_sr_fp32read", "dyn4_upd_sr_fp32read", "dyn4_lookahead_sr", "dyn4_upd_sr_fp32read_nextbc",
+}
+_DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
+_UNSUPPORTED_SCHEMES = {
+    "linear": "8-bit linear state", "dynamic": "8-bit dynamic state",
+    "lin4_upd_sr": "update-unbiased SR with a sampled read", "dyn4_upd_sr": "update-unbiased SR with a sampled read",
+    "lin4_upd_sr_store_eden": "update-SR with store-side EDEN", "dyn4_upd_sr_store_eden": "update-SR with store-side EDEN",
+    "dyn4_la_upd_sr": "oracle lookahead update-SR", "dyn4_proxy_la_upd_sr": "proxy lookahead update-SR",
+    "dyn4_vproxy_la_upd_sr": "v-proxy lookahead update-SR",
+}
+
+
+def _f32(x: float) -> float:
+    return float(np.float32(x))
+
+
+def _rcp32(x: float) -> float:
+    """Correctly rounded fp32 reciprocal of the fp32 value ``x``."""
+    return float(np.float32(1.0) / np.float32(x))
+
+
+def _byte_range(t: torch.Tensor) -> Tuple[str, int, int]:
+    """Storage interval of a tensor (``_moment_buffer.py:13-20``)."""
+    if t.is_contiguous():
+        start = t.data_ptr()
+        return str(t.device), start, start + t.numel() * t.element_size()
+    storage = t.untyped_storage()
+    return str(t.device), storage.data_ptr(), storage.data_ptr() + storage.nbytes()
+
+
+def _overlaps(a, b) -> bool:
+    return a[0] == b[0] and a[1] < b[2] and b[1] < a[2]
+
+
+def _moment_tensors(state: Dict[str, Any]) -> List[torch.Tensor]:
+    """Writable moment buffers of one parameter (``_moment_buffer.py:22-41``)."""
+    out = []
+    for key in ("m1", "m2"):
+        for name in (key, f"{key}_code"):
+            value = state.get(name)
+            if isinstance(value, torch.Tensor) and value.layout == torch.strided and value.numel():
+                out.append(value)
+        meta = state.get(f"{key}_quant_state")
+        if (isinstance(meta, QuantState) and isinstance(meta.absmax, torch.Tensor)
+                and meta.absmax.layout == torch.strided and meta.absmax.numel()):
+            out.append(meta.absmax)
+    return out
+
+
+class QuantizedAdamW(Optimizer):
+    r"""AdamW with 4-bit or fp32 moment storage, stepped on the GPU by one fused kernel.
+
+    Arguments, defaults and validation follow ``adamw4bit.QuantizedAdamW``
+    (reference ``adamw.py:46-239``).  ``optimized`` selects the optimized
+    backend's stochastic-rounding guards and initial-draw accounting; both
+    settings run the same fused kernel.
+    """
+
+    _VALID_SCHEMES = (
+        "linear", "dynamic",
+        "sdyn4", "sdyn4_sr", "nf4", "nf4_sr",
+        "lin4", "lin4_sr", "lin4_upd_sr", "lin4_upd_sr_store_eden", "lin4_upd_sr_fp32read", "lin4_nz",
+        "dyn4", "dyn4_sr", "dyn4_upd_sr", "dyn4_upd_sr_store_eden", "dyn4_upd_sr_fp32read",
+        "dyn4_lookahead_sr", "dyn4_upd_sr_fp32read_nextbc", "dyn4_la_upd_sr", "dyn4_proxy_la_upd_sr",
+        "dyn4_vproxy_la_upd_sr", "dyn4_nz",
+        "fp32",
+    )
+    _UPDATE_SR_STORE_EDEN_SCHEMES = {"lin4_upd_sr_store_eden", "dyn4_upd_sr_store_eden"}
+    _ORACLE_LOOKAHEAD_UPDATE_SR_SCHEMES = {"dyn4_la_upd_sr"}
+    _PROXY_LOOKAHEAD_UPDATE_SR_SCHEMES = {"dyn4_proxy_la_upd_sr"}
+    _VPROXY_LOOKAHEAD_UPDATE_SR_SCHEMES = {"dyn4_vproxy_la_upd_sr"}
+    _QUANT_RNG_STATE_KEY = "_quant_rng_state"
+    _QUANT_RNG_OFFSETS = {"m1": 0x1A2B3C4D, "m2": 0x5E6F7789}  # adamw.py:122-125
+
+    def __init__(self,
+                 params: Iterator[torch.nn.Parameter],
+                 lr: float = 1e-3,
+                 betas: Tuple[float, float] = (0.9, 0.95),
+                 eps: float = 1e-8,
+                 weight_decay: float = 1e-1,
+                 block_size: Optional[int] = None,
+                 quant_scheme: str = "linear",
+                 use_eden_m2: bool = False,
+                 m1_quant_scheme: Optional[str] = None,
+                 m2_quant_scheme: Optional[str] = None,
+                 quant_rng_seed: Optional[int] = None,
+                 telemetry=None,
+                 update_sign_clip: Optional[float] = None,
+                 update_norm_clip: Optional[float] = None,
+                 record_update_direction_every: Optional[int] = None,
+                 record_preconditioner_every: Optional[int] = None,
+                 record_preconditioner_steps=None,
+                 optimized: bool = False):
+        # Validation, messages and order as adamw.py:148-208.
+        if not 0.0 <= lr:
+            raise ValueError(f"Invalid learning rate: {lr}")
+        if not 0.0 <= eps:
+            raise ValueError(f"Invalid epsilon value: {eps}")
+        if not 0.0 <= betas[0] < 1.0:
+            raise ValueError(f"Invalid beta parameter at index 0: {betas[0]}")
+        if not 0.0 <= betas[1] < 1.0:
+            raise ValueError(f"Invalid beta parameter at index 1: {betas[1]}")
+        if not 0.0 <= weight_decay:
+            raise ValueError(f"Invalid weight_decay value: {weight_decay}")
+        if quant_rng_seed is not None and (
+            isinstance(quant_rng_seed, bool) or not isinstance(quant_rng_seed, int) or quant_rng_seed < 0
+        ):
+            raise ValueError(f"quant_rng_seed must be a non-negative integer or None, got {quant_rng_seed!r}")
+        if update_sign_clip is not None and not update_sign_clip > 0.0:
+            raise ValueError(f"update_sign_clip must be positive or None, got {update_sign_clip}")
+        if update_norm_clip is not None and not update_norm_clip > 0.0:
+            raise ValueError(f"update_norm_clip must be positive or None, got {update_norm_clip}")
+        if update_sign_clip is not None and update_norm_clip is not None:
+            raise ValueError("Set at most one of update_sign_clip / update_norm_clip "
+                             "(they are alternative update-clip mechanisms).")
+        if record_update_direction_every is not None and record_update_direction_every <= 0:
+            raise ValueError("record_update_direction_every must be positive or None, "
+                             f"got {record_update_direction_every}")
+        if record_preconditioner_every is not None and record_preconditioner_every <= 0:
+            raise ValueError("record_preconditioner_every must be positive or None, "
+                             f"got {record_preconditioner_every}")
+        if record_preconditioner_steps is not None:
+            record_preconditioner_steps = tuple(sorted(set(int(s) for s in record_preconditioner_steps)))
+            if any(s <= 0 for s in record_preconditioner_steps):
+                raise ValueError("record_preconditioner_steps must contain positive optimizer steps")
+
+        m1_scheme = m1_quant_scheme or quant_scheme
+        m2_scheme = m2_quant_scheme or quant_scheme
+        for name, s in (("quant_scheme", quant_scheme), ("m1_quant_scheme", m1_scheme),
+                        ("m2_quant_scheme", m2_scheme)):
+            if s not in self._VALID_SCHEMES:
+                raise ValueError(f"{name} must be one of {self._VALID_SCHEMES}, got {s!r}")
+        if use_eden_m2 and m2_scheme in {"lin4_sr", "dyn4_sr"}:
+            raise ValueError("Vanilla stochastic-rounding m2 schemes should not be combined with use_eden_m2")
+        if use_eden_m2 and m2_scheme in self._UPDATE_SR_STORE_EDEN_SCHEMES:
+            raise ValueError("Do not set use_eden_m2 with *_upd_sr_store_eden; EDEN is built into the store path")
+        if m2_scheme in (self._ORACLE_LOOKAHEAD_UPDATE_SR_SCHEMES | self._PROXY_LOOKAHEAD_UPDATE_SR_SCHEMES
+                         | self._VPROXY_LOOKAHEAD_UPDATE_SR_SCHEMES):
+            if m1_scheme not in {"fp32", "nf4"}:
+                raise ValueError("lookahead update-SR currently supports m1_quant_scheme='fp32' or 'nf4'")
+            if use_eden_m2:
+                raise ValueError("lookahead update-SR should not be combined with use_eden_m2")
+            if update_sign_clip is not None or update_norm_clip is not None:
+                raise ValueError("lookahead update-SR should not be combined with update clipping")
+
+        # The parts of the reference API outside the fused 4-bit path.
+        for name, s in (("m1_quant_scheme", m1_scheme), ("m2_quant_scheme", m2_scheme)):
+            if s in _UNSUPPORTED_SCHEMES:
+                raise NotImplementedError(
+                    f"{name}={s!r} ({_UNSUPPORTED_SCHEMES[s]}) is not part of the fused 4-bit HIP step")
+        for name, value in (("telemetry", telemetry), ("update_sign_clip", update_sign_clip),
+                            ("update_norm_clip", update_norm_clip),
+                            ("record_update_direction_every", record_update_direction_every),
+                            ("record_preconditioner_every", record_preconditioner_every),
+                            ("record_preconditioner_steps", record_preconditioner_steps)):
+            if value is not None:
+                raise NotImplementedError(f"{name} is not part of the fused 4-bit HIP step")
+        if block_size is not None and block_size != _lib.BLOCK:
+            raise NotImplementedError(f"block_size={block_size}: the fused step encodes {_lib.BLOCK}-value blocks")
+
+        self.telemetry = telemetry
+        self._m1_quant_scheme_overrides: Dict[int, str] = {}
+        self._quant_rng_seed = quant_rng_seed
+        self._quant_generators: Dict[str, Dict[str, PhiloxStream]] = {"m1": {}, "m2": {}}
+        self._pending_quant_rng_states: Dict[str, Dict[str, torch.Tensor]] = {"m1": {}, "m2": {}}
+        self._global_streams: Dict[str, Dict[str, PhiloxStream]] = {"m1": {}, "m2": {}}
+        defaults = dict(lr=lr, betas=betas, eps=eps, weight_decay=weight_decay,
+                        block_size=block_size, quant_scheme=quant_scheme, use_eden_m2=use_eden_m2,
+                        m1_quant_scheme=m1_scheme, m2_quant_scheme=m2_scheme,
+                        update_sign_clip=update_sign_clip, update_norm_clip=update_norm_clip,
+                        record_update_direction_every=record_update_direction_every,
+                        record_preconditioner_every=record_preconditioner_every,
+                        record_preconditioner_steps=record_preconditioner_steps)
+        super().__init__(params, defaults)
+        self._optimized = optimized
+        # Test hook: callable(param, moment, numel, device) -> fp32 uniforms used instead of the
+        # on-device Philox draws of a stochastic write (bit-exact comparisons with fed draws).
+        self._draw_provider = None
+        if optimized:
+            for group in self.param_groups:
+                group.setdefault(_CHUNK_KEY, _CHUNK_NUMEL)
+            self.register_load_state_dict_post_hook(self._after_load)
+
+    # ------------------------------------------------------------------
+    # Scheme resolution (adamw.py:241-279, 807-817)
+    # ------------------------------------------------------------------
+    def _m1_scheme_for(self, parameter: torch.Tensor, group_scheme: str) -> str:
+        return self._m1_quant_scheme_overrides.get(id(parameter), group_scheme)
+
+    def set_m1_quant_scheme_for_parameters(self, parameters: Iterable[torch.nn.Parameter], scheme: str) -> None:
+        """Retarget future m1 writes for existing optimizer parameters."""
+        if scheme not in {"nf4", "nf4_sr"}:
+            raise ValueError("runtime m1 retargeting supports only nf4 and nf4_sr")
+        optimizer_parameter_ids = {id(p) for group in self.param_groups for p in group["params"]}
+        selected = list(parameters)
+        if not selected:
+            raise ValueError("runtime m1 retargeting requires parameters")
+        if any(id(p) not in optimizer_parameter_ids for p in selected):
+            raise ValueError("runtime m1 retargeting received parameters outside optimizer")
+        for p in selected:
+            self._m1_quant_scheme_overrides[id(p)] = scheme
+
+    @staticmethod
+    def _eligible_for_quantized_state(p: torch.Tensor, block_size: int) -> bool:
+        n = p.numel()
+        return n >= _TORCHAO_MIN_QUANT_NUMEL and n % block_size == 0
+
+    @classmethod
+    def _effective_scheme(cls, p: torch.Tensor, scheme: str, block_size: int) -> str:
+        if scheme == "fp32" or cls._eligible_for_quantized_state(p, block_size):
+            return scheme
+        return "fp32"
+
+    # ------------------------------------------------------------------
+    # Quantization RNG streams (adamw.py:281-324)
+    # ------------------------------------------------------------------
+    def _quant_generator(self, moment: str, device: torch.device) -> Optional[PhiloxStream]:
+        if self._quant_rng_seed is None:
+            return None
+        if moment not in self._QUANT_RNG_OFFSETS:
+            raise ValueError(f"Unsupported quantization RNG stream: {moment!r}")
+        device_key = str(device)
+        generators = self._quant_generators[moment]
+        if device_key in generators:
+            return generators[device_key]
+        stream = PhiloxStream((self._quant_rng_seed + self._QUANT_RNG_OFFSETS[moment]) % ((1 << 63) - 1))
+        pending = self._pending_quant_rng_states[moment]
+        state = pending.pop(device_key, None)
+        if state is None:
+            compatible = [k for k in pending if k.split(":", maxsplit=1)[0] == device.type]
+            if len(compatible) == 1:
+                state = pending.pop(compatible[0])
+            elif pending:
+                raise ValueError(f"Unable to restore quantization RNG state for {moment} on {device}; "
+                                 f"saved devices={sorted(pending)}")
+        if state is not None:
+            stream.set_state(state)
+        generators[device_key] = stream
+        return stream
+
+    def _stream(self, moment: str, device: torch.device) -> PhiloxStream:
+        """The stream a stochastic write of ``moment`` draws from on ``device``."""
+        stream = self._quant_generator(moment, device)
+        if stream is not None:
+            return stream
+        # quant_rng_seed=None: the reference draws from torch's global RNG; here a
+        # per-(moment, device) stream keyed once from torch's global generator.
+        key = str(device)
+        streams = self._global_streams[moment]
+        if key not in streams:
+            streams[key] = PhiloxStream(int(torch.randint(0, (1 << 62) - 1, (1,)).item()))
+        return streams[key]
+
+    # ------------------------------------------------------------------
+    # Checkpoints (adamw.py:326-470, _optimized.py:53-83)
+    # ------------------------------------------------------------------
+    def state_dict(self):
+        result = super().state_dict()
+        result["state"] = {
+            index: {key: vars(value).copy() if isinstance(value, QuantState) else value
+                    for key, value in parameter_state.items()}
+            for index, parameter_state in result["state"].items()
+        }
+        if self._quant_rng_seed is None:
+            return result
+        states = {moment: {device: state.detach().cpu().clone()
+                           for device, state in self._pending_quant_rng_states[moment].items()}
+                  for moment in self._QUANT_RNG_OFFSETS}
+        for moment, generators in self._quant_generators.items():
+            states[moment].update({device: g.get_state() for device, g in generators.items()})
+        result[self._QUANT_RNG_STATE_KEY] = {"version": 1, "seed": self._quant_rng_seed, "states": states}
+        return result
+
+    def load_state_dict(self, state_dict):
+        """Restore fp32 moments and integer codes on each parameter's device."""
+        rng_payload = state_dict.get(self._QUANT_RNG_STATE_KEY)
+        optimizer_state = {k: v for k, v in state_dict.items() if k != self._QUANT_RNG_STATE_KEY}
+
+        def capture_state(_optimizer, loaded_state):
+            nonlocal optimizer_state
+            optimizer_state = loaded_state
+
+        def restore_moments(_optimizer):
+            for group, saved_group in zip(self.param_groups, optimizer_state["param_groups"]):
+                for parameter, saved_index in zip(group["params"], saved_group["params"]):
+                    original = optimizer_state["state"].get(saved_index, {})
+                    if not original:
+                        continue
+                    state = self.state[parameter]
+                    for key in ("m1", "m2", "lookahead_pending_exp_avg_sq", "m2_read_preconditioner"):
+                        if key in original:
+                            state[key] = original[key].to(device=parameter.device, dtype=torch.float32)
+                    for key in ("m1_quant_state", "m2_quant_state"):
+                        if key in original:
+                            value = original[key]
+                            fields = dict(value) if isinstance(value, Mapping) else vars(value).copy()
+                            fields["absmax"] = fields["absmax"].to(device=parameter.device, dtype=torch.float32)
+                            state[key] = QuantState(**fields)
+                    schemes = {"m1": self._m1_scheme_for(parameter, group["m1_quant_scheme"]),
+                               "m2": group["m2_quant_scheme"]}
+                    for key, scheme in schemes.items():
+                        code_key = f"{key}_code"
+                        if code_key in original:
+                            code_dtype = torch.int8 if scheme == "linear" else torch.uint8
+                            state[code_key] = original[code_key].to(device=parameter.device, dtype=code_dtype)
+
+        capture_hook = self.register_load_state_dict_pre_hook(capture_state)
+        restore_hook = self.register_load_state_dict_post_hook(restore_moments, prepend=True)
+        try:
+            result = super().load_state_dict(optimizer_state)
+        finally:
+            capture_hook.remove()
+            restore_hook.remove()
+        self._quant_generators = {"m1": {}, "m2": {}}
+        self._pending_quant_rng_states = {"m1": {}, "m2": {}}
+        if rng_payload is not None:
+            if not isinstance(rng_payload, Mapping):
+                raise ValueError("Invalid quantization RNG checkpoint payload")
+            if rng_payload.get("version") != 1:
+                raise ValueError(f"Unsupported quantization RNG checkpoint version: {rng_payload.get('version')!r}")
+            if self._quant_rng_seed is None:
+                raise ValueError("Checkpoint contains separated quantization RNG state, but quant_rng_seed is disabled")
+            saved_seed = rng_payload.get("seed")
+            if saved_seed != self._quant_rng_seed:
+                raise ValueError(f"Quantization RNG seed mismatch: checkpoint={saved_seed!r}, "
+                                 f"configured={self._quant_rng_seed!r}")
+            saved_states = rng_payload.get("states")
+            if not isinstance(saved_states, Mapping):
+                raise ValueError("Quantization RNG checkpoint states are missing")
+            for moment in self._QUANT_RNG_OFFSETS:
+                moment_states = saved_states.get(moment, {})
+                if not isinstance(moment_states, Mapping):
+                    raise ValueError(f"Invalid quantization RNG states for {moment}")
+                for device, state in moment_states.items():
+                    if not isinstance(device, str) or not torch.is_tensor(state):
+                        raise ValueError(f"Invalid quantization RNG state entry for {moment}")
+                    self._pending_quant_rng_states[moment][device] = state.detach().cpu().clone()
+        return result
+
+    @staticmethod
+    def _after_load(optimizer: "QuantizedAdamW") -> None:
+        """Mark parameters whose loaded moment storage aliases another's (``_optimized.py:53-83``)."""
+        intervals = []
+        for group in optimizer.param_groups:
+            group.setdefault(_CHUNK_KEY, _CHUNK_NUMEL)
+            for parameter in group["params"]:
+                for tensor in _moment_tensors(optimizer.state.get(parameter, {})):
+                    intervals.append((*_byte_range(tensor), id(parameter)))
+        intervals.sort()
+        aliased, owners = set(), set()
+        device, end, count = "", 0, 0
+        for current_device, start, stop, owner in intervals:
+            if current_device != device or start >= end:
+                if count > 1:
+                    aliased.update(owners)
+                device, end, count, owners = current_device, stop, 1, {owner}
+            else:
+                end = max(end, stop)
+                count += 1
+                owners.add(owner)
+        if count > 1:
+            aliased.update(owners)
+        for group in optimizer.param_groups:
+            for parameter in group["params"]:
+                if id(parameter) in aliased:
+                    optimizer.state[parameter][_FALLBACK_KEY] = True
+
+    # ------------------------------------------------------------------
+    # The step
+    # ------------------------------------------------------------------
+    @torch.no_grad()
+    def step(self, closure=None):  # type: ignore[override]
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+        per_device: Dict[torch.device, List[Tuple]] = {}
+        keep: List[torch.Tensor] = []
+        for group in self.param_groups:
+            for p in group["params"]:
+                if p.grad is None:
+                    continue
+                row = self._prepare(p, group, keep)
+                per_device.setdefault(p.device, []).append(row)
+        for device, rows in per_device.items():
+            table = np.array(rows, dtype=_lib.TENSOR)
+            with torch.cuda.device(device):
+                _lib.fused_step(table, torch.cuda.current_stream(device).cuda_stream)
+        return loss
+
+    def _plan_accepts(self, p: torch.Tensor, grad: torch.Tensor, group, requested, schemes, state) -> bool:
+        """Whether the optimized backend's preflight takes this parameter (``_optimized.py:85-126``)."""
+        if not self._optimized or state.get(_FALLBACK_KEY, False):
+            return False
+        if requested[0] not in _OPT_M1_SCHEMES or requested[1] not in _OPT_M2_SCHEMES:
+            return False
+        if not grad.is_contiguous() or ("step" in state and not isinstance(state["step"], int)):
+            return False
+        occupied = [_byte_range(p), _byte_range(grad)]
+        if _overlaps(occupied[0], occupied[1]):
+            return False
+        for tensor in _moment_tensors(state):
+            region = _byte_range(tensor)
+            if any(_overlaps(region, prev) for prev in occupied):
+                return False
+            occupied.append(region)
+        limit = group.get(_CHUNK_KEY, _CHUNK_NUMEL)
+        if isinstance(limit, bool) or not isinstance(limit, int) or limit <= 0:
+            return False
+        return limit >= (_lib.BLOCK if any(s != "fp32" for s in schemes) else 1)
+
+    def _chunk_numel(self, group, schemes) -> int:
+        limit = group.get(_CHUNK_KEY, _CHUNK_NUMEL)
+        align = _lib.BLOCK if any(s != "fp32" for s in schemes) else 1
+        return limit // align * align
+
+    def _prepare(self, p: torch.Tensor, group, keep: List[torch.Tensor]) -> Tuple:
+        if not p.is_cuda:
+            raise NotImplementedError("the fused 4-bit step runs on HIP devices only; move the parameters to the GPU")
+        if p.dtype not in _DTYPES:
+            raise NotImplementedError(f"parameter dtype {p.dtype} (supported: float32, bfloat16, float16)")
+        if p.layout != torch.strided or not p.is_contiguous():
+            raise NotImplementedError("the fused step updates contiguous dense parameters in place")
+        grad = p.grad
+        if grad.layout != torch.strided or grad.dtype not in _DTYPES or grad.device != p.device:
+            raise NotImplementedError("gradients must be dense float32/bfloat16/float16 tensors on the parameter's device")
+        if grad.shape != p.shape:
+            raise ValueError(f"gradient shape {tuple(grad.shape)} does not match parameter shape {tuple(p.shape)}")
+        state = self.state[p]
+        requested = (self._m1_scheme_for(p, group["m1_quant_scheme"]), group["m2_quant_scheme"])
+        sizes = tuple(group["block_size"] if group["block_size"] is not None else default_block_size(m)
+                      for m in requested)
+        schemes = tuple(self._effective_scheme(p, m, s) for m, s in zip(requested, sizes))
+        optimized = self._plan_accepts(p, grad, group, requested, schemes, state)
+        if optimized:
+            group.setdefault(_CHUNK_KEY, _CHUNK_NUMEL)
+        else:
+            # The reference step writes fresh tensors: detach aliased state and gradients.
+            occupied = [_byte_range(p)]
+            if _overlaps(occupied[0], _byte_range(grad)):
+                grad = grad.clone()
+            occupied.append(_byte_range(grad))
+            for key in ("m1", "m2", "m1_code", "m2_code"):
+                value = state.get(key)
+                if isinstance(value, torch.Tensor):
+                    if any(_overlaps(_byte_range(value), r) for r in occupied):
+                        state[key] = value = value.clone()
+                    occupied.append(_byte_range(value))
+            for key in ("m1_quant_state", "m2_quant_state"):
+                meta = state.get(key)
+                if isinstance(meta, QuantState) and isinstance(meta.absmax, torch.Tensor):
+                    if any(_overlaps(_byte_range(meta.absmax), r) for r in occupied):
+                        meta.absmax = meta.absmax.clone()
+                    occupied.append(_byte_range(meta.absmax))
+        if not grad.is_contiguous():
+            grad = grad.contiguous()
+        keep.append(grad)
+        # Streams are opened (and checkpointed streams restored) before any state
+        # changes, so a restore failure leaves the parameter untouched (_optimized.py:157-158).
+        self._quant_generator("m1", p.device)
+        self._quant_generator("m2", p.device)
+
+        n = p.numel()
+        if "step" not in state:
+            chunk = self._chunk_numel(group, schemes) if optimized else n
+            for moment, scheme, size, eden in (("m1", schemes[0], sizes[0], False),
+                                               ("m2", schemes[1], sizes[1], group["use_eden_m2"])):
+                self._init_moment(p, state, moment, scheme, size, eden, chunk)
+            state["step"] = 0
+        else:
+            for moment, scheme in zip(("m1", "m2"), schemes):
+                self._check_moment(p, state, moment, scheme)
+        state["step"] = int(state["step"]) + 1
+        step = state["step"]
+
+        beta1, beta2 = group["betas"]
+        lr, wd, eps = group["lr"], group["weight_decay"], group["eps"]
+        bias1, bias2 = 1 - beta1 ** step, 1 - beta2 ** step
+        storage_bias = 1 - beta2 ** (step + 1) if schemes[1] in NEXT_BIAS_SCHEMES else bias2
+        flags = 0
+        w1, w2 = np.float32(1 - beta1), np.float32(1 - beta2)
+        if not abs(w1) < 0.5:  # ATen lerp switches formulas at |weight| >= 0.5
+            flags |= _lib.TENSOR_LERP1_LARGE
+            w1 = w1 - np.float32(1.0)
+        if not abs(w2) < 0.5:
+            flags |= _lib.TENSOR_LERP2_LARGE
+            w2 = w2 - np.float32(1.0)
+        psize = 4 * (4 if p.dtype == torch.float32 else 2)
+        gsize = 4 * (4 if grad.dtype == torch.float32 else 2)
+        if p.data_ptr() % psize == 0 and grad.data_ptr() % gsize == 0:
+            flags |= _lib.TENSOR_VEC_ALIGNED
+        bc2_sqrt = _f32(math.sqrt(bias2))
+        m1 = self._moment_row(p, state, "m1", schemes[0], False, optimized, 1.0, 1e-8, keep)
+        m2 = self._moment_row(p, state, "m2", schemes[1], group["use_eden_m2"], optimized,
+                              storage_bias, eps, keep)
+        return (p.data_ptr(), grad.data_ptr(), n, _DTYPES[p.dtype], _DTYPES[grad.dtype], flags,
+                float(w1), float(w2), _f32(1 - lr * wd), _f32(-lr / bias1), bc2_sqrt, _rcp32(bc2_sqrt),
+                _f32(eps), m1, m2)
+
+    def _init_moment(self, p, state, moment, scheme, size, eden, chunk) -> None:
+        """Zero state (``_moment_buffer.py:89-126`` / ``adamw.py:524-545``)."""
+        n = p.numel()
+        if scheme == "fp32":
+            state[moment] = torch.zeros(p.shape, device=p.device, dtype=torch.float32)
+            state.pop(f"{moment}_code", None)
+            state.pop(f"{moment}_quant_state", None)
+            return
+        code, scale = initial_code_and_scale(scheme, eden)
+        state[f"{moment}_code"] = torch.full(((n + 1) // 2,), code | (code << 4), dtype=torch.uint8, device=p.device)
+        absmax = torch.full((n // size,), scale, dtype=torch.float32, device=p.device)
+        state[f"{moment}_quant_state"] = QuantState(absmax=absmax, shape=p.shape, dtype=torch.float32,
+                                                    blocksize=size, packed=True)
+        state.pop(moment, None)
+        if SCHEMES[scheme][1] in (ROUND_STATE_SR, ROUND_UPDATE_SR):
+            # Encoding the zero tile consumes draws without affecting the codes.
+            tile = n if n <= chunk else math.lcm(size, 2)
+            self._stream(moment, p.device).advance(tile)
+
+    def _check_moment(self, p, state, moment, scheme) -> None:
+        """Accept existing state in the layout the kernel writes (``_moment_buffer.py:54-87,127-141``)."""
+        n = p.numel()
+        if scheme == "fp32":
+            value = state.get(moment)
+            if value is None and f"{moment}_code" in state:
+                raise NotImplementedError(f"{moment}: quantized state found where the scheme is fp32")
+            if not (isinstance(value, torch.Tensor) and value.device == p.device and value.dtype == torch.float32
+                    and value.numel() == n):
+                raise ValueError(f"{moment}: fp32 state does not match the parameter")
+            if not value.is_contiguous():
+                state[moment] = value.contiguous()
+            return
+        codes = state.get(f"{moment}_code")
+        meta = state.get(f"{moment}_quant_state")
+        if not isinstance(codes, torch.Tensor) or not isinstance(meta, QuantState):
+            raise NotImplementedError(f"{moment}: fp32 state found where the scheme is quantized")
+        if meta.blocksize != _lib.BLOCK or meta.absmax.numel() != n // _lib.BLOCK:
+            raise NotImplementedError(f"{moment}: block size {meta.blocksize} state")
+        if codes.dtype != torch.uint8 or codes.device != p.device:
+            raise ValueError(f"{moment}: codes must be uint8 on {p.device}")
+        if meta.absmax.device != p.device or meta.absmax.dtype != torch.float32 or not meta.absmax.is_contiguous():
+            meta.absmax = meta.absmax.to(device=p.device, dtype=torch.float32).contiguous()
+        if codes.numel() == n and not getattr(meta, "packed", False):
+            codes = pack_4bit_codes(codes.reshape(-1))  # legacy unpacked codes
+        elif codes.numel() != (n + 1) // 2:
+            raise ValueError(f"{moment}: {codes.numel()} code bytes for {n} values")
+        if not codes.is_contiguous():
+            codes = codes.contiguous()
+        state[f"{moment}_code"] = codes
+        meta.packed = True
+
+    def _moment_row(self, p, state, moment, scheme, eden, optimized, bias, eps, keep) -> Tuple:
+        n = p.numel()
+        if scheme == "fp32":
+            return (0, 0, state[moment].data_ptr(), 0, 0, 0, 0, _lib.ROUND_FP32, 0, 1.0, 1.0, _f32(1e-8))
+        codebook, rounding, floor_zero = SCHEMES[scheme]
+        flags = (_lib.MOMENT_ZERO_FLOOR if floor_zero else 0) | (_lib.MOMENT_EDEN if eden else 0)
+        if optimized:
+            flags |= _lib.MOMENT_GUARDS
+        seed = offset = draws = 0
+        if rounding in (ROUND_STATE_SR, ROUND_UPDATE_SR):
+            stream = self._stream(moment, p.device)
+            seed, offset = stream.seed, stream.take(n)
+            if self._draw_provider is not None:
+                u = self._draw_provider(p, moment, n, p.device)
+                if u.dtype != torch.float32 or u.numel() != n or u.device != p.device:
+                    raise ValueError("draw provider must return n float32 uniforms on the parameter's device")
+                u = u.contiguous()
+                keep.append(u)
+                draws = u.data_ptr()
+                flags |= _lib.MOMENT_EXT_DRAWS
+        sr_bias = _f32(max(float(bias), 1e-12))
+        return (state[f"{moment}_code"].data_ptr(), state[f"{moment}_quant_state"].absmax.data_ptr(), 0, draws,
+                seed, offset, codebook, rounding, flags, sr_bias, _rcp32(sr_bias), _f32(eps))
+
+
+class AdamW8bit(QuantizedAdamW):
+    """Compatibility name of the reference's 8-bit defaults (``adamw.py:865-866``); 8-bit state is
+    outside the fused 4-bit step, so construction raises ``NotImplementedError``."""
+
+
+class ZIPSRAdamW4Bit(QuantizedAdamW):
+    """NF4 first moments and zero-inclusive Dyn4 preconditioner-space SR (``adamw.py:869-879``)."""
+
+    def __init__(self, params, **kwargs):
+        super().__init__(params, m1_quant_scheme="nf4", m2_quant_scheme="dyn4_upd_sr_fp32read",
+                         use_eden_m2=False, **kwargs)
+
+
+class ZEEDENAdamW4Bit(QuantizedAdamW):
+    """NF4 first moments and zero-exclusive Dyn4 second moments with EDEN (``adamw.py:882-892``)."""
+
+    def __init__(self, params, **kwargs):
+        super().__init__(params, m1_quant_scheme="nf4", m2_quant_scheme="dyn4_nz", use_eden_m2=True, **kwargs)

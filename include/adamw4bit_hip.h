@@ -1,0 +1,178 @@
+/*
+ * adamw4bit_hip.h -- C ABI of the MI355X (gfx950) fused 4-bit AdamW step.
+ *
+ * The library (libadamw4bit_hip.so) exports plain-C entry points that take
+ * device addresses, sizes and a HIP stream.  No torch types cross this
+ * boundary: the Python host code passes tensor data pointers and the
+ * current stream handle through ctypes, exactly as a cgo/JNI/N-API binding
+ * would.
+ *
+ * Reference interfaces replaced (nubank/adamw4bit, paths under src/adamw4bit/):
+ *   aw4_fused_step   -> OptimizedBackend._step_parameter + _step_chunk
+ *                       (_optimized.py:145-234) for EVERY parameter of one
+ *                       optimizer.step() in a single launch; also the
+ *                       element arithmetic of the reference step
+ *                       QuantizedAdamW.step (adamw.py:547-803) for the
+ *                       scheme set it shares with the optimized path.
+ *   aw4_quantize     -> _optimized_quantization.quantize (:46-88) followed by
+ *                       pack_4bit_codes (quantization.py:627-638) and the
+ *                       in-place copy of MomentBuffer.write (_moment_buffer.py:164-179).
+ *   aw4_dequantize   -> _optimized_quantization.dequantize (:91-107) on packed
+ *                       codes (MomentBuffer.read, _moment_buffer.py:157-162).
+ *
+ * All entry points return 0 on success and a negative AW4_E* code on error;
+ * aw4_last_error() then describes the failure (thread-local string).
+ */
+#ifndef ADAMW4BIT_HIP_H
+#define ADAMW4BIT_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AW4_ABI_VERSION 1
+#define AW4_BLOCK 128 /* values per block scale (quantization.py:694-703, 4-bit default) */
+
+/* Error codes. */
+#define AW4_OK 0
+#define AW4_EINVAL -1  /* malformed descriptor (null pointer, bad enum, bad size) */
+#define AW4_EHIP -2    /* a HIP runtime call failed */
+#define AW4_EALIGN -3  /* a buffer violates the alignment its descriptor promises */
+
+/* 16-level codebooks (quantization.py:201-237, 401-422, 457-497). */
+#define AW4_CB_NF4 0     /* nf4, nf4_sr */
+#define AW4_CB_SDYN4 1   /* sdyn4, sdyn4_sr */
+#define AW4_CB_DYN4 2    /* dyn4, dyn4_sr, dyn4_nz, dyn4_upd_sr_fp32read, dyn4_lookahead_sr, ..._nextbc */
+#define AW4_CB_LIN4 3    /* lin4, lin4_sr, lin4_upd_sr_fp32read */
+#define AW4_CB_LIN4_NZ 4 /* lin4_nz */
+#define AW4_NUM_CODEBOOKS 5
+
+/* How a moment is stored and re-encoded. */
+#define AW4_ROUND_FP32 0      /* fp32 state tensor, no codec (adamw.py:807-817 ineligible or "fp32") */
+#define AW4_ROUND_RTN 1       /* nearest level, ties up (_compiled_quantization.py:41-45) */
+#define AW4_ROUND_STATE_SR 2  /* value-unbiased SR (_compiled_quantization.py:60-71) */
+#define AW4_ROUND_UPDATE_SR 3 /* preconditioner-space SR (_compiled_quantization.py:74-109) */
+
+/* aw4_moment.flags */
+#define AW4_MOMENT_ZERO_FLOOR 0x1 /* code 0 -> code 1 after rounding (dyn4_nz, quantization.py:529-552) */
+#define AW4_MOMENT_EDEN 0x2       /* EDEN block-scale calibration (_optimized_quantization.py:81-85) */
+#define AW4_MOMENT_GUARDS 0x4     /* exact-level SR guards of the optimized path (_compiled_quantization.py:48-57);
+                                     clear for the reference step (quantization.py:279-377) */
+#define AW4_MOMENT_EXT_DRAWS 0x8  /* read uniforms from aw4_moment.draws instead of on-device Philox */
+
+/* aw4_tensor.param_dtype / grad_dtype */
+#define AW4_F32 0
+#define AW4_BF16 1
+#define AW4_F16 2
+
+/* aw4_tensor.flags */
+#define AW4_TENSOR_LERP1_LARGE 0x1 /* lerp weight 1-beta1 >= 0.5: m1 = fma(w-1, g-m1, g) */
+#define AW4_TENSOR_LERP2_LARGE 0x2 /* same for m2 with g*g */
+#define AW4_TENSOR_VEC_ALIGNED 0x4 /* param and grad allow 4-element vector access */
+
+/*
+ * One moment (m1 or m2) of one parameter.  For a quantized moment, `codes`
+ * holds ceil(numel/2) bytes (element 2j in the low nibble of byte j) and
+ * `scales` numel/128 fp32 block scales; `values` is 0.  For an fp32-state
+ * moment only `values` (numel fp32) is set.  Layout as in optimizer.state
+ * (_moment_buffer.py:89-142, adamw.py:326-362).
+ */
+typedef struct aw4_moment {
+    uint64_t codes;      /* device address, uint8[ceil(numel/2)] or 0 */
+    uint64_t scales;     /* device address, float[numel/128] or 0 */
+    uint64_t values;     /* device address, float[numel] or 0 */
+    uint64_t draws;      /* device address, float[numel] uniforms (AW4_MOMENT_EXT_DRAWS) or 0 */
+    uint64_t rng_seed;   /* Philox4x32-10 key: generator seed of this moment's stream */
+    uint64_t rng_offset; /* stream position of this write's first draw; multiple of 4 */
+    int32_t codebook;    /* AW4_CB_* (ignored for AW4_ROUND_FP32) */
+    int32_t rounding;    /* AW4_ROUND_* */
+    int32_t flags;       /* AW4_MOMENT_* */
+    float sr_bias;       /* update-SR storage bias correction, fp32(max(c,1e-12)) (_optimized_quantization.py:66-67) */
+    float sr_bias_rcp;   /* correctly rounded 1/sr_bias */
+    float sr_eps;        /* update-SR epsilon, fp32(eps) */
+} aw4_moment; /* 72 bytes */
+
+/*
+ * One parameter of a step.  All scalars are the fp32 values the reference's
+ * ATen kernels see (_optimized.py:168-173, :215-222):
+ *   w1 = fp32(1-beta1) (or fp32(1-beta1) - 1 with LERP1_LARGE), w2 likewise,
+ *   decay = fp32(1 - lr*wd), step_coef = fp32(-lr/bc1),
+ *   bc2_sqrt = fp32(sqrt(bc2)), bc2_sqrt_rcp = RN(1/bc2_sqrt), eps = fp32(eps).
+ */
+typedef struct aw4_tensor {
+    uint64_t param;      /* device address, contiguous, param_dtype[numel]; updated in place */
+    uint64_t grad;       /* device address, contiguous, grad_dtype[numel] */
+    int64_t numel;
+    int32_t param_dtype; /* AW4_F32 / AW4_BF16 / AW4_F16 */
+    int32_t grad_dtype;
+    int32_t flags;       /* AW4_TENSOR_* */
+    float w1, w2, decay, step_coef, bc2_sqrt, bc2_sqrt_rcp, eps;
+    aw4_moment m1;
+    aw4_moment m2;
+} aw4_tensor; /* 208 bytes */
+
+/* Library ABI version (AW4_ABI_VERSION of the build). */
+int aw4_abi_version(void);
+
+/* Description of the last error on this thread ("" if none). */
+const char* aw4_last_error(void);
+
+/*
+ * One fused AdamW step over `count` parameters in ONE kernel launch on
+ * `stream` (a hipStream_t; 0 = legacy default stream).  `tensors` is a host
+ * array; it is staged to device memory by the library (the call returns
+ * before the step completes, stream-ordered like any HIP launch).
+ * Replaces the per-parameter chunk loop of _optimized.py:145-203 and the
+ * chunk update _optimized.py:206-234.
+ */
+int aw4_fused_step(const aw4_tensor* tensors, int32_t count, void* stream);
+
+/*
+ * Encode `numel` fp32 values (numel a multiple of 128) into the quantized
+ * moment `m` (codes + scales written in place), with m's rounding, codebook,
+ * flags and draws.  Replaces _optimized_quantization.quantize (:46-88) +
+ * pack_4bit_codes.  `values` is a device address.
+ */
+int aw4_quantize(const float* values, int64_t numel, const aw4_moment* m, void* stream);
+
+/*
+ * Decode a quantized moment into fp32 `out` (device address, numel values,
+ * numel a multiple of 128).  Replaces _optimized_quantization.dequantize (:91-107).
+ */
+int aw4_dequantize(const aw4_moment* m, int64_t numel, float* out, void* stream);
+
+/*
+ * Fill `out` (device address, n floats) with the uniforms in [0,1) that a
+ * stochastic write draws at stream positions offset .. offset+n-1 of the
+ * Philox4x32-10 stream keyed by `seed` (offset a multiple of 4).  Draw k of a
+ * write of moment m is the uniform at position m.rng_offset + k, k being the
+ * element index; it replaces _optimized_quantization._uniform_draws (:37-43),
+ * whose CPU mt19937 / CUDA Philox streams a device kernel cannot reproduce.
+ */
+int aw4_uniforms(uint64_t seed, uint64_t offset, int64_t n, float* out, void* stream);
+
+/*
+ * Host-only: copy the encode lookup tables the kernels use into `out`
+ * (host memory, `bytes` long); returns the table size in bytes (call with
+ * out = 0 to query) or a negative error.  Layout: for each of AW4_NUM_LUTS
+ * tables, AW4_LUT_ENTRIES pairs {float threshold; uint32 base}: a value x
+ * in bucket k (aw4 bucket function below) encodes to base + (x >= threshold).
+ * Tables 0..5: round-to-nearest codes for nf4, sdyn4, dyn4, lin4, lin4_nz,
+ * dyn4 with the zero floor; tables 6..10: searchsorted-left counts
+ * (number of levels < x) for nf4, sdyn4, dyn4, lin4, lin4_nz.
+ * Bucket of x: a = bits(x) & 0x7fffffff; k = clamp((a >> 20) - AW4_LUT_EXP0 + 1,
+ * 0, AW4_LUT_HALF - 1); bucket = k + (bits(x) >> 31) * AW4_LUT_HALF.
+ */
+#define AW4_NUM_LUTS 11
+#define AW4_LUT_HALF 89
+#define AW4_LUT_ENTRIES (2 * AW4_LUT_HALF)
+#define AW4_LUT_EXP0 936 /* (127 - 10) << 3: |x| < 2^-10 shares bucket 0 */
+int64_t aw4_encode_tables(void* out, int64_t bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ADAMW4BIT_HIP_H */

@@ -230,7 +230,8 @@ class Oracle:
 
     def __init__(self, params: List[torch.Tensor], hyper: Hyper, m1_schemes: List[str],
                  m2_schemes: List[str], eden: List[bool], *, seed: Optional[int] = None,
-                 optimized: bool = True, chunk: int = CHUNK_NUMEL, record_draws: bool = False):
+                 optimized: bool = True, chunk: int = CHUNK_NUMEL, record_draws: bool = False,
+                 draw_fn=None):
         self.params = params
         self.hyper = hyper
         self.m1_schemes = list(m1_schemes)
@@ -248,12 +249,18 @@ class Oracle:
                 gen.manual_seed((seed + offset) % ((1 << 63) - 1))
                 self.generators[moment] = gen
         self.record_draws = record_draws
+        # Optional source of uniforms: draw_fn(moment, n) -> n float32 values, used in place of
+        # the CPU generators (to replay the draws a device implementation consumed).
+        self.draw_fn = draw_fn
         self.draw_log: List[DrawLog] = []
         self.draw_counts = {"m1": 0, "m2": 0}
 
     # -- random draws -------------------------------------------------------
     def _draw(self, moment: str, n: int, param: int, step: int, log: bool) -> torch.Tensor:
-        u = torch.rand((n // BLOCK, BLOCK), dtype=torch.float32, generator=self.generators[moment])
+        if self.draw_fn is not None:
+            u = self.draw_fn(moment, n).reshape(n // BLOCK, BLOCK).to(torch.float32)
+        else:
+            u = torch.rand((n // BLOCK, BLOCK), dtype=torch.float32, generator=self.generators[moment])
         self.draw_counts[moment] += n
         if self.record_draws and log:
             self.draw_log.append(DrawLog(param, moment, step, u.reshape(-1).clone()))

@@ -1,0 +1,139 @@
+"""Shared helpers for the GPU tests: build the drop-in optimizer from a fixture
+configuration, replay draws, compare states with the oracle."""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+import adamw4bit_amd as aw
+from adamw4bit_amd import _lib
+from oracle import philox
+from oracle import reference_step as ref
+
+DEVICE = "cuda"
+# Parameters: the reference's CPU square root (MKL vector math) is up to 1 ulp below the
+# correctly rounded one the kernel uses, so values downstream of sqrt agree within a few ulps.
+PARAM_RTOL = 1e-6
+
+
+def heavy_tailed(shape, gen, row_mu=-7.0, row_sigma=1.0):
+    """Student-t(3) values times per-row log-normal magnitudes (fixed generator)."""
+    z = torch.randn(shape, generator=gen)
+    chi2 = (torch.randn((3,) + tuple(shape), generator=gen) ** 2).sum(0)
+    t = z / torch.sqrt(chi2 / 3.0)
+    rows = shape[0] if len(shape) > 1 else 1
+    scale = torch.exp(row_mu + row_sigma * torch.randn(rows, generator=gen))
+    return t * (scale.view(-1, *([1] * (len(shape) - 1))) if len(shape) > 1 else scale)
+
+
+def build_optimizer(cfg, params):
+    """The drop-in optimizer configured like a golden-fixture run."""
+    hp = cfg["hyper"]
+    kw = dict(lr=hp["lr"], betas=tuple(hp["betas"]), eps=hp["eps"], weight_decay=hp["weight_decay"],
+              optimized=cfg["optimized"], quant_rng_seed=cfg["seed"])
+    name = cfg["optimizer"]
+    if name == "ZEEDENAdamW4Bit":
+        opt = aw.ZEEDENAdamW4Bit(params, **kw)
+    elif name == "ZIPSRAdamW4Bit":
+        opt = aw.ZIPSRAdamW4Bit(params, **kw)
+    else:
+        groups = [dict(params=[p], m1_quant_scheme=e["m1"], m2_quant_scheme=e["m2"], use_eden_m2=e["eden"])
+                  for p, e in zip(params, cfg["per_param"])]
+        opt = aw.QuantizedAdamW(groups, m1_quant_scheme="nf4", m2_quant_scheme="dyn4_nz", **kw)
+    if cfg["optimized"]:
+        for g in opt.param_groups:
+            g["max_chunk_numel"] = cfg["chunk"]
+    if cfg.get("m1_override"):
+        idx, scheme = cfg["m1_override"]
+        opt.set_m1_quant_scheme_for_parameters([params[j] for j in idx], scheme)
+    return opt
+
+
+class LoggedDraws:
+    """Draw provider replaying the uniforms an oracle run recorded, write by write."""
+
+    def __init__(self, oracle: ref.Oracle, params):
+        self.queues = {}
+        for entry in oracle.draw_log:
+            self.queues.setdefault((entry.param, entry.moment), []).append(entry.draws)
+        self.index = {id(p): i for i, p in enumerate(params)}
+
+    def __call__(self, p, moment, n, device):
+        draws = self.queues[(self.index[id(p)], moment)].pop(0)
+        assert draws.numel() == n
+        return draws.to(device)
+
+
+class PhiloxMirror:
+    """Oracle draw_fn replaying the device's Philox streams (same seeds, same positions)."""
+
+    def __init__(self, optimizer: aw.QuantizedAdamW, device):
+        self.opt = optimizer
+        self.device = torch.device(device)
+        self.offsets = {"m1": 0, "m2": 0}
+
+    def __call__(self, moment, n):
+        seed = self.opt._stream(moment, self.device).seed
+        off = self.offsets[moment]
+        self.offsets[moment] = off + (n + 3) // 4 * 4
+        return torch.from_numpy(philox.uniforms(seed, off, n))
+
+
+def state_of(opt, p):
+    st = opt.state[p]
+    out = {"step": st["step"]}
+    for m in ("m1", "m2"):
+        if f"{m}_code" in st:
+            out[f"{m}_code"] = st[f"{m}_code"].cpu()
+            out[f"{m}_scale"] = st[f"{m}_quant_state"].absmax.cpu()
+        else:
+            out[f"{m}_fp32"] = st[m].cpu()
+    return out
+
+
+def oracle_state(ms_pair):
+    st = {}
+    for name, ms in zip(("m1", "m2"), ms_pair):
+        if ms.scheme == "fp32":
+            st[f"{name}_fp32"] = ms.values.clone()
+        else:
+            st[f"{name}_code"] = ms.codes.clone()
+            st[f"{name}_scale"] = ms.scales.clone()
+    return st
+
+
+def bits(t: torch.Tensor) -> torch.Tensor:
+    t = t.detach().cpu().contiguous()
+    return t.view({4: torch.int32, 2: torch.int16, 1: torch.uint8}[t.element_size()])
+
+
+def assert_params_close(got: torch.Tensor, expect: torch.Tensor, what: str, rtol: float = PARAM_RTOL):
+    """Parameters within the stated relative tolerance (elementwise, relative to |expect|)."""
+    g = got.detach().cpu().double()
+    e = expect.detach().cpu().double()
+    if got.dtype in (torch.bfloat16, torch.float16):
+        # one storage ulp of a 16-bit parameter is far above 1e-6: compare in storage ulps
+        diff = (bits(got).int() - bits(expect).int()).abs()
+        assert int(diff.max()) <= 1, f"{what}: {int((diff > 0).sum())} values differ by more than one ulp"
+        return
+    err = (g - e).abs()
+    tol = rtol * e.abs() + 1e-30
+    bad = err > tol
+    assert not bool(bad.any()), f"{what}: {int(bad.sum())} of {e.numel()} values exceed rtol {rtol}; " \
+                                f"max rel err {float((err / e.abs().clamp_min(1e-30)).max()):.3g}"
+
+
+def code_mismatch(a: torch.Tensor, b: torch.Tensor) -> int:
+    """Number of differing 4-bit codes between two packed code tensors."""
+    a = a.cpu()
+    b = b.cpu()
+    lo = ((a & 0x0F) != (b & 0x0F)).sum()
+    hi = ((a >> 4) != (b >> 4)).sum()
+    return int(lo + hi)
+
+
+def uniforms_gpu(seed: int, offset: int, n: int) -> torch.Tensor:
+    out = torch.empty(n, dtype=torch.float32, device=DEVICE)
+    _lib.uniforms(seed, offset, n, out.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    return out

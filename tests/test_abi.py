@@ -1,0 +1,210 @@
+"""The C-ABI boundary without a GPU: library loads, exports every declared symbol,
+struct layouts agree with the header, and the host-built encode tables reproduce
+the reference's rounding rules."""
+
+import ctypes
+import os
+import re
+import subprocess
+import tempfile
+
+import numpy as np
+import pytest
+import torch
+
+from adamw4bit_amd import _lib
+from adamw4bit_amd import quantization as q
+from oracle import reference_step as ref
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "adamw4bit_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(aw4_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.library()
+    names = declared_functions()
+    assert names == sorted(_lib.SIGNATURES), "ctypes signatures and header disagree"
+    for name in names:
+        assert hasattr(lib, name), name
+    assert lib.aw4_abi_version() == _lib.ABI_VERSION
+
+
+def test_error_path_reports_message():
+    # Invalid arguments are rejected on the host before any device work.
+    lib = _lib.library()
+    rc = lib.aw4_uniforms(1, 2, 16, None, None)  # offset not a multiple of 4, null output
+    assert rc == _lib.EINVAL
+    assert b"aw4_uniforms" in lib.aw4_last_error()
+    table = np.zeros(1, dtype=_lib.TENSOR)  # null pointers
+    with pytest.raises(_lib.HipLibraryError, match="null param"):
+        _lib.fused_step(table, 0)
+
+
+def test_struct_layout_matches_header():
+    src = r"""
+#include <stddef.h>
+#include <stdio.h>
+#include "adamw4bit_hip.h"
+#define P(T, f) printf(#T "." #f " %zu\n", offsetof(T, f));
+int main(void) {
+  printf("aw4_moment %zu\naw4_tensor %zu\n", sizeof(aw4_moment), sizeof(aw4_tensor));
+  P(aw4_moment, codes) P(aw4_moment, scales) P(aw4_moment, values) P(aw4_moment, draws)
+  P(aw4_moment, rng_seed) P(aw4_moment, rng_offset) P(aw4_moment, codebook) P(aw4_moment, rounding)
+  P(aw4_moment, flags) P(aw4_moment, sr_bias) P(aw4_moment, sr_bias_rcp) P(aw4_moment, sr_eps)
+  P(aw4_tensor, param) P(aw4_tensor, grad) P(aw4_tensor, numel) P(aw4_tensor, param_dtype)
+  P(aw4_tensor, grad_dtype) P(aw4_tensor, flags) P(aw4_tensor, w1) P(aw4_tensor, w2) P(aw4_tensor, decay)
+  P(aw4_tensor, step_coef) P(aw4_tensor, bc2_sqrt) P(aw4_tensor, bc2_sqrt_rcp) P(aw4_tensor, eps)
+  P(aw4_tensor, m1) P(aw4_tensor, m2)
+  return 0;
+}
+"""
+    with tempfile.TemporaryDirectory() as d:
+        c = os.path.join(d, "layout.c")
+        exe = os.path.join(d, "layout")
+        open(c, "w").write(src)
+        subprocess.run(["gcc", "-I", os.path.dirname(HEADER), c, "-o", exe], check=True)
+        out = subprocess.run([exe], check=True, capture_output=True, text=True).stdout.split("\n")
+    got = dict(line.split() for line in out if line)
+    assert int(got["aw4_moment"]) == _lib.MOMENT.itemsize
+    assert int(got["aw4_tensor"]) == _lib.TENSOR.itemsize
+    for name, dtype in (("aw4_moment", _lib.MOMENT), ("aw4_tensor", _lib.TENSOR)):
+        for field, (_, offset) in dtype.fields.items():
+            assert int(got[f"{name}.{field}"]) == offset, (name, field)
+
+
+def test_header_constants_match_python():
+    text = open(HEADER).read()
+    consts = dict(re.findall(r"#define (AW4_[A-Z0-9_]+) (-?(?:0x)?[0-9A-Fa-f]+)\b", text))
+    val = {k: int(v, 0) for k, v in consts.items()}
+    assert val["AW4_CB_NF4"] == q.CB_NF4 == _lib.CB_NF4
+    assert val["AW4_CB_SDYN4"] == q.CB_SDYN4 and val["AW4_CB_DYN4"] == q.CB_DYN4
+    assert val["AW4_CB_LIN4"] == q.CB_LIN4 and val["AW4_CB_LIN4_NZ"] == q.CB_LIN4_NZ
+    assert val["AW4_ROUND_RTN"] == q.ROUND_RTN == _lib.ROUND_RTN
+    assert val["AW4_ROUND_STATE_SR"] == q.ROUND_STATE_SR and val["AW4_ROUND_UPDATE_SR"] == q.ROUND_UPDATE_SR
+    assert val["AW4_NUM_LUTS"] == _lib.NUM_LUTS and val["AW4_LUT_HALF"] == _lib.LUT_HALF
+    assert val["AW4_LUT_EXP0"] == _lib.LUT_EXP0 and val["AW4_BLOCK"] == _lib.BLOCK
+    for name in ("MOMENT_ZERO_FLOOR", "MOMENT_EDEN", "MOMENT_GUARDS", "MOMENT_EXT_DRAWS",
+                 "TENSOR_LERP1_LARGE", "TENSOR_LERP2_LARGE", "TENSOR_VEC_ALIGNED", "F32", "BF16", "F16"):
+        assert val[f"AW4_{name}"] == getattr(_lib, name), name
+
+
+# ---------------------------------------------------------------------------
+# Encode tables: bucket lookup == reference rounding rule
+# ---------------------------------------------------------------------------
+
+LUT_CODEBOOKS = [("nf4", q.CB_NF4), ("sdyn4", q.CB_SDYN4), ("dyn4", q.CB_DYN4), ("lin4", q.CB_LIN4),
+                 ("lin4_nz", q.CB_LIN4_NZ)]
+
+
+def lut_eval(tables, lut_id, x):
+    """The kernel's lut_index() restated in numpy."""
+    u = x.view(np.uint32).astype(np.int64)
+    k = ((u & 0x7FFFFFFF) >> 20) - (_lib.LUT_EXP0 - 1)
+    k = np.clip(k, 0, _lib.LUT_HALF - 1)
+    idx = k + (u >> 31) * _lib.LUT_HALF
+    thr = tables[lut_id, idx, 0].view(np.float32)
+    return tables[lut_id, idx, 1].astype(np.int64) + (x >= thr)
+
+
+def reference_rules(cb: np.ndarray, x: np.ndarray):
+    """searchsorted-left count and the round-to-nearest code, via the oracle's torch ops."""
+    xt = torch.from_numpy(x)
+    cbt = torch.from_numpy(cb)
+    idx = torch.searchsorted(cbt, xt, out_int32=True)
+    lower, upper, a, b = ref._endpoints(xt, cbt)
+    rtn = torch.where((xt - a).abs() < (b - xt).abs(), lower, upper)
+    return idx.numpy().astype(np.int64), rtn.numpy().astype(np.int64)
+
+
+def probe_values(cb: np.ndarray, tables: np.ndarray) -> np.ndarray:
+    rng = np.random.default_rng(0)
+    pts = [rng.uniform(-1, 1, 200000).astype(np.float32), (rng.uniform(0, 1, 100000) ** 6).astype(np.float32),
+           np.array([0.0, -0.0, 1.0, -1.0, 1e-30, -1e-30, 2.0 ** -10, -(2.0 ** -10), 1e-45], dtype=np.float32)]
+    # every threshold of every table and every level, +-40 ulps
+    marks = [cb, tables[:, :, 0].view(np.float32).reshape(-1)]
+    for m in marks:
+        m = m[np.isfinite(m)].astype(np.float32)
+        bits = m.view(np.int32)
+        for d in range(-40, 41):
+            b = bits + d
+            pts.append(b.view(np.float32))
+            pts.append((-(m)).astype(np.float32).view(np.int32) + d)
+    # bucket edges +-3 ulps
+    edges = (np.arange(_lib.LUT_EXP0, _lib.LUT_EXP0 + _lib.LUT_HALF, dtype=np.int64) << 20)
+    for d in range(-3, 4):
+        e = (edges + d).astype(np.uint32).view(np.float32)
+        pts += [e, -e]
+    x = np.concatenate([np.asarray(p).view(np.float32) if np.asarray(p).dtype != np.float32 else p for p in pts])
+    x = x[np.isfinite(x) & (np.abs(x) <= 1.0)]
+    return np.ascontiguousarray(x, dtype=np.float32)
+
+
+@pytest.mark.parametrize("mode,cb_id", LUT_CODEBOOKS)
+def test_encode_tables_reproduce_rounding_rules(mode, cb_id):
+    tables = _lib.encode_tables()
+    cb = np.array(q.CODEBOOK_VALUES[cb_id], dtype=np.float32)
+    x = probe_values(cb, tables)
+    count, rtn = reference_rules(cb, x)
+    assert np.array_equal(lut_eval(tables, cb_id, x), rtn)                 # round-to-nearest table
+    assert np.array_equal(lut_eval(tables, 6 + cb_id, x), count)           # level-count table
+    if mode == "dyn4":
+        assert np.array_equal(lut_eval(tables, 5, x), np.maximum(rtn, 1))  # dyn4_nz floor table
+
+
+def test_aten_row_sum_order():
+    """The per-block sum order the kernel reproduces (8 lanes x 4 accumulators) is ATen's."""
+    gen = torch.Generator().manual_seed(0)
+    rows = torch.rand(4000, 128, generator=gen) ** 3
+    got = rows.sum(dim=1)
+    r = rows.numpy().reshape(-1, 16, 8)
+    acc = [r[:, k] + np.float32(0) for k in range(4)]
+    for k in range(4):
+        for v in (k + 4, k + 8, k + 12):
+            acc[k] = (acc[k] + r[:, v]).astype(np.float32)
+    a = (((acc[0] + acc[1]).astype(np.float32) + acc[2]).astype(np.float32) + acc[3]).astype(np.float32)
+    s = np.zeros(len(rows), dtype=np.float32)
+    for lane in range(8):
+        s = (s + a[:, lane]).astype(np.float32)
+    assert np.array_equal(s, got.numpy())
+    # a plausible slip (sequential order) would not match
+    seq = np.zeros(len(rows), dtype=np.float32)
+    for j in range(128):
+        seq = (seq + rows.numpy()[:, j]).astype(np.float32)
+    assert not np.array_equal(seq, got.numpy())
+
+
+def test_aten_elementwise_semantics():
+    """ATen CPU facts the kernel's arithmetic relies on: lerp is one fused multiply-add,
+    division by a Python scalar is a true fp32 division, addcdiv is p + (v*t1)/t2."""
+    gen = torch.Generator().manual_seed(1)
+    m = torch.randn(100003, generator=gen) * 1e-3
+    g = torch.randn(100003, generator=gen) * 1e-3
+    for w in (0.1, 0.05, 0.7):
+        got = m.clone().lerp_(g, w).numpy()
+        wf = np.float32(w)
+        mn, gn = m.numpy(), g.numpy()
+        d = (gn - mn).astype(np.float32)
+        if abs(wf) < 0.5:
+            expect = np.float32(mn.astype(np.float64) + np.float64(wf) * d.astype(np.float64))
+        else:
+            expect = np.float32(gn.astype(np.float64) + np.float64(wf - np.float32(1)) * d.astype(np.float64))
+        assert np.array_equal(got, expect.astype(np.float32)), w
+    s = 0.31622776601683794
+    a = m.abs()
+    assert np.array_equal(a.clone().div_(s).numpy(), a.numpy() / np.float32(s))
+    # ATen's CPU sqrt (MKL vector math) is not correctly rounded: results are the correctly
+    # rounded square root or 1 ulp below it.  The HIP kernel uses the correctly rounded
+    # square root, so values downstream of a square root agree within 1 ulp per use.
+    cr = np.sqrt(a.numpy().astype(np.float64)).astype(np.float32)
+    ulps = a.sqrt().numpy().view(np.int32).astype(np.int64) - cr.view(np.int32)
+    assert set(np.unique(ulps).tolist()) <= {-1, 0}
+    assert np.mean(ulps != 0) < 0.02
+    t1, t2 = m.numpy(), np.abs(g.numpy()) + np.float32(1e-3)
+    got = torch.from_numpy(np.ones_like(t1)).addcdiv_(m, torch.from_numpy(t2), value=-1e-3).numpy()
+    assert np.array_equal(got, np.float32(1) + (np.float32(-1e-3) * t1) / t2)

@@ -1,0 +1,434 @@
+"""Parity of the fused HIP step with the CPU oracle and the reference's golden fixtures.
+
+Bars (stated per comparison):
+* codes and block scales of round-to-nearest moments: bit-exact;
+* codes of stochastic moments fed the same uniforms: bit-exact up to draws that fall
+  between two probabilities one sqrt-ulp apart (budget 1e-5 of the codes);
+* fp32-state moments: bit-exact;
+* parameters: within 1e-6 relative (fp32) / one storage ulp (bf16, fp16), because the
+  reference's CPU square root is up to 1 ulp below the correctly rounded one.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import adamw4bit_amd as aw
+from adamw4bit_amd import _lib
+from adamw4bit_amd import quantization as q
+from oracle import philox
+from oracle import reference_step as ref
+from tests import gpu_helpers as H
+from tests._fixtures import load, tensor, trajectory_names
+
+pytestmark = pytest.mark.gpu
+SR_BUDGET = 1e-5
+
+
+def stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def log(msg):
+    print(msg, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# Random draws
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("seed,offset,n", [(0, 0, 4096), (0x1A2B3C4D, 128, 1000), ((1 << 63) - 5, 1 << 34, 8192),
+                                           (1584363401, 4 * 12345, 333)])
+def test_uniforms_match_cpu_philox(seed, offset, n):
+    log(f"uniforms seed={seed} offset={offset} n={n}")
+    got = H.uniforms_gpu(seed, offset, n).cpu().numpy()
+    assert np.array_equal(got, philox.uniforms(seed, offset, n))
+    assert got.min() >= 0.0 and got.max() < 1.0
+
+
+# ---------------------------------------------------------------------------
+# Codec (aw4_quantize / aw4_dequantize) against the reference's chunk codec vectors
+# ---------------------------------------------------------------------------
+
+def moment_desc(mode, eden, guards, codes, scales, draws=None, bias=1.0, eps=1e-8):
+    cb, rounding, floor_zero = q.SCHEMES[mode]
+    m = np.zeros((), dtype=_lib.MOMENT)
+    m["codes"], m["scales"] = codes.data_ptr(), scales.data_ptr()
+    m["codebook"], m["rounding"] = cb, rounding
+    flags = (_lib.MOMENT_ZERO_FLOOR if floor_zero else 0) | (_lib.MOMENT_EDEN if eden else 0)
+    flags |= _lib.MOMENT_GUARDS if guards else 0
+    if draws is not None:
+        m["draws"] = draws.data_ptr()
+        flags |= _lib.MOMENT_EXT_DRAWS
+    m["flags"] = flags
+    b = np.float32(max(bias, 1e-12))
+    m["sr_bias"], m["sr_bias_rcp"], m["sr_eps"] = b, np.float32(1) / b, np.float32(eps)
+    return m
+
+
+def gpu_encode(values, mode, eden, guards, draws=None, bias=1.0, eps=1e-8):
+    n = values.numel()
+    v = values.to(H.DEVICE).contiguous()
+    codes = torch.empty(n // 2, dtype=torch.uint8, device=H.DEVICE)
+    scales = torch.empty(n // 128, dtype=torch.float32, device=H.DEVICE)
+    d = draws.reshape(-1).to(H.DEVICE).contiguous() if draws is not None else None
+    m = moment_desc(mode, eden, guards, codes, scales, d, bias, eps)
+    _lib.quantize(v.data_ptr(), n, m, stream())
+    torch.cuda.synchronize()
+    return codes.cpu(), scales.cpu()
+
+
+def test_codec_vectors():
+    entries, arrays = load("codec_vectors.npz")
+    for e in entries:
+        k = e["key"]
+        log(f"codec vector {k}")
+        values = torch.from_numpy(arrays[f"{k}_values"])
+        draws = torch.from_numpy(arrays[f"{k}_draws"]) if e["stochastic"] else None
+        codes, scales = gpu_encode(values, e["mode"], e["eden"], True, draws, e["bias"], e["eps"])
+        expect_codes = torch.from_numpy(arrays[f"{k}_codes"])
+        got = q.unpack_4bit_codes(codes, numel=values.numel())
+        flips = int((got != expect_codes).sum())
+        if e["stochastic"] and "upd" in e["mode"] or "lookahead" in e["mode"]:
+            assert flips <= max(0, int(SR_BUDGET * values.numel())), (k, flips)
+        else:
+            assert flips == 0, (k, flips)
+        if flips == 0:
+            assert torch.equal(H.bits(scales), H.bits(torch.from_numpy(arrays[f"{k}_scales"]))), k
+
+
+@pytest.mark.parametrize("mode", ["nf4", "nf4_sr", "sdyn4_sr", "dyn4_sr", "lin4_sr", "dyn4_upd_sr_fp32read",
+                                  "lin4_upd_sr_fp32read"])
+def test_codec_without_guards_matches_reference_step_rules(mode):
+    """The reference step's rounding (no exact-level guards, quantization.py:279-377)."""
+    gen = torch.Generator().manual_seed(11)
+    cb = ref.codebook(mode)
+    signed = bool(cb[0] < 0)
+    x = torch.rand(128 * 64, generator=gen) ** 3 * (1e-3 if not signed else 1.0)
+    if signed:
+        x = x * torch.sign(torch.randn(x.numel(), generator=gen))
+    x.view(-1, 128)[:, :16] = cb * x.view(-1, 128)[:, :1].abs().clamp_min(1e-6)  # exact levels hit the guards
+    draws = torch.rand(x.numel() // 128, 128, generator=gen)
+    stochastic = ref.is_stochastic(mode)
+    codes, scales = gpu_encode(x, mode, False, False, draws if stochastic else None, 0.0975, 1e-8)
+    exp_codes, exp_scales = ref.encode(x, mode, draws=draws if stochastic else None, bias=0.0975, eps=1e-8,
+                                       guards=False)
+    flips = int((q.unpack_4bit_codes(codes, numel=x.numel()) != exp_codes).sum())
+    assert flips <= (int(SR_BUDGET * x.numel()) if "upd" in mode else 0), flips
+    assert torch.equal(H.bits(scales), H.bits(exp_scales))
+
+
+@pytest.mark.parametrize("mode", ["nf4", "sdyn4", "dyn4", "lin4", "lin4_nz"])
+def test_dequantize_matches_oracle(mode):
+    gen = torch.Generator().manual_seed(5)
+    n = 128 * 300
+    codes = torch.randint(0, 256, (n // 2,), dtype=torch.uint8, generator=gen)
+    scales = torch.rand(n // 128, generator=gen) * 1e-2
+    m = moment_desc(mode, False, False, codes.to(H.DEVICE), scales.to(H.DEVICE))
+    c_dev, s_dev = codes.to(H.DEVICE), scales.to(H.DEVICE)
+    m["codes"], m["scales"] = c_dev.data_ptr(), s_dev.data_ptr()
+    out = torch.empty(n, dtype=torch.float32, device=H.DEVICE)
+    _lib.dequantize(m, n, out.data_ptr(), stream())
+    assert torch.equal(H.bits(out), H.bits(ref.decode(codes, scales, mode, n)))
+
+
+# ---------------------------------------------------------------------------
+# Golden trajectories produced by the reference itself
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("name", trajectory_names())
+def test_golden_trajectory(name):
+    cfg, arrays = load(name)
+    log(f"trajectory {name}")
+    from tests.test_oracle_golden import run_oracle
+    oracle, _ = run_oracle(cfg, arrays, record_draws=True)
+    n_params = len(cfg["shapes"])
+    params = [torch.nn.Parameter(tensor(arrays[f"init_p{i}"], cfg["dtype"]).clone()
+                                 .reshape(cfg["shapes"][i]).to(H.DEVICE)) for i in range(n_params)]
+    opt = H.build_optimizer(cfg, params)
+    opt._draw_provider = H.LoggedDraws(oracle, params)
+    for k in range(cfg["steps"]):
+        for i, p in enumerate(params):
+            p.grad = tensor(arrays[f"grad_s{k}_p{i}"], cfg["dtype"]).reshape(cfg["shapes"][i]).to(H.DEVICE)
+        opt.step()
+        if (k + 1) not in cfg["snap_steps"]:
+            continue
+        torch.cuda.synchronize()
+        for i, p in enumerate(params):
+            pre = f"after{k + 1}_p{i}"
+            H.assert_params_close(p, tensor(arrays[pre], cfg["dtype"]).reshape(p.shape), f"{name} step {k+1} p{i}")
+            st = H.state_of(opt, p)
+            assert st["step"] == int(arrays[f"{pre}_step"])
+            for m in ("m1", "m2"):
+                scheme_sr = False
+                if f"{pre}_{m}_code" in arrays:
+                    expect = torch.from_numpy(arrays[f"{pre}_{m}_code"])
+                    flips = H.code_mismatch(st[f"{m}_code"], expect)
+                    budget = int(SR_BUDGET * p.numel()) if cfg["seed"] is not None or scheme_sr else 0
+                    assert flips <= budget, f"{name} {pre} {m}: {flips} code flips"
+                    if flips == 0:
+                        assert torch.equal(H.bits(st[f"{m}_scale"]),
+                                           H.bits(torch.from_numpy(arrays[f"{pre}_{m}_scale"]))), (name, pre, m)
+                else:
+                    assert torch.equal(H.bits(st[f"{m}_fp32"].reshape(-1)),
+                                       H.bits(torch.from_numpy(arrays[f"{pre}_{m}_fp32"]).reshape(-1))), (name, m)
+
+
+# ---------------------------------------------------------------------------
+# Fresh inputs, on-device Philox draws replayed into the oracle
+# ---------------------------------------------------------------------------
+
+def run_pair(make_opt, shapes, dtype, steps, *, seed=0, grad_seed=1, m1_override=None, oracle_kwargs=None,
+             zero_block_frac=0.0):
+    """Step the drop-in optimizer on the GPU and the oracle on the CPU with identical inputs/draws."""
+    gen = torch.Generator().manual_seed(grad_seed)
+    init = [(torch.randn(s, generator=gen) * 0.02).to(dtype) for s in shapes]
+    params = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
+    opt = make_opt(params)
+    if m1_override:
+        opt.set_m1_quant_scheme_for_parameters([params[j] for j in m1_override[0]], m1_override[1])
+    per = []
+    for group in opt.param_groups:
+        for p in group["params"]:
+            per.append((opt._m1_scheme_for(p, group["m1_quant_scheme"]), group["m2_quant_scheme"],
+                        group["use_eden_m2"]))
+    hp = opt.param_groups[0]
+    cpu_params = [t.clone() for t in init]
+    oracle = ref.Oracle(cpu_params, ref.Hyper(hp["lr"], tuple(hp["betas"]), hp["eps"], hp["weight_decay"]),
+                        [e[0] for e in per], [e[1] for e in per], [e[2] for e in per],
+                        seed=seed, optimized=opt._optimized,
+                        chunk=hp.get("max_chunk_numel", ref.CHUNK_NUMEL),
+                        draw_fn=H.PhiloxMirror(opt, H.DEVICE), **(oracle_kwargs or {}))
+    for _ in range(steps):
+        grads = []
+        for s in shapes:
+            g = H.heavy_tailed(s, gen)
+            if zero_block_frac and g.numel() % 128 == 0:
+                nb = g.numel() // 128
+                g.view(nb, 128)[torch.rand(nb, generator=gen) < zero_block_frac] = 0.0
+            grads.append(g.to(dtype))
+        for p, g in zip(params, grads):
+            p.grad = g.to(H.DEVICE)
+        opt.step()
+        oracle.step(grads)
+    torch.cuda.synchronize()
+    return opt, params, oracle, cpu_params
+
+
+def compare_pair(opt, params, oracle, cpu_params, what, sr_moments=()):
+    total_flips = 0
+    total_codes = 0
+    for i, (p, cp) in enumerate(zip(params, cpu_params)):
+        H.assert_params_close(p, cp, f"{what} p{i}")
+        st = H.state_of(opt, p)
+        ost = H.oracle_state((oracle.states[i].m1, oracle.states[i].m2))
+        assert set(st) - {"step"} == set(ost), (what, i, sorted(st), sorted(ost))
+        for m in ("m1", "m2"):
+            if f"{m}_code" in ost:
+                flips = H.code_mismatch(st[f"{m}_code"], ost[f"{m}_code"])
+                total_flips += flips
+                total_codes += p.numel()
+                if m not in sr_moments:
+                    assert flips == 0, f"{what} p{i} {m}: {flips} flips"
+                    assert torch.equal(H.bits(st[f"{m}_scale"]), H.bits(ost[f"{m}_scale"])), (what, i, m)
+            else:
+                assert torch.equal(H.bits(st[f"{m}_fp32"].reshape(-1)), H.bits(ost[f"{m}_fp32"])), (what, i, m)
+    assert total_flips <= SR_BUDGET * max(total_codes, 1) + 0.5, f"{what}: {total_flips} flips of {total_codes}"
+    return total_flips
+
+
+def test_zeeden_1024x1024_matches_oracle():
+    log("zeeden 1024x1024 x 12 steps")
+    args = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True)
+    out = run_pair(lambda ps: aw.ZEEDENAdamW4Bit(ps, **args), [(1024, 1024)], torch.float32, 12, seed=None)
+    compare_pair(*out, "zeeden 1024^2")
+
+
+def test_zipsr_philox_matches_oracle():
+    log("zipsr 512x1024 philox x 6 steps, nf4_sr head")
+    args = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True, quant_rng_seed=0)
+    out = run_pair(lambda ps: aw.ZIPSRAdamW4Bit(ps, **args), [(512, 1024), (256, 128)], torch.float32, 6, seed=0,
+                   m1_override=([1], "nf4_sr"))
+    compare_pair(*out, "zipsr philox", sr_moments=("m1", "m2"))
+
+
+def test_zipsr_4096x4096_matches_oracle():
+    log("zipsr 4096x4096 x 2 steps (full size)")
+    args = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True, quant_rng_seed=0)
+    out = run_pair(lambda ps: aw.ZIPSRAdamW4Bit(ps, **args), [(4096, 4096)], torch.float32, 2, seed=0)
+    compare_pair(*out, "zipsr 4096^2", sr_moments=("m2",))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_mixed_list_16bit(dtype):
+    """Many tensors of ragged sizes, fp32-state ones included, one launch; 16-bit params and grads."""
+    log(f"mixed list {dtype}")
+    shapes = [(768,), (4096,), (4097,), (1,), (3,), (129,), (128,), (50, 256), (3072, 768), (4096, 3), (1000,)]
+    args = dict(lr=2e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True, quant_rng_seed=3)
+    out = run_pair(lambda ps: aw.ZIPSRAdamW4Bit(ps, **args), shapes, dtype, 4, seed=3, m1_override=([8], "nf4_sr"),
+                   zero_block_frac=0.05)
+    compare_pair(*out, f"mixed {dtype}", sr_moments=("m1", "m2"))
+
+
+def test_scheme_groups_reference_step():
+    """optimized=False (the reference step) over every scheme family, one group per scheme pair."""
+    log("scheme groups, reference step")
+    pairs = [("nf4", "dyn4_nz", True), ("sdyn4_sr", "lin4_sr", False), ("fp32", "dyn4", True),
+             ("nf4", "lin4_nz", True), ("nf4", "dyn4_lookahead_sr", True), ("nf4", "fp32", False),
+             ("nf4_sr", "dyn4_upd_sr_fp32read", True), ("sdyn4", "dyn4_sr", False),
+             ("nf4", "lin4_upd_sr_fp32read", False), ("nf4", "lin4", False)]
+
+    def make(ps):
+        groups = [dict(params=[p], m1_quant_scheme=a, m2_quant_scheme=b, use_eden_m2=e) for p, (a, b, e) in zip(ps, pairs)]
+        return aw.QuantizedAdamW(groups, lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1,
+                                 m1_quant_scheme="nf4", m2_quant_scheme="dyn4_nz", quant_rng_seed=9, optimized=False)
+    out = run_pair(make, [(8192,)] * len(pairs), torch.float32, 3, seed=9, zero_block_frac=0.02)
+    compare_pair(*out, "scheme groups", sr_moments=("m1", "m2"))
+
+
+def test_lerp_large_weight_betas():
+    """betas with 1-beta >= 0.5 use ATen's other lerp formula."""
+    log("large lerp weights")
+    args = dict(lr=1e-3, betas=(0.3, 0.45), eps=1e-6, weight_decay=0.0, optimized=True)
+    out = run_pair(lambda ps: aw.ZEEDENAdamW4Bit(ps, **args), [(64, 128), (700,)], torch.float32, 3, seed=None)
+    compare_pair(*out, "large lerp")
+
+
+# ---------------------------------------------------------------------------
+# Checkpoints
+# ---------------------------------------------------------------------------
+
+def test_state_dict_resume_is_exact(tmp_path):
+    log("state_dict resume")
+    gen = torch.Generator().manual_seed(4)
+    shapes = [(256, 128), (768,)]
+    init = [torch.randn(s, generator=gen) * 0.02 for s in shapes]
+    grads = [[H.heavy_tailed(s, gen) for s in shapes] for _ in range(6)]
+
+    def make(ps):
+        opt = aw.ZIPSRAdamW4Bit(ps, quant_rng_seed=21, optimized=True)
+        opt.set_m1_quant_scheme_for_parameters([ps[0]], "nf4_sr")
+        return opt
+
+    a = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
+    oa = make(a)
+    for k in range(6):
+        for p, g in zip(a, grads[k]):
+            p.grad = g.to(H.DEVICE)
+        oa.step()
+
+    b = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
+    ob = make(b)
+    for k in range(3):
+        for p, g in zip(b, grads[k]):
+            p.grad = g.to(H.DEVICE)
+        ob.step()
+    torch.save(ob.state_dict(), tmp_path / "ckpt.pt")
+    sd = torch.load(tmp_path / "ckpt.pt", weights_only=True)
+    assert sd["_quant_rng_state"]["version"] == 1
+    assert set(sd["state"][0]) == {"step", "m1_code", "m1_quant_state", "m2_code", "m2_quant_state"}
+    assert sd["state"][0]["m1_quant_state"]["packed"] is True
+    c = [torch.nn.Parameter(p.detach().clone()) for p in b]
+    oc = make(c)
+    oc.load_state_dict(sd)
+    for k in range(3, 6):
+        for p, g in zip(c, grads[k]):
+            p.grad = g.to(H.DEVICE)
+        oc.step()
+    torch.cuda.synchronize()
+    for pa, pc in zip(a, c):
+        assert torch.equal(H.bits(pa), H.bits(pc))
+    for pa, pc in zip(a, c):
+        sa, sc = H.state_of(oa, pa), H.state_of(oc, pc)
+        for key in sa:
+            if key == "step":
+                assert sa[key] == sc[key]
+            else:
+                assert torch.equal(H.bits(sa[key]), H.bits(sc[key])), key
+
+
+def test_reference_checkpoint_loads_on_gpu():
+    """A state_dict written by the reference (CPU) loads onto GPU parameters; its CPU RNG
+    streams cannot move to another device type, as in the reference (adamw.py:306-320)."""
+    sd = torch.load("tests/golden/zipsr_state_dict.pt", weights_only=True)
+    params = torch.load("tests/golden/zipsr_state_dict_params.pt", weights_only=True)
+    p = torch.nn.Parameter(params["p"].to(H.DEVICE))
+    qv = torch.nn.Parameter(params["q"].to(H.DEVICE))
+    opt = aw.ZIPSRAdamW4Bit([p, qv], quant_rng_seed=11, optimized=True)
+    opt.load_state_dict(sd)
+    st = opt.state[p]
+    assert st["m2_code"].device.type == "cuda" and st["m2_quant_state"].absmax.device.type == "cuda"
+    assert torch.equal(st["m2_code"].cpu(), sd["state"][0]["m2_code"])
+    p.grad = torch.zeros_like(p)
+    qv.grad = torch.zeros_like(qv)
+    with pytest.raises(ValueError, match="Unable to restore quantization RNG state"):
+        opt.step()
+
+
+# ---------------------------------------------------------------------------
+# On-device draws: statistics
+# ---------------------------------------------------------------------------
+
+def test_state_sr_on_device_draws_are_value_unbiased():
+    log("state-SR statistics")
+    gen = torch.Generator().manual_seed(6)
+    block = torch.rand(128, generator=gen) * 2 - 1
+    block[0] = 1.0
+    reps = 8192
+    values = block.repeat(reps)
+    cb = ref.codebook("nf4_sr")
+    n = values.numel()
+    codes = torch.empty(n // 2, dtype=torch.uint8, device=H.DEVICE)
+    scales = torch.empty(n // 128, dtype=torch.float32, device=H.DEVICE)
+    m = moment_desc("nf4_sr", False, True, codes, scales)
+    m["rng_seed"], m["rng_offset"] = 12345, 0
+    v = values.to(H.DEVICE)
+    _lib.quantize(v.data_ptr(), n, m, stream())
+    got = q.unpack_4bit_codes(codes.cpu(), numel=n).view(reps, 128).long()
+    mean = cb[got].double().mean(0)
+    lower, upper, a, b = ref._endpoints(block, cb)
+    width = (b - a).double()
+    p_hi = ((block.double() - a.double()) / width.clamp_min(1e-12)).clamp(0, 1)
+    sd = (width * torch.sqrt(p_hi * (1 - p_hi) / reps)).clamp_min(1e-9)
+    assert ((mean - block.double()).abs() <= 5 * sd + 1e-7).all()
+    # code histogram: only the two neighbours occur, with frequency P(hi)
+    assert bool(((got == lower.long()) | (got == upper.long())).all())
+    freq = (got == upper.long()).double().mean(0)
+    mid = (lower != upper)
+    assert ((freq - p_hi).abs()[mid] <= 5 * torch.sqrt(p_hi * (1 - p_hi) / reps)[mid] + 1e-3).all()
+
+
+def test_update_sr_on_device_draws_are_preconditioner_unbiased():
+    log("update-SR statistics")
+    gen = torch.Generator().manual_seed(7)
+    block = torch.rand(128, generator=gen) ** 6 * 1e-6
+    block[0] = 1e-6
+    reps = 8192
+    values = block.repeat(reps)
+    n = values.numel()
+    bias, eps = 0.0975, 1e-8
+    codes = torch.empty(n // 2, dtype=torch.uint8, device=H.DEVICE)
+    scales = torch.empty(n // 128, dtype=torch.float32, device=H.DEVICE)
+    m = moment_desc("dyn4_upd_sr_fp32read", False, True, codes, scales, bias=bias, eps=eps)
+    m["rng_seed"], m["rng_offset"] = 777, 4096
+    v = values.to(H.DEVICE)
+    _lib.quantize(v.data_ptr(), n, m, stream())
+    got = q.unpack_4bit_codes(codes.cpu(), numel=n).view(reps, 128).long()
+    cb = ref.codebook("dyn4").double()
+    s = block.abs().max().double()
+
+    def f(level):
+        return 1.0 / (torch.sqrt(torch.clamp(s * level / bias, min=0.0)) + eps)
+
+    est = f(cb[got]).mean(0)
+    x = block.double() / s
+    target = f(x)
+    lower, upper, a, b = ref._endpoints((block / block.abs().max()).contiguous(), cb.float())
+    fa, fb = f(a.double()), f(b.double())
+    p_lo = ((target - fb) / (fa - fb).clamp_min(1e-300)).clamp(0, 1)
+    sd = (fa - fb).abs() * torch.sqrt(p_lo * (1 - p_lo) / reps)
+    assert ((est - target).abs() <= 5 * sd + 1e-5 * target).all()
