@@ -37,6 +37,17 @@ def log(msg):
     print(msg, flush=True)
 
 
+def test_host_sqrt_rounding_report():
+    """Record how often this host's ATen CPU sqrt (the oracle's) differs from the correctly
+    rounded square root the kernel computes; parameter comparisons depend on it."""
+    x = torch.rand(1 << 20, generator=torch.Generator().manual_seed(0)) * 1e-3
+    cr = np.sqrt(x.numpy().astype(np.float64)).astype(np.float32)
+    ulps = x.sqrt().numpy().view(np.int32).astype(np.int64) - cr.view(np.int32)
+    log(f"host {torch.backends.cpu.get_cpu_capability()}: ATen sqrt differs from correctly rounded on "
+        f"{np.mean(ulps != 0):.4%} of values (ulp offsets {sorted(set(np.unique(ulps).tolist()))})")
+    assert np.abs(ulps).max() <= 1
+
+
 # ---------------------------------------------------------------------------
 # Random draws
 # ---------------------------------------------------------------------------
@@ -160,15 +171,13 @@ def test_golden_trajectory(name):
         torch.cuda.synchronize()
         for i, p in enumerate(params):
             pre = f"after{k + 1}_p{i}"
-            H.assert_params_close(p, tensor(arrays[pre], cfg["dtype"]).reshape(p.shape), f"{name} step {k+1} p{i}")
             st = H.state_of(opt, p)
             assert st["step"] == int(arrays[f"{pre}_step"])
             for m in ("m1", "m2"):
-                scheme_sr = False
                 if f"{pre}_{m}_code" in arrays:
                     expect = torch.from_numpy(arrays[f"{pre}_{m}_code"])
                     flips = H.code_mismatch(st[f"{m}_code"], expect)
-                    budget = int(SR_BUDGET * p.numel()) if cfg["seed"] is not None or scheme_sr else 0
+                    budget = int(SR_BUDGET * p.numel()) if cfg["seed"] is not None else 0
                     assert flips <= budget, f"{name} {pre} {m}: {flips} code flips"
                     if flips == 0:
                         assert torch.equal(H.bits(st[f"{m}_scale"]),
@@ -176,6 +185,9 @@ def test_golden_trajectory(name):
                 else:
                     assert torch.equal(H.bits(st[f"{m}_fp32"].reshape(-1)),
                                        H.bits(torch.from_numpy(arrays[f"{pre}_{m}_fp32"]).reshape(-1))), (name, m)
+            exact = H.assert_params_close(p, tensor(arrays[pre], cfg["dtype"]).reshape(p.shape),
+                                          f"{name} step {k+1} p{i}", steps=k + 1)
+            log(f"  p{i}: parameters bit-exact {exact:.6f}")
 
 
 # ---------------------------------------------------------------------------
@@ -219,11 +231,10 @@ def run_pair(make_opt, shapes, dtype, steps, *, seed=0, grad_seed=1, m1_override
     return opt, params, oracle, cpu_params
 
 
-def compare_pair(opt, params, oracle, cpu_params, what, sr_moments=()):
+def compare_pair(opt, params, oracle, cpu_params, what, sr_moments=(), steps=1):
     total_flips = 0
     total_codes = 0
     for i, (p, cp) in enumerate(zip(params, cpu_params)):
-        H.assert_params_close(p, cp, f"{what} p{i}")
         st = H.state_of(opt, p)
         ost = H.oracle_state((oracle.states[i].m1, oracle.states[i].m2))
         assert set(st) - {"step"} == set(ost), (what, i, sorted(st), sorted(ost))
@@ -237,6 +248,9 @@ def compare_pair(opt, params, oracle, cpu_params, what, sr_moments=()):
                     assert torch.equal(H.bits(st[f"{m}_scale"]), H.bits(ost[f"{m}_scale"])), (what, i, m)
             else:
                 assert torch.equal(H.bits(st[f"{m}_fp32"].reshape(-1)), H.bits(ost[f"{m}_fp32"])), (what, i, m)
+        exact = H.assert_params_close(p, cp, f"{what} p{i}", steps=steps)
+        log(f"  p{i} {tuple(p.shape)}: parameters bit-exact {exact:.6f}")
+    log(f"  code flips {total_flips} of {total_codes}")
     assert total_flips <= SR_BUDGET * max(total_codes, 1) + 0.5, f"{what}: {total_flips} flips of {total_codes}"
     return total_flips
 
@@ -271,7 +285,7 @@ def test_mixed_list_16bit(dtype):
     args = dict(lr=2e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True, quant_rng_seed=3)
     out = run_pair(lambda ps: aw.ZIPSRAdamW4Bit(ps, **args), shapes, dtype, 4, seed=3, m1_override=([8], "nf4_sr"),
                    zero_block_frac=0.05)
-    compare_pair(*out, f"mixed {dtype}", sr_moments=("m1", "m2"))
+    compare_pair(*out, f"mixed {dtype}", sr_moments=("m1", "m2"), steps=4)
 
 
 def test_scheme_groups_reference_step():
