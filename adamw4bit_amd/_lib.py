@@ -117,9 +117,10 @@ def uniforms(seed: int, offset: int, n: int, out_ptr: int, stream: int) -> None:
 
 
 def encode_tables() -> np.ndarray:
-    """The kernels' encode lookup tables, shape (NUM_LUTS, LUT_ENTRIES, 2) uint32 (host only)."""
+    """The kernels' encode lookup tables, shape (NUM_LUTS, LUT_ENTRIES, 4) uint32 words
+    {threshold bits, base, level_lo bits, level_hi bits} (host only)."""
     lib = library()
     size = check(lib.aw4_encode_tables(None, 0), "aw4_encode_tables")
     out = np.zeros(size // 4, dtype=np.uint32)
     check(lib.aw4_encode_tables(out.ctypes.data, size), "aw4_encode_tables")
-    return out.reshape(NUM_LUTS, LUT_ENTRIES, 2)
+    return out.reshape(NUM_LUTS, LUT_ENTRIES, 4)

@@ -41,7 +41,7 @@ def command(output: str = LIBRARY, extra=()) -> list:
         "-ffp-contract=off",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-Wall", "-Wno-unused-function",
-        f"-I{INCLUDE}", SOURCE, "-o", output, *extra,
+        f"-I{INCLUDE}", f"-I{os.path.dirname(SOURCE)}", SOURCE, "-o", output, *extra,
     ]
 
 

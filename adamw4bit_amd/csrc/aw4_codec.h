@@ -1,0 +1,251 @@
+// 4-bit block codec of the fused step: codebook tables, decode, and encode with
+// round-to-nearest, value-space or preconditioner-space stochastic rounding.
+//
+// Block layout: a 128-value block is owned by 8 lanes; lane j holds the 16 values at
+// offsets 32q + 4j + t (q, t = 0..3).  Its codes are 4 little-endian 16-bit words
+// (word q at byte offset 16q + 2j of the block's 64 code bytes; nibble t = value t).
+#pragma once
+
+#include "aw4_math.h"
+#include "adamw4bit_hip.h"
+
+namespace aw4 {
+
+constexpr int kBlock = AW4_BLOCK;
+constexpr int kPairs = 17;  // searchsorted-left results 0..16
+
+// Rounding kinds (AW4_ROUND_*) and "any": the kind is read from the descriptor at run time.
+enum : int { K_FP32 = AW4_ROUND_FP32, K_RTN = AW4_ROUND_RTN, K_SSR = AW4_ROUND_STATE_SR,
+             K_USR = AW4_ROUND_UPDATE_SR, K_ANY = 7 };
+
+// Lookup-table ids (aw4_encode_tables): round-to-nearest tables, then level-count tables.
+constexpr int kLutRtn[AW4_NUM_CODEBOOKS] = {0, 1, 2, 3, 4};
+constexpr int kLutRtnDyn4Floor = 5;
+constexpr int kLutLevels[AW4_NUM_CODEBOOKS] = {6, 7, 8, 9, 10};
+
+// Bucket of x -> code = base + (x >= thr).  For round-to-nearest tables lv_lo/lv_hi are
+// the levels of codes base and base + 1 (what EDEN multiplies by).
+struct __align__(16) LutEntry {
+    float thr;
+    uint32_t base;
+    float lv_lo;
+    float lv_hi;
+};
+
+// Neighbouring levels of a searchsorted-left index (_compiled_quantization.py:30-38).
+struct __align__(16) PairEntry {
+    float a;          // cb[lo]
+    float b;          // cb[hi]
+    float width_rcp;  // RN(1 / max(b - a, 1e-12))
+    uint32_t lohi;    // lo | hi << 8
+};
+
+// Per-block update-SR quantities for each searchsorted index (update_sr_tables()).
+struct __align__(16) UpdEntry {
+    float f_hi;   // preconditioner at the upper level
+    float den;    // max(f(lo) - f(hi), 1e-30)
+    float den_rcp;
+    float valid;  // 1 when (b > a) & (f(lo) - f(hi) > 0), else 0
+};
+
+// All tables of all codebooks, built on the host and kept in device memory.
+struct Tables {
+    float codebook[AW4_NUM_CODEBOOKS][16];
+    PairEntry pairs[AW4_NUM_CODEBOOKS][kPairs];
+    float2 dec[AW4_NUM_CODEBOOKS][256];  // code byte -> (level of low nibble, level of high nibble)
+    LutEntry lut[AW4_NUM_LUTS][AW4_LUT_ENTRIES];
+};
+
+// LDS views of the tables one moment needs.
+struct MomentTables {
+    const float* cb;
+    const PairEntry* pairs;
+    const float2* dec;
+    const LutEntry* lut;
+};
+
+__device__ __forceinline__ int lut_bucket_signed(float x) {
+    const uint32_t u = f2u(x);
+    const int k = min(max((int)__builtin_amdgcn_ubfe(u, 20, 11) - (AW4_LUT_EXP0 - 1), 0), AW4_LUT_HALF - 1);
+    return k + (int)(u >> 31) * AW4_LUT_HALF;
+}
+
+// Decode the 4 values of one 16-bit code word: two LDS reads of level pairs.
+__device__ __forceinline__ void decode4(const float2* dec, uint32_t w, float scale, float (&m)[4]) {
+    const float2 lo = dec[w & 0xffu];
+    const float2 hi = dec[(w >> 8) & 0xffu];
+    m[0] = lo.x * scale;
+    m[1] = lo.y * scale;
+    m[2] = hi.x * scale;
+    m[3] = hi.y * scale;
+}
+
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Per-block update-SR tables (_compiled_quantization.py:74-109): for every
+// searchsorted index i, f(hi), max(f(lo) - f(hi), 1e-30), its reciprocal and the
+// validity flag, with f(l) = 1 / (sqrt(max((s * l) / bias, 0)) + eps).
+__device__ __forceinline__ void update_sr_tables(const MomentTables& L, int j, float s, float bias, float bias_rcp,
+                                                 float eps, UpdEntry* upd, float* pre) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int k = j + 8 * h;
+        const float vh = clamp_min_nan(div_by_rcp(s * L.cb[k], bias, bias_rcp), 0.0f);
+        pre[k] = 1.0f / (sqrt_cr(vh) + eps);
+    }
+    wave_lds_sync();
+#pragma unroll
+    for (int h = 0; h < 3; ++h) {
+        const int i = j + 8 * h;
+        if (i < kPairs) {
+            const PairEntry pe = L.pairs[i];
+            const float flo = pre[pe.lohi & 0xffu], fhi = pre[pe.lohi >> 8];
+            const float den = flo - fhi;
+            const float dc = clamp_min_nan(den, 1e-30f);
+            UpdEntry e;
+            e.f_hi = fhi;
+            e.den = dc;
+            e.den_rcp = 1.0f / dc;
+            e.valid = (pe.b > pe.a && den > 0.0f) ? 1.0f : 0.0f;
+            upd[i] = e;
+        }
+    }
+    wave_lds_sync();
+}
+
+// Uniforms of this lane's 4 values of quarter q of block `blk` for one write of moment M.
+__device__ __forceinline__ void draws4(const aw4_moment& M, int64_t blk, int j, int q, bool active, float (&u)[4]) {
+    const int64_t e = blk * kBlock + 32 * q + 4 * j;
+    if (M.flags & AW4_MOMENT_EXT_DRAWS) {
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (active) v = *(const float4*)((const float*)M.draws + e);
+        u[0] = v.x; u[1] = v.y; u[2] = v.z; u[3] = v.w;
+    } else {
+        uniforms4(M.rng_seed, M.rng_offset + (uint64_t)e, u);
+    }
+}
+
+// Encode this lane's 16 values of block `blk` (_optimized_quantization.py:46-88):
+//   s = max(max|m|, 1e-12); x = m / s; codes by the rounding rule; [dyn4_nz floor]; [EDEN]
+// and store the 4 code words and (lane 0) the block scale.  Codes are produced a quarter
+// (4 values) at a time; the EDEN sums run in ATen's order (block_sum_cross).
+//
+// x is RN(m / s) computed from RN(1 / s).  When the quotient is subnormal (|m| < 2^-125 s)
+// it may differ from RN(m / s) by a few subnormal ulps; no output can see that: every
+// rounding table resolves [-2^-10, 2^-10] to one code or to the level-0 threshold at the
+// smallest subnormal, the preconditioner of such an x equals the one of 0 (eps absorbs
+// it), and its EDEN products vanish next to the block's |x| = 1 element.
+template <int KIND>
+__device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTables& L, int64_t blk, int j,
+                                             bool active, const float (&m)[16], UpdEntry* upd, float* pre) {
+    uint32_t amax = 0u;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) amax = max(amax, f2u(m[i]) & 0x7fffffffu);  // NaN-propagating |m| max
+    amax = block_max_u32(amax);
+    const float s = u2f(max(amax, 0x2B8CBCCCu));  // max(absmax, fp32(1e-12))
+    const bool fast = s < 0x1p125f;                // otherwise huge, infinite or NaN: IEEE division
+    const float y = 1.0f / s;
+    const bool eden = (M.flags & AW4_MOMENT_EDEN) != 0;
+    const bool guards = (M.flags & AW4_MOMENT_GUARDS) != 0;
+    const bool floor0 = (M.flags & AW4_MOMENT_ZERO_FLOOR) != 0;
+    if constexpr (KIND == K_USR) update_sr_tables(L, j, s, M.sr_bias, M.sr_bias_rcp, M.sr_eps, upd, pre);
+
+    float acc_xx[4] = {0.0f, 0.0f, 0.0f, 0.0f}, acc_xl[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    uint8_t* codes = (uint8_t*)M.codes + blk * (kBlock / 2) + 2 * j;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        float x[4];
+        if (__builtin_expect(fast, 1)) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) x[t] = div_by_rcp(m[4 * q + t], s, y);
+        } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) x[t] = m[4 * q + t] / s;
+        }
+        uint32_t code[4];
+        float lv[4];
+        if constexpr (KIND == K_RTN) {
+            // code = base + (x >= thr); the level for EDEN comes with the entry.
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const LutEntry e = L.lut[lut_bucket_signed(x[t])];
+                const bool up = x[t] >= e.thr;
+                code[t] = e.base + (up ? 1u : 0u);
+                lv[t] = up ? e.lv_hi : e.lv_lo;
+            }
+        } else {
+            float u[4];
+            draws4(M, blk, j, q, active, u);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const LutEntry le = L.lut[lut_bucket_signed(x[t])];
+                const uint32_t idx = le.base + (x[t] >= le.thr ? 1u : 0u);
+                const PairEntry pe = L.pairs[idx];
+                float p;
+                if constexpr (KIND == K_SSR) {
+                    // P(hi) = (x - a) / max(b - a, 1e-12), 0 where b == a, clamped; guards x<=a -> 0,
+                    // x>=b -> 1 (_compiled_quantization.py:60-71); code = u < P ? hi : lo.
+                    const float width = pe.b - pe.a;
+                    p = div_by_rcp(x[t] - pe.a, width < 1e-12f ? 1e-12f : width, pe.width_rcp);
+                    p = width > 0.0f ? p : 0.0f;
+                    p = clamp01_nan(p);
+                    if (guards) {
+                        p = x[t] >= pe.b ? 1.0f : p;
+                        p = x[t] <= pe.a ? 0.0f : p;
+                    }
+                    code[t] = u[t] < p ? (pe.lohi >> 8) : (pe.lohi & 0xffu);
+                } else {
+                    // P(lo) = (f(x) - f(b)) / max(f(a) - f(b), 1e-30), 1 unless b > a and f(a) > f(b),
+                    // clamped; guards x<=a -> 1, x>=b -> 0 (_compiled_quantization.py:74-109).
+                    const UpdEntry ue = upd[idx];
+                    const float vh = clamp_min_nan(div_by_rcp(s * x[t], M.sr_bias, M.sr_bias_rcp), 0.0f);
+                    const float fx = 1.0f / (sqrt_cr(vh) + M.sr_eps);
+                    p = div_by_rcp(fx - ue.f_hi, ue.den, ue.den_rcp);
+                    p = ue.valid != 0.0f ? p : 1.0f;
+                    p = clamp01_nan(p);
+                    if (guards) {
+                        p = x[t] >= pe.b ? 0.0f : p;
+                        p = x[t] <= pe.a ? 1.0f : p;
+                    }
+                    code[t] = u[t] < p ? (pe.lohi & 0xffu) : (pe.lohi >> 8);
+                }
+                if (floor0) code[t] = max(code[t], 1u);
+                lv[t] = eden ? L.cb[code[t]] : 0.0f;
+            }
+        }
+        if (eden) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                acc_xx[t] = acc_xx[t] + x[t] * x[t];
+                acc_xl[t] = acc_xl[t] + x[t] * lv[t];
+            }
+        }
+        if (active) {
+            const uint32_t w = code[0] | (code[1] << 4) | (code[2] << 8) | (code[3] << 12);
+            __builtin_nontemporal_store((uint16_t)w, (uint16_t*)(codes + 16 * q));
+        }
+    }
+
+    float scale = s;
+    if (eden) {
+        // s' = s * (sum x*x / max(sum x*cb[code], 1e-12))  (_optimized_quantization.py:81-85)
+        const float num = block_sum_cross(acc_xx);
+        const float den = block_sum_cross(acc_xl);
+        scale = s * (num / clamp_min_nan(den, 1e-12f));
+    }
+    if (active && j == 0) __builtin_nontemporal_store(scale, (float*)M.scales + blk);
+}
+
+// Runtime dispatch over the rounding kind (generic kernels).
+__device__ __forceinline__ void encode_block_any(const aw4_moment& M, const MomentTables& L, int64_t blk, int j,
+                                                 bool active, const float (&m)[16], UpdEntry* upd, float* pre) {
+    if (M.rounding == K_RTN) encode_block<K_RTN>(M, L, blk, j, active, m, upd, pre);
+    else if (M.rounding == K_SSR) encode_block<K_SSR>(M, L, blk, j, active, m, upd, pre);
+    else encode_block<K_USR>(M, L, blk, j, active, m, upd, pre);
+}
+
+}  // namespace aw4

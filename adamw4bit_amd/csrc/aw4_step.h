@@ -1,0 +1,453 @@
+// The fused AdamW step over one launch table: per-tile pipeline (prefetch the next
+// tile's inputs, decode, AdamW, re-encode, store) specialised by moment kinds and
+// parameter dtype.
+#pragma once
+
+#include <type_traits>
+
+#include "aw4_codec.h"
+
+namespace aw4 {
+
+constexpr int kBlocksPerWave = 8;
+constexpr int kWaveTile = kBlock * kBlocksPerWave;  // 1024 values per wave tile
+constexpr int kThreads = 256;
+constexpr int kWavesPerGroup = kThreads / 64;
+
+// Parameter/gradient storage kinds (AW4_F32 / AW4_BF16 / AW4_F16) and "any" (run time).
+enum : int { D_F32 = AW4_F32, D_BF16 = AW4_BF16, D_F16 = AW4_F16, D_ANY = 7 };
+
+// Launch table staged in device memory: header, tensors[count], tile_start[count + 1].
+struct StepHeader {
+    int32_t count;
+    int32_t cb1, lut1, cb2, lut2;  // codebook / lookup table of each moment (specialised kernels)
+    int32_t reserved;
+    int64_t total_tiles;
+    int64_t tiles_per_wave;
+};
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// 4-value vector access (streaming: each byte is touched once per step)
+// ---------------------------------------------------------------------------
+
+// Raw 32-bit words of 4 values: fp32 values, or 2 words of packed 16-bit values.
+template <int D>
+__device__ __forceinline__ void load_words(const void* base, int64_t e, bool vec, uint32_t* w) {
+    if constexpr (D == D_F32) {
+        const float* p = (const float*)base + e;
+        if (vec) {
+            const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+            w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+        } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) w[t] = f2u(p[t]);
+        }
+    } else {
+        const uint16_t* p = (const uint16_t*)base + e;
+        if (vec) {
+            const u32x2 v = __builtin_nontemporal_load((const u32x2*)p);
+            w[0] = v.x; w[1] = v.y;
+        } else {
+            w[0] = (uint32_t)p[0] | ((uint32_t)p[1] << 16);
+            w[1] = (uint32_t)p[2] | ((uint32_t)p[3] << 16);
+        }
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void words_to_f32(const uint32_t* w, float (&o)[4]) {
+    if constexpr (D == D_F32) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) o[t] = u2f(w[t]);
+    } else if constexpr (D == D_BF16) {
+        o[0] = bf16_to_f32(w[0] & 0xffffu); o[1] = bf16_to_f32(w[0] >> 16);
+        o[2] = bf16_to_f32(w[1] & 0xffffu); o[3] = bf16_to_f32(w[1] >> 16);
+    } else {
+        o[0] = f16_to_f32(w[0] & 0xffffu); o[1] = f16_to_f32(w[0] >> 16);
+        o[2] = f16_to_f32(w[1] & 0xffffu); o[3] = f16_to_f32(w[1] >> 16);
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void store_f32(void* base, int64_t e, bool vec, const float (&v)[4]) {
+    if constexpr (D == D_F32) {
+        float* p = (float*)base + e;
+        if (vec) {
+            __builtin_nontemporal_store(f32x4{v[0], v[1], v[2], v[3]}, (f32x4*)p);
+        } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) p[t] = v[t];
+        }
+    } else {
+        uint32_t h[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) h[t] = D == D_BF16 ? f32_to_bf16(v[t]) : f32_to_f16(v[t]);
+        uint16_t* p = (uint16_t*)base + e;
+        if (vec) {
+            __builtin_nontemporal_store(u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)}, (u32x2*)p);
+        } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) p[t] = (uint16_t)h[t];
+        }
+    }
+}
+
+template <int D>
+__device__ __forceinline__ float round_to_storage(float v) {
+    if constexpr (D == D_BF16) return bf16_to_f32(f32_to_bf16(v));
+    else if constexpr (D == D_F16) return f16_to_f32(f32_to_f16(v));
+    else return v;
+}
+
+// Run-time dtype dispatch for the generic kernel (D_ANY): loads convert to fp32 words.
+__device__ __forceinline__ void load_words_any(int dtype, const void* base, int64_t e, bool vec, uint32_t* w) {
+    uint32_t r[4];
+    float f[4];
+    if (dtype == D_F32) {
+        load_words<D_F32>(base, e, vec, w);
+        return;
+    }
+    if (dtype == D_BF16) {
+        load_words<D_BF16>(base, e, vec, r);
+        words_to_f32<D_BF16>(r, f);
+    } else {
+        load_words<D_F16>(base, e, vec, r);
+        words_to_f32<D_F16>(r, f);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) w[t] = f2u(f[t]);
+}
+
+// ---------------------------------------------------------------------------
+// AdamW arithmetic of one value (_optimized.py:215-222, ATen operation order)
+// ---------------------------------------------------------------------------
+
+// m1 = lerp(m1, g, 1-beta1); m2 = lerp(m2, g*g, 1-beta2): ATen's lerp is one fused
+// multiply-add, fma(w, end - start, start) for |w| < 0.5 and fma(w - 1, end - start, end)
+// otherwise (the host passes w - 1 and sets the LERP*_LARGE flag).
+template <bool kLarge1, bool kLarge2>
+__device__ __forceinline__ void moments_update(const aw4_tensor& T, float g, float& m1, float& m2) {
+    const float gg = g * g;
+    m1 = __builtin_fmaf(T.w1, g - m1, kLarge1 ? g : m1);
+    m2 = __builtin_fmaf(T.w2, gg - m2, kLarge2 ? gg : m2);
+}
+
+// p = p * (1 - lr*wd) [rounded to storage]; p = p + (-lr/bc1 * m1) / (sqrt(m2) / sqrt(bc2) + eps).
+template <int D>
+__device__ __forceinline__ float param_update(const aw4_tensor& T, float p, float m1, float m2) {
+    const float sq = sqrt_cr(m2);
+    const float d = __builtin_amdgcn_div_fixupf(div_by_rcp(sq, T.bc2_sqrt, T.bc2_sqrt_rcp), T.bc2_sqrt, sq) + T.eps;
+    const float p1 = round_to_storage<D>(p * T.decay);
+    return p1 + div_cr(T.step_coef * m1, d);
+}
+
+// ---------------------------------------------------------------------------
+// Tiles of tensors whose numel is a multiple of 128 (block layout)
+// ---------------------------------------------------------------------------
+
+// Raw inputs of one lane for one wave tile (blocks blk0 .. blk0+7; lane's block blk0 + lane/8).
+template <int M1K, int M2K, int D>
+struct TileInputs {
+    static constexpr int kW = (D == D_F32 || D == D_ANY) ? 4 : 2;  // words per 4 values
+    static constexpr bool kQ1 = M1K != K_FP32, kV1 = M1K == K_FP32 || M1K == K_ANY;
+    static constexpr bool kQ2 = M2K != K_FP32, kV2 = M2K == K_FP32 || M2K == K_ANY;
+    uint32_t g[4 * kW];
+    uint32_t p[4 * kW];
+    uint32_t c1[kQ1 ? 4 : 1], c2[kQ2 ? 4 : 1];
+    float s1, s2;
+    float v1[kV1 ? 16 : 1], v2[kV2 ? 16 : 1];
+};
+
+__device__ __forceinline__ bool is_quantized(const aw4_moment& m) { return m.rounding != K_FP32; }
+
+template <int MK>
+__device__ __forceinline__ bool moment_quantized(const aw4_moment& m) {
+    if constexpr (MK == K_ANY) return is_quantized(m);
+    else return MK != K_FP32;
+}
+
+template <int M1K, int M2K, int D>
+__device__ __forceinline__ void load_tile(const aw4_tensor& T, int64_t blk0, int lane, TileInputs<M1K, M2K, D>& in) {
+    using In = TileInputs<M1K, M2K, D>;
+    const int j = lane & 7;
+    const int64_t blk = blk0 + (lane >> 3);
+    const bool active = blk < (T.numel >> 7);
+    const int64_t e0 = blk * kBlock + 4 * j;
+    const bool vec = (T.flags & AW4_TENSOR_VEC_ALIGNED) != 0;
+#pragma unroll
+    for (int i = 0; i < 4 * In::kW; ++i) in.g[i] = in.p[i] = 0u;
+    in.s1 = in.s2 = 0.0f;
+    if (active) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if constexpr (D == D_ANY) {
+                load_words_any(T.grad_dtype, (const void*)T.grad, e0 + 32 * q, vec, &in.g[4 * q]);
+                load_words_any(T.param_dtype, (const void*)T.param, e0 + 32 * q, vec, &in.p[4 * q]);
+            } else {
+                load_words<D>((const void*)T.grad, e0 + 32 * q, vec, &in.g[In::kW * q]);
+                load_words<D>((const void*)T.param, e0 + 32 * q, vec, &in.p[In::kW * q]);
+            }
+        }
+    }
+    auto load_moment = [&](const aw4_moment& M, uint32_t* c, float& s, float* v, auto quant, auto vals) {
+        constexpr bool kQ = decltype(quant)::value, kV = decltype(vals)::value;
+        if constexpr (kQ) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) c[q] = 0u;
+        }
+        if constexpr (kV) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[i] = 0.0f;
+        }
+        if (!active) return;
+        if (kQ && (!kV || is_quantized(M))) {
+            if constexpr (kQ) {
+                const uint8_t* codes = (const uint8_t*)M.codes + blk * (kBlock / 2) + 2 * j;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) c[q] = __builtin_nontemporal_load((const uint16_t*)(codes + 16 * q));
+                s = ((const float*)M.scales)[blk];
+            }
+        } else if constexpr (kV) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const f32x4 x = __builtin_nontemporal_load((const f32x4*)((const float*)M.values + e0 + 32 * q));
+                v[4 * q] = x.x; v[4 * q + 1] = x.y; v[4 * q + 2] = x.z; v[4 * q + 3] = x.w;
+            }
+        }
+    };
+    load_moment(T.m1, in.c1, in.s1, in.v1, std::integral_constant<bool, In::kQ1>(),
+                std::integral_constant<bool, In::kV1>());
+    load_moment(T.m2, in.c2, in.s2, in.v2, std::integral_constant<bool, In::kQ2>(),
+                std::integral_constant<bool, In::kV2>());
+}
+
+template <int MK>
+__device__ __forceinline__ void encode_moment(const aw4_moment& M, const MomentTables& L, int64_t blk, int j,
+                                              bool active, const float (&m)[16], UpdEntry* upd, float* pre) {
+    if constexpr (MK == K_ANY) encode_block_any(M, L, blk, j, active, m, upd, pre);
+    else encode_block<MK>(M, L, blk, j, active, m, upd, pre);
+}
+
+// Decode, update and store one quarter (4 values) of this lane; the new moments go to m1/m2.
+template <int M1K, int M2K, int D, int DP, bool kGenericLerp>
+__device__ __forceinline__ void update_quarter(const aw4_tensor& T, int q, const TileInputs<M1K, M2K, D>& in,
+                                               const MomentTables& L1, const MomentTables& L2, bool active,
+                                               int64_t e0, bool vec, float (&m1)[16], float (&m2)[16]) {
+    using In = TileInputs<M1K, M2K, D>;
+    constexpr int DC = D == D_ANY ? D_F32 : D;  // generic loads are already fp32 words
+    float g[4], p[4], a[4], b[4];
+    words_to_f32<DC>(&in.g[In::kW * q], g);
+    words_to_f32<DC>(&in.p[In::kW * q], p);
+    if (moment_quantized<M1K>(T.m1)) {
+        if constexpr (In::kQ1) decode4(L1.dec, in.c1[q], in.s1, a);
+    } else {
+        if constexpr (In::kV1) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) a[t] = in.v1[4 * q + t];
+        }
+    }
+    if (moment_quantized<M2K>(T.m2)) {
+        if constexpr (In::kQ2) decode4(L2.dec, in.c2[q], in.s2, b);
+    } else {
+        if constexpr (In::kV2) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) b[t] = in.v2[4 * q + t];
+        }
+    }
+    const bool large1 = (T.flags & AW4_TENSOR_LERP1_LARGE) != 0, large2 = (T.flags & AW4_TENSOR_LERP2_LARGE) != 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        if constexpr (kGenericLerp) {
+            const float gg = g[t] * g[t];
+            a[t] = __builtin_fmaf(T.w1, g[t] - a[t], large1 ? g[t] : a[t]);
+            b[t] = __builtin_fmaf(T.w2, gg - b[t], large2 ? gg : b[t]);
+        } else {
+            moments_update<false, false>(T, g[t], a[t], b[t]);
+        }
+        p[t] = param_update<DP>(T, p[t], a[t], b[t]);
+        m1[4 * q + t] = a[t];
+        m2[4 * q + t] = b[t];
+    }
+    if (active) {
+        if constexpr (D == D_ANY) {
+            if (T.param_dtype == D_F32) store_f32<D_F32>((void*)T.param, e0 + 32 * q, vec, p);
+            else if (T.param_dtype == D_BF16) store_f32<D_BF16>((void*)T.param, e0 + 32 * q, vec, p);
+            else store_f32<D_F16>((void*)T.param, e0 + 32 * q, vec, p);
+        } else {
+            store_f32<D>((void*)T.param, e0 + 32 * q, vec, p);
+        }
+    }
+}
+
+template <int M1K, int M2K, int D, int DP>
+__device__ __forceinline__ void update_tile(const aw4_tensor& T, const TileInputs<M1K, M2K, D>& in,
+                                            const MomentTables& L1, const MomentTables& L2, bool active, int64_t e0,
+                                            bool vec, float (&m1)[16], float (&m2)[16]) {
+    if (__builtin_expect((T.flags & (AW4_TENSOR_LERP1_LARGE | AW4_TENSOR_LERP2_LARGE)) == 0, 1)) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            update_quarter<M1K, M2K, D, DP, false>(T, q, in, L1, L2, active, e0, vec, m1, m2);
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            update_quarter<M1K, M2K, D, DP, true>(T, q, in, L1, L2, active, e0, vec, m1, m2);
+    }
+}
+
+template <int M1K, int M2K, int D>
+__device__ __forceinline__ void compute_tile(const aw4_tensor& T, int64_t blk0, int lane,
+                                             const TileInputs<M1K, M2K, D>& in, const MomentTables& L1,
+                                             const MomentTables& L2, UpdEntry (*upd)[kPairs], float (*pre)[16]) {
+    const int j = lane & 7;
+    const int grp = lane >> 3;
+    const int64_t blk = blk0 + grp;
+    const bool active = blk < (T.numel >> 7);
+    const int64_t e0 = blk * kBlock + 4 * j;
+    const bool vec = (T.flags & AW4_TENSOR_VEC_ALIGNED) != 0;
+
+    float m1[16], m2[16];
+    if constexpr (D == D_ANY) {
+        if (T.param_dtype == D_F32) update_tile<M1K, M2K, D, D_F32>(T, in, L1, L2, active, e0, vec, m1, m2);
+        else if (T.param_dtype == D_BF16) update_tile<M1K, M2K, D, D_BF16>(T, in, L1, L2, active, e0, vec, m1, m2);
+        else update_tile<M1K, M2K, D, D_F16>(T, in, L1, L2, active, e0, vec, m1, m2);
+    } else {
+        update_tile<M1K, M2K, D, D>(T, in, L1, L2, active, e0, vec, m1, m2);
+    }
+
+    auto finish = [&](const aw4_moment& M, const MomentTables& L, const float (&m)[16], auto kind) {
+        constexpr int MK = decltype(kind)::value;
+        if (moment_quantized<MK>(M)) {
+            if constexpr (MK != K_FP32) encode_moment<MK>(M, L, blk, j, active, m, upd[grp], pre[grp]);
+        } else if (active) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                __builtin_nontemporal_store(f32x4{m[4 * q], m[4 * q + 1], m[4 * q + 2], m[4 * q + 3]},
+                                            (f32x4*)((float*)M.values + e0 + 32 * q));
+        }
+    };
+    finish(T.m1, L1, m1, std::integral_constant<int, M1K>());
+    finish(T.m2, L2, m2, std::integral_constant<int, M2K>());
+}
+
+// ---------------------------------------------------------------------------
+// Tiles of fp32-state tensors with any numel (values e_tile .. e_tile + 1023)
+// ---------------------------------------------------------------------------
+
+template <int D>
+__device__ __forceinline__ float load_value(const aw4_tensor& T, const void* base, int dtype, int64_t k) {
+    const int dt = D == D_ANY ? dtype : D;
+    if (dt == D_F32) return ((const float*)base)[k];
+    const uint32_t h = ((const uint16_t*)base)[k];
+    return dt == D_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+}
+
+template <int D>
+__device__ __forceinline__ void step_values_one(const aw4_tensor& T, int64_t k) {
+    float* v1 = (float*)T.m1.values;
+    float* v2 = (float*)T.m2.values;
+    const float g = load_value<D>(T, (const void*)T.grad, T.grad_dtype, k);
+    float p = load_value<D>(T, (const void*)T.param, T.param_dtype, k);
+    float a = v1[k], b = v2[k];
+    const int lf = T.flags & (AW4_TENSOR_LERP1_LARGE | AW4_TENSOR_LERP2_LARGE);
+    if (lf == 0) moments_update<false, false>(T, g, a, b);
+    else if (lf == AW4_TENSOR_LERP1_LARGE) moments_update<true, false>(T, g, a, b);
+    else if (lf == AW4_TENSOR_LERP2_LARGE) moments_update<false, true>(T, g, a, b);
+    else moments_update<true, true>(T, g, a, b);
+    const int dt = D == D_ANY ? T.param_dtype : D;
+    if (dt == D_F32) {
+        p = param_update<D_F32>(T, p, a, b);
+        ((float*)T.param)[k] = p;
+    } else if (dt == D_BF16) {
+        p = param_update<D_BF16>(T, p, a, b);
+        ((uint16_t*)T.param)[k] = (uint16_t)f32_to_bf16(p);
+    } else {
+        p = param_update<D_F16>(T, p, a, b);
+        ((uint16_t*)T.param)[k] = (uint16_t)f32_to_f16(p);
+    }
+    v1[k] = a;
+    v2[k] = b;
+}
+
+template <int D>
+__device__ void step_tile_values(const aw4_tensor& T, int64_t e_tile, int lane) {
+    const int j = lane & 7;
+    const int grp = lane >> 3;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int64_t e = e_tile + grp * kBlock + 32 * q + 4 * j;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            if (e + t < T.numel) step_values_one<D>(T, e + t);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// The kernel: each wave walks a contiguous range of wave tiles; the inputs of the
+// next block-layout tile are loaded before the current tile is computed.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ bool values_only(const aw4_tensor& T) {
+    return !is_quantized(T.m1) && !is_quantized(T.m2);
+}
+
+template <int M1K, int M2K, int D, class LdsT>
+__device__ __forceinline__ void run_tiles(const StepHeader* hdr, const LdsT& lds_tables, UpdEntry (*upd)[kPairs],
+                                          float (*pre)[16]) {
+    const aw4_tensor* tensors = (const aw4_tensor*)(hdr + 1);
+    const int64_t* tile_start = (const int64_t*)(tensors + hdr->count);
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * kWavesPerGroup + (threadIdx.x >> 6)));
+    const int64_t total = hdr->total_tiles;
+    int64_t tile = wave * hdr->tiles_per_wave;
+    const int64_t end = min(tile + hdr->tiles_per_wave, total);
+    if (tile >= end) return;
+
+    int lo = 0, hi = hdr->count - 1;  // tensor of `tile`: last ti with tile_start[ti] <= tile
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (tile_start[mid] <= tile) lo = mid; else hi = mid - 1;
+    }
+    int ti = lo;
+
+    TileInputs<M1K, M2K, D> cur;
+    bool cur_loaded = false;
+    while (tile < end) {
+        while (tile >= tile_start[ti + 1]) ++ti;
+        const aw4_tensor& T = tensors[ti];
+        const int64_t local = tile - tile_start[ti];
+        if (values_only(T) || (T.numel & (kBlock - 1)) != 0) {
+            if constexpr (D == D_ANY) step_tile_values<D_ANY>(T, local * kWaveTile, lane);
+            else step_tile_values<D>(T, local * kWaveTile, lane);
+            ++tile;
+            cur_loaded = false;
+            continue;
+        }
+        if (!cur_loaded) load_tile(T, local * kBlocksPerWave, lane, cur);
+        // prefetch the next tile when it is a block-layout tile (specialised kernels only:
+        // the generic kernel's register budget has no room for a second tile)
+        constexpr bool kPrefetch = M1K != K_ANY && M2K != K_ANY && D != D_ANY;
+        const int64_t next = tile + 1;
+        TileInputs<M1K, M2K, D> nxt;
+        bool nxt_loaded = false;
+        if (kPrefetch && next < end) {
+            const int tn = next >= tile_start[ti + 1] ? ti + 1 : ti;
+            const aw4_tensor& N = tensors[tn];
+            if (!values_only(N) && (N.numel & (kBlock - 1)) == 0) {
+                load_tile(N, (next - tile_start[tn]) * kBlocksPerWave, lane, nxt);
+                nxt_loaded = true;
+            }
+        }
+        const MomentTables L1 = lds_tables.moment(T.m1, 0);
+        const MomentTables L2 = lds_tables.moment(T.m2, 1);
+        compute_tile(T, local * kBlocksPerWave, lane, cur, L1, L2, upd, pre);
+        cur = nxt;
+        cur_loaded = nxt_loaded;
+        tile = next;
+    }
+}
+
+}  // namespace aw4

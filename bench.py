@@ -115,6 +115,8 @@ def main():
     ap.add_argument("--recipes", default="zeeden,zipsr")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--copy-probe-gb", type=float, default=0.0,
+                    help="also run plain device copies of this many GB (calibrates HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the optimizer step is replica-local "
@@ -127,6 +129,16 @@ def main():
 
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
+    if args.copy_probe_gb > 0:
+        # A plain copy of known size: its FETCH_SIZE / WRITE_SIZE per dispatch calibrate the counters.
+        n = int(args.copy_probe_gb * 1e9) // 4
+        src = torch.ones(n, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"[bench] copy probe: 3 copies of {n * 4} bytes", file=sys.stderr, flush=True)
+        del src, dst
     shapes = CONFIGS[args.config]()
     numels = [math.prod(s) for s in shapes]
     total = sum(numels)

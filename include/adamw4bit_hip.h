@@ -157,8 +157,10 @@ int aw4_uniforms(uint64_t seed, uint64_t offset, int64_t n, float* out, void* st
  * Host-only: copy the encode lookup tables the kernels use into `out`
  * (host memory, `bytes` long); returns the table size in bytes (call with
  * out = 0 to query) or a negative error.  Layout: for each of AW4_NUM_LUTS
- * tables, AW4_LUT_ENTRIES pairs {float threshold; uint32 base}: a value x
- * in bucket k (aw4 bucket function below) encodes to base + (x >= threshold).
+ * tables, AW4_LUT_ENTRIES entries {float threshold; uint32 base; float
+ * level_lo; float level_hi}: a value x in bucket k (bucket function below)
+ * encodes to base + (x >= threshold), whose codebook level is level_lo or
+ * level_hi (round-to-nearest tables; 0 in the level-count tables).
  * Tables 0..5: round-to-nearest codes for nf4, sdyn4, dyn4, lin4, lin4_nz,
  * dyn4 with the zero floor; tables 6..10: searchsorted-left counts
  * (number of levels < x) for nf4, sdyn4, dyn4, lin4, lin4_nz.

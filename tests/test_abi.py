@@ -112,6 +112,16 @@ def lut_eval(tables, lut_id, x):
     return tables[lut_id, idx, 1].astype(np.int64) + (x >= thr)
 
 
+def lut_level(tables, lut_id, x):
+    """Level of the encoded code as the kernel reads it from the entry."""
+    u = x.view(np.uint32).astype(np.int64)
+    k = np.clip(((u & 0x7FFFFFFF) >> 20) - (_lib.LUT_EXP0 - 1), 0, _lib.LUT_HALF - 1)
+    idx = k + (u >> 31) * _lib.LUT_HALF
+    e = tables[lut_id, idx]
+    up = x >= e[:, 0].view(np.float32)
+    return np.where(up, e[:, 3].view(np.float32), e[:, 2].view(np.float32))
+
+
 def reference_rules(cb: np.ndarray, x: np.ndarray):
     """searchsorted-left count and the round-to-nearest code, via the oracle's torch ops."""
     xt = torch.from_numpy(x)
@@ -153,8 +163,11 @@ def test_encode_tables_reproduce_rounding_rules(mode, cb_id):
     count, rtn = reference_rules(cb, x)
     assert np.array_equal(lut_eval(tables, cb_id, x), rtn)                 # round-to-nearest table
     assert np.array_equal(lut_eval(tables, 6 + cb_id, x), count)           # level-count table
+    assert np.array_equal(lut_level(tables, cb_id, x), cb[rtn])            # the level EDEN uses
     if mode == "dyn4":
-        assert np.array_equal(lut_eval(tables, 5, x), np.maximum(rtn, 1))  # dyn4_nz floor table
+        floored = np.maximum(rtn, 1)
+        assert np.array_equal(lut_eval(tables, 5, x), floored)             # dyn4_nz floor table
+        assert np.array_equal(lut_level(tables, 5, x), cb[floored])
 
 
 def test_aten_row_sum_order():
