@@ -64,6 +64,11 @@ struct MomentTables {
     const LutEntry* lut;
 };
 
+// Bucket of an x >= -0 (second moments): only the magnitude half of the table.
+__device__ __forceinline__ int lut_bucket_unsigned(float x) {
+    return min(max((int)__builtin_amdgcn_ubfe(f2u(x), 20, 11) - (AW4_LUT_EXP0 - 1), 0), AW4_LUT_HALF - 1);
+}
+
 __device__ __forceinline__ int lut_bucket_signed(float x) {
     const uint32_t u = f2u(x);
     const int k = min(max((int)__builtin_amdgcn_ubfe(u, 20, 11) - (AW4_LUT_EXP0 - 1), 0), AW4_LUT_HALF - 1);
@@ -95,7 +100,7 @@ __device__ __forceinline__ void update_sr_tables(const MomentTables& L, int j, f
     for (int h = 0; h < 2; ++h) {
         const int k = j + 8 * h;
         const float vh = clamp_min_nan(div_by_rcp(s * L.cb[k], bias, bias_rcp), 0.0f);
-        pre[k] = 1.0f / (sqrt_cr(vh) + eps);
+        pre[k] = rcp_faithful(sqrt_faithful(vh) + eps);
     }
     wave_lds_sync();
 #pragma unroll
@@ -117,15 +122,15 @@ __device__ __forceinline__ void update_sr_tables(const MomentTables& L, int j, f
     wave_lds_sync();
 }
 
-// Uniforms of this lane's 4 values of quarter q of block `blk` for one write of moment M.
-__device__ __forceinline__ void draws4(const aw4_moment& M, int64_t blk, int j, int q, bool active, float (&u)[4]) {
-    const int64_t e = blk * kBlock + 32 * q + 4 * j;
+// Uniforms of this lane's 4 values at offset `off` from value blk0 * 128 of one write of
+// moment M (stream position rng_offset + value index).
+__device__ __forceinline__ void draws4(const aw4_moment& M, int64_t blk0, uint32_t off, bool active, float (&u)[4]) {
     if (M.flags & AW4_MOMENT_EXT_DRAWS) {
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (active) v = *(const float4*)((const float*)M.draws + e);
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        if (active) v = *(gptr<const f32x4>)(gaddr<const float>(M.draws) + blk0 * kBlock + off);
         u[0] = v.x; u[1] = v.y; u[2] = v.z; u[3] = v.w;
     } else {
-        uniforms4(M.rng_seed, M.rng_offset + (uint64_t)e, u);
+        uniforms4(M.rng_seed, M.rng_offset + (uint64_t)blk0 * kBlock + off, u);
     }
 }
 
@@ -134,13 +139,16 @@ __device__ __forceinline__ void draws4(const aw4_moment& M, int64_t blk, int j, 
 // and store the 4 code words and (lane 0) the block scale.  Codes are produced a quarter
 // (4 values) at a time; the EDEN sums run in ATen's order (block_sum_cross).
 //
+// kNonNeg: the values are >= +0 (second moments: a lerp of a non-negative state towards
+// g*g), so only the magnitude half of the lookup tables is indexed.
+//
 // x is RN(m / s) computed from RN(1 / s).  When the quotient is subnormal (|m| < 2^-125 s)
 // it may differ from RN(m / s) by a few subnormal ulps; no output can see that: every
 // rounding table resolves [-2^-10, 2^-10] to one code or to the level-0 threshold at the
 // smallest subnormal, the preconditioner of such an x equals the one of 0 (eps absorbs
 // it), and its EDEN products vanish next to the block's |x| = 1 element.
-template <int KIND>
-__device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTables& L, int64_t blk, int j,
+template <int KIND, bool kNonNeg>
+__device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTables& L, int64_t blk0, int grp, int j,
                                              bool active, const float (&m)[16], UpdEntry* upd, float* pre) {
     uint32_t amax = 0u;
 #pragma unroll
@@ -155,7 +163,9 @@ __device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTa
     if constexpr (KIND == K_USR) update_sr_tables(L, j, s, M.sr_bias, M.sr_bias_rcp, M.sr_eps, upd, pre);
 
     float acc_xx[4] = {0.0f, 0.0f, 0.0f, 0.0f}, acc_xl[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    uint8_t* codes = (uint8_t*)M.codes + blk * (kBlock / 2) + 2 * j;
+    const gptr<uint8_t> codes = gaddr<uint8_t>(M.codes) + blk0 * (kBlock / 2);  // the tile's code bytes
+    const uint32_t coff = (uint32_t)(grp * (kBlock / 2) + 2 * j);
+    const uint32_t voff = (uint32_t)(grp * kBlock + 4 * j);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         float x[4];
@@ -172,17 +182,17 @@ __device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTa
             // code = base + (x >= thr); the level for EDEN comes with the entry.
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                const LutEntry e = L.lut[lut_bucket_signed(x[t])];
+                const LutEntry e = L.lut[kNonNeg ? lut_bucket_unsigned(x[t]) : lut_bucket_signed(x[t])];
                 const bool up = x[t] >= e.thr;
                 code[t] = e.base + (up ? 1u : 0u);
                 lv[t] = up ? e.lv_hi : e.lv_lo;
             }
         } else {
             float u[4];
-            draws4(M, blk, j, q, active, u);
+            draws4(M, blk0, voff + 32u * q, active, u);
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                const LutEntry le = L.lut[lut_bucket_signed(x[t])];
+                const LutEntry le = L.lut[kNonNeg ? lut_bucket_unsigned(x[t]) : lut_bucket_signed(x[t])];
                 const uint32_t idx = le.base + (x[t] >= le.thr ? 1u : 0u);
                 const PairEntry pe = L.pairs[idx];
                 float p;
@@ -203,7 +213,7 @@ __device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTa
                     // clamped; guards x<=a -> 1, x>=b -> 0 (_compiled_quantization.py:74-109).
                     const UpdEntry ue = upd[idx];
                     const float vh = clamp_min_nan(div_by_rcp(s * x[t], M.sr_bias, M.sr_bias_rcp), 0.0f);
-                    const float fx = 1.0f / (sqrt_cr(vh) + M.sr_eps);
+                    const float fx = rcp_faithful(sqrt_faithful(vh) + M.sr_eps);
                     p = div_by_rcp(fx - ue.f_hi, ue.den, ue.den_rcp);
                     p = ue.valid != 0.0f ? p : 1.0f;
                     p = clamp01_nan(p);
@@ -226,7 +236,7 @@ __device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTa
         }
         if (active) {
             const uint32_t w = code[0] | (code[1] << 4) | (code[2] << 8) | (code[3] << 12);
-            __builtin_nontemporal_store((uint16_t)w, (uint16_t*)(codes + 16 * q));
+            __builtin_nontemporal_store((uint16_t)w, (gptr<uint16_t>)(codes + coff + 16u * q));
         }
     }
 
@@ -237,15 +247,17 @@ __device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTa
         const float den = block_sum_cross(acc_xl);
         scale = s * (num / clamp_min_nan(den, 1e-12f));
     }
-    if (active && j == 0) __builtin_nontemporal_store(scale, (float*)M.scales + blk);
+    if (active && j == 0) __builtin_nontemporal_store(scale, gaddr<float>(M.scales) + blk0 + grp);
 }
 
 // Runtime dispatch over the rounding kind (generic kernels).
-__device__ __forceinline__ void encode_block_any(const aw4_moment& M, const MomentTables& L, int64_t blk, int j,
-                                                 bool active, const float (&m)[16], UpdEntry* upd, float* pre) {
-    if (M.rounding == K_RTN) encode_block<K_RTN>(M, L, blk, j, active, m, upd, pre);
-    else if (M.rounding == K_SSR) encode_block<K_SSR>(M, L, blk, j, active, m, upd, pre);
-    else encode_block<K_USR>(M, L, blk, j, active, m, upd, pre);
+template <bool kNonNeg>
+__device__ __forceinline__ void encode_block_any(const aw4_moment& M, const MomentTables& L, int64_t blk0, int grp,
+                                                 int j, bool active, const float (&m)[16], UpdEntry* upd,
+                                                 float* pre) {
+    if (M.rounding == K_RTN) encode_block<K_RTN, kNonNeg>(M, L, blk0, grp, j, active, m, upd, pre);
+    else if (M.rounding == K_SSR) encode_block<K_SSR, kNonNeg>(M, L, blk0, grp, j, active, m, upd, pre);
+    else encode_block<K_USR, kNonNeg>(M, L, blk0, grp, j, active, m, upd, pre);
 }
 
 }  // namespace aw4

@@ -1,16 +1,33 @@
 // Scalar arithmetic, cross-lane primitives and the counter-based generator of the fused step.
 //
-// Every routine that stands in for an ATen CPU operation returns the correctly
-// rounded fp32 result of that operation (ATen's fp32 division, reciprocal and
-// multiply-add are correctly rounded; its square root comes from a vector math
-// library and is within one ulp of the correctly rounded value, so results
-// downstream of a square root agree with it to one ulp).
+// ATen's fp32 multiply, add, division, reciprocal and fused multiply-add (lerp) are
+// correctly rounded, and so are the routines here that stand in for them wherever a
+// result feeds a code or a block scale.  ATen's CPU square root comes from a vector
+// math library and is only faithful (within one ulp of the correctly rounded value,
+// and host dependent), so the square roots here are the hardware's faithful one:
+// values downstream of a square root (the parameter update, update-SR preconditioners)
+// agree with the reference to about one ulp, as the reference agrees with itself
+// across hosts.
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace aw4 {
+
+// Global-memory pointers.  Device addresses read from a launch table are generic (flat)
+// pointers to the compiler; a flat access also counts against the LDS wait counter, so
+// every wait for an LDS table read would wait for the outstanding global loads and
+// stores too.  Casting to address space 1 gives global_* instructions (scalar base +
+// 32-bit lane offset) that leave LDS waits independent of HBM traffic.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <class T>
+using gptr = __attribute__((address_space(1))) T*;
+template <class T>
+__device__ __forceinline__ gptr<T> gaddr(uint64_t a) { return (gptr<T>)a; }
 
 __device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
 __device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
@@ -56,6 +73,16 @@ __device__ __forceinline__ float sqrt_cr(float x) {
     y = rdn <= 0.0f ? ydn : y;
     y = rup > 0.0f ? yup : y;
     return tiny ? y * 0x1p-16f : y;
+}
+
+// Faithful sqrt (v_sqrt_f32, <= 1 ulp), the precision class of ATen's CPU sqrt.
+__device__ __forceinline__ float sqrt_faithful(float x) { return __builtin_amdgcn_sqrtf(x); }
+
+// Reciprocal within one ulp: hardware estimate refined by one Newton step.
+__device__ __forceinline__ float rcp_faithful(float t) {
+    const float y0 = __builtin_amdgcn_rcpf(t);
+    const float e0 = __builtin_fmaf(-t, y0, 1.0f);
+    return __builtin_fmaf(e0, y0, y0);
 }
 
 // bf16 round-to-nearest-even (c10::BFloat16), NaN kept quiet.

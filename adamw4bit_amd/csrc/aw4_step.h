@@ -26,30 +26,26 @@ struct StepHeader {
     int64_t tiles_per_wave;
 };
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
 // ---------------------------------------------------------------------------
 // 4-value vector access (streaming: each byte is touched once per step)
 // ---------------------------------------------------------------------------
 
 // Raw 32-bit words of 4 values: fp32 values, or 2 words of packed 16-bit values.
 template <int D>
-__device__ __forceinline__ void load_words(const void* base, int64_t e, bool vec, uint32_t* w) {
+__device__ __forceinline__ void load_words(uint64_t base, int64_t e, bool vec, uint32_t* w) {
     if constexpr (D == D_F32) {
-        const float* p = (const float*)base + e;
+        const gptr<const float> p = gaddr<const float>(base) + e;
         if (vec) {
-            const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+            const u32x4 v = __builtin_nontemporal_load((gptr<const u32x4>)p);
             w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
         } else {
 #pragma unroll
             for (int t = 0; t < 4; ++t) w[t] = f2u(p[t]);
         }
     } else {
-        const uint16_t* p = (const uint16_t*)base + e;
+        const gptr<const uint16_t> p = gaddr<const uint16_t>(base) + e;
         if (vec) {
-            const u32x2 v = __builtin_nontemporal_load((const u32x2*)p);
+            const u32x2 v = __builtin_nontemporal_load((gptr<const u32x2>)p);
             w[0] = v.x; w[1] = v.y;
         } else {
             w[0] = (uint32_t)p[0] | ((uint32_t)p[1] << 16);
@@ -73,11 +69,11 @@ __device__ __forceinline__ void words_to_f32(const uint32_t* w, float (&o)[4]) {
 }
 
 template <int D>
-__device__ __forceinline__ void store_f32(void* base, int64_t e, bool vec, const float (&v)[4]) {
+__device__ __forceinline__ void store_f32(uint64_t base, int64_t e, bool vec, const float (&v)[4]) {
     if constexpr (D == D_F32) {
-        float* p = (float*)base + e;
+        const gptr<float> p = gaddr<float>(base) + e;
         if (vec) {
-            __builtin_nontemporal_store(f32x4{v[0], v[1], v[2], v[3]}, (f32x4*)p);
+            __builtin_nontemporal_store(f32x4{v[0], v[1], v[2], v[3]}, (gptr<f32x4>)p);
         } else {
 #pragma unroll
             for (int t = 0; t < 4; ++t) p[t] = v[t];
@@ -86,9 +82,9 @@ __device__ __forceinline__ void store_f32(void* base, int64_t e, bool vec, const
         uint32_t h[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) h[t] = D == D_BF16 ? f32_to_bf16(v[t]) : f32_to_f16(v[t]);
-        uint16_t* p = (uint16_t*)base + e;
+        const gptr<uint16_t> p = gaddr<uint16_t>(base) + e;
         if (vec) {
-            __builtin_nontemporal_store(u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)}, (u32x2*)p);
+            __builtin_nontemporal_store(u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)}, (gptr<u32x2>)p);
         } else {
 #pragma unroll
             for (int t = 0; t < 4; ++t) p[t] = (uint16_t)h[t];
@@ -104,7 +100,7 @@ __device__ __forceinline__ float round_to_storage(float v) {
 }
 
 // Run-time dtype dispatch for the generic kernel (D_ANY): loads convert to fp32 words.
-__device__ __forceinline__ void load_words_any(int dtype, const void* base, int64_t e, bool vec, uint32_t* w) {
+__device__ __forceinline__ void load_words_any(int dtype, uint64_t base, int64_t e, bool vec, uint32_t* w) {
     uint32_t r[4];
     float f[4];
     if (dtype == D_F32) {
@@ -139,7 +135,7 @@ __device__ __forceinline__ void moments_update(const aw4_tensor& T, float g, flo
 // p = p * (1 - lr*wd) [rounded to storage]; p = p + (-lr/bc1 * m1) / (sqrt(m2) / sqrt(bc2) + eps).
 template <int D>
 __device__ __forceinline__ float param_update(const aw4_tensor& T, float p, float m1, float m2) {
-    const float sq = sqrt_cr(m2);
+    const float sq = sqrt_faithful(m2);
     const float d = __builtin_amdgcn_div_fixupf(div_by_rcp(sq, T.bc2_sqrt, T.bc2_sqrt_rcp), T.bc2_sqrt, sq) + T.eps;
     const float p1 = round_to_storage<D>(p * T.decay);
     return p1 + div_cr(T.step_coef * m1, d);
@@ -170,52 +166,88 @@ __device__ __forceinline__ bool moment_quantized(const aw4_moment& m) {
     else return MK != K_FP32;
 }
 
+// Addressing of one lane within a wave tile: the tile's base pointers are wave-uniform
+// (scalar registers), the lane offsets 32-bit (values: grp*128 + 4j + 32q; code bytes:
+// grp*64 + 2j + 16q; scales: grp).
+struct TileLane {
+    int j, grp;
+    bool active;     // the lane's block exists (the last tile of a tensor may be partial)
+    int64_t blk0;    // first block of the tile (uniform)
+    uint32_t voff;   // value offset of (q = 0, t = 0) from the tile's first value
+};
+
+__device__ __forceinline__ TileLane tile_lane(const aw4_tensor& T, int64_t blk0, int lane) {
+    TileLane tl;
+    tl.j = lane & 7;
+    tl.grp = lane >> 3;
+    tl.blk0 = blk0;
+    tl.active = blk0 + tl.grp < (T.numel >> 7);
+    tl.voff = (uint32_t)(tl.grp * kBlock + 4 * tl.j);
+    return tl;
+}
+
+template <int D>
+__device__ __forceinline__ uint64_t tile_values(uint64_t base, int64_t blk0) {
+    return base + (uint64_t)blk0 * kBlock * (D == D_F32 ? 4 : 2);
+}
+
 template <int M1K, int M2K, int D>
-__device__ __forceinline__ void load_tile(const aw4_tensor& T, int64_t blk0, int lane, TileInputs<M1K, M2K, D>& in) {
+__device__ __forceinline__ void load_tile(const aw4_tensor& T, const TileLane& tl, TileInputs<M1K, M2K, D>& in) {
     using In = TileInputs<M1K, M2K, D>;
-    const int j = lane & 7;
-    const int64_t blk = blk0 + (lane >> 3);
-    const bool active = blk < (T.numel >> 7);
-    const int64_t e0 = blk * kBlock + 4 * j;
-    const bool vec = (T.flags & AW4_TENSOR_VEC_ALIGNED) != 0;
+    const bool vec = D != D_ANY || (T.flags & AW4_TENSOR_VEC_ALIGNED) != 0;  // specialised kernels: host-checked
 #pragma unroll
     for (int i = 0; i < 4 * In::kW; ++i) in.g[i] = in.p[i] = 0u;
     in.s1 = in.s2 = 0.0f;
-    if (active) {
+    if constexpr (In::kQ1) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            if constexpr (D == D_ANY) {
-                load_words_any(T.grad_dtype, (const void*)T.grad, e0 + 32 * q, vec, &in.g[4 * q]);
-                load_words_any(T.param_dtype, (const void*)T.param, e0 + 32 * q, vec, &in.p[4 * q]);
-            } else {
-                load_words<D>((const void*)T.grad, e0 + 32 * q, vec, &in.g[In::kW * q]);
-                load_words<D>((const void*)T.param, e0 + 32 * q, vec, &in.p[In::kW * q]);
-            }
+        for (int q = 0; q < 4; ++q) in.c1[q] = 0u;
+    }
+    if constexpr (In::kQ2) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) in.c2[q] = 0u;
+    }
+    if constexpr (In::kV1) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) in.v1[i] = 0.0f;
+    }
+    if constexpr (In::kV2) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) in.v2[i] = 0.0f;
+    }
+    if (!tl.active) return;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t off = tl.voff + 32u * q;
+        if constexpr (D == D_ANY) {
+            const int64_t e = tl.blk0 * kBlock + off;
+            load_words_any(T.grad_dtype, T.grad, e, vec, &in.g[4 * q]);
+            load_words_any(T.param_dtype, T.param, e, vec, &in.p[4 * q]);
+        } else {
+            load_words<D>(tile_values<D>(T.grad, tl.blk0), off, true, &in.g[In::kW * q]);
+            load_words<D>(tile_values<D>(T.param, tl.blk0), off, true, &in.p[In::kW * q]);
         }
     }
     auto load_moment = [&](const aw4_moment& M, uint32_t* c, float& s, float* v, auto quant, auto vals) {
         constexpr bool kQ = decltype(quant)::value, kV = decltype(vals)::value;
-        if constexpr (kQ) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) c[q] = 0u;
-        }
-        if constexpr (kV) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] = 0.0f;
-        }
-        if (!active) return;
-        if (kQ && (!kV || is_quantized(M))) {
+        bool quantized = kQ;
+        if constexpr (kQ && kV) quantized = is_quantized(M);
+        if (quantized) {
             if constexpr (kQ) {
-                const uint8_t* codes = (const uint8_t*)M.codes + blk * (kBlock / 2) + 2 * j;
+                const gptr<const uint8_t> codes = gaddr<const uint8_t>(M.codes) + tl.blk0 * (kBlock / 2);
+                const uint32_t coff = (uint32_t)(tl.grp * (kBlock / 2) + 2 * tl.j);
 #pragma unroll
-                for (int q = 0; q < 4; ++q) c[q] = __builtin_nontemporal_load((const uint16_t*)(codes + 16 * q));
-                s = ((const float*)M.scales)[blk];
+                for (int q = 0; q < 4; ++q)
+                    c[q] = __builtin_nontemporal_load((gptr<const uint16_t>)(codes + coff + 16u * q));
+                s = (gaddr<const float>(M.scales) + tl.blk0)[tl.grp];
             }
-        } else if constexpr (kV) {
+        } else {
+            if constexpr (kV) {
+                const gptr<const float> vals_tile = gaddr<const float>(M.values) + tl.blk0 * kBlock;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const f32x4 x = __builtin_nontemporal_load((const f32x4*)((const float*)M.values + e0 + 32 * q));
-                v[4 * q] = x.x; v[4 * q + 1] = x.y; v[4 * q + 2] = x.z; v[4 * q + 3] = x.w;
+                for (int q = 0; q < 4; ++q) {
+                    const f32x4 x = __builtin_nontemporal_load((gptr<const f32x4>)(vals_tile + tl.voff + 32u * q));
+                    v[4 * q] = x.x; v[4 * q + 1] = x.y; v[4 * q + 2] = x.z; v[4 * q + 3] = x.w;
+                }
             }
         }
     };
@@ -225,18 +257,18 @@ __device__ __forceinline__ void load_tile(const aw4_tensor& T, int64_t blk0, int
                 std::integral_constant<bool, In::kV2>());
 }
 
-template <int MK>
-__device__ __forceinline__ void encode_moment(const aw4_moment& M, const MomentTables& L, int64_t blk, int j,
-                                              bool active, const float (&m)[16], UpdEntry* upd, float* pre) {
-    if constexpr (MK == K_ANY) encode_block_any(M, L, blk, j, active, m, upd, pre);
-    else encode_block<MK>(M, L, blk, j, active, m, upd, pre);
+template <int MK, bool kNonNeg>
+__device__ __forceinline__ void encode_moment(const aw4_moment& M, const MomentTables& L, const TileLane& tl,
+                                              const float (&m)[16], UpdEntry* upd, float* pre) {
+    if constexpr (MK == K_ANY) encode_block_any<kNonNeg>(M, L, tl.blk0, tl.grp, tl.j, tl.active, m, upd, pre);
+    else encode_block<MK, kNonNeg>(M, L, tl.blk0, tl.grp, tl.j, tl.active, m, upd, pre);
 }
 
 // Decode, update and store one quarter (4 values) of this lane; the new moments go to m1/m2.
 template <int M1K, int M2K, int D, int DP, bool kGenericLerp>
 __device__ __forceinline__ void update_quarter(const aw4_tensor& T, int q, const TileInputs<M1K, M2K, D>& in,
-                                               const MomentTables& L1, const MomentTables& L2, bool active,
-                                               int64_t e0, bool vec, float (&m1)[16], float (&m2)[16]) {
+                                               const MomentTables& L1, const MomentTables& L2, const TileLane& tl,
+                                               float (&m1)[16], float (&m2)[16]) {
     using In = TileInputs<M1K, M2K, D>;
     constexpr int DC = D == D_ANY ? D_F32 : D;  // generic loads are already fp32 words
     float g[4], p[4], a[4], b[4];
@@ -272,65 +304,60 @@ __device__ __forceinline__ void update_quarter(const aw4_tensor& T, int q, const
         m1[4 * q + t] = a[t];
         m2[4 * q + t] = b[t];
     }
-    if (active) {
+    if (tl.active) {
+        const uint32_t off = tl.voff + 32u * q;
         if constexpr (D == D_ANY) {
-            if (T.param_dtype == D_F32) store_f32<D_F32>((void*)T.param, e0 + 32 * q, vec, p);
-            else if (T.param_dtype == D_BF16) store_f32<D_BF16>((void*)T.param, e0 + 32 * q, vec, p);
-            else store_f32<D_F16>((void*)T.param, e0 + 32 * q, vec, p);
+            const bool vec = (T.flags & AW4_TENSOR_VEC_ALIGNED) != 0;
+            const int64_t e = tl.blk0 * kBlock + off;
+            if (T.param_dtype == D_F32) store_f32<D_F32>(T.param, e, vec, p);
+            else if (T.param_dtype == D_BF16) store_f32<D_BF16>(T.param, e, vec, p);
+            else store_f32<D_F16>(T.param, e, vec, p);
         } else {
-            store_f32<D>((void*)T.param, e0 + 32 * q, vec, p);
+            store_f32<D>(tile_values<D>(T.param, tl.blk0), off, true, p);
         }
     }
 }
 
 template <int M1K, int M2K, int D, int DP>
 __device__ __forceinline__ void update_tile(const aw4_tensor& T, const TileInputs<M1K, M2K, D>& in,
-                                            const MomentTables& L1, const MomentTables& L2, bool active, int64_t e0,
-                                            bool vec, float (&m1)[16], float (&m2)[16]) {
+                                            const MomentTables& L1, const MomentTables& L2, const TileLane& tl,
+                                            float (&m1)[16], float (&m2)[16]) {
     if (__builtin_expect((T.flags & (AW4_TENSOR_LERP1_LARGE | AW4_TENSOR_LERP2_LARGE)) == 0, 1)) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-            update_quarter<M1K, M2K, D, DP, false>(T, q, in, L1, L2, active, e0, vec, m1, m2);
+        for (int q = 0; q < 4; ++q) update_quarter<M1K, M2K, D, DP, false>(T, q, in, L1, L2, tl, m1, m2);
     } else {
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-            update_quarter<M1K, M2K, D, DP, true>(T, q, in, L1, L2, active, e0, vec, m1, m2);
+        for (int q = 0; q < 4; ++q) update_quarter<M1K, M2K, D, DP, true>(T, q, in, L1, L2, tl, m1, m2);
     }
 }
 
 template <int M1K, int M2K, int D>
-__device__ __forceinline__ void compute_tile(const aw4_tensor& T, int64_t blk0, int lane,
+__device__ __forceinline__ void compute_tile(const aw4_tensor& T, const TileLane& tl,
                                              const TileInputs<M1K, M2K, D>& in, const MomentTables& L1,
                                              const MomentTables& L2, UpdEntry (*upd)[kPairs], float (*pre)[16]) {
-    const int j = lane & 7;
-    const int grp = lane >> 3;
-    const int64_t blk = blk0 + grp;
-    const bool active = blk < (T.numel >> 7);
-    const int64_t e0 = blk * kBlock + 4 * j;
-    const bool vec = (T.flags & AW4_TENSOR_VEC_ALIGNED) != 0;
-
     float m1[16], m2[16];
     if constexpr (D == D_ANY) {
-        if (T.param_dtype == D_F32) update_tile<M1K, M2K, D, D_F32>(T, in, L1, L2, active, e0, vec, m1, m2);
-        else if (T.param_dtype == D_BF16) update_tile<M1K, M2K, D, D_BF16>(T, in, L1, L2, active, e0, vec, m1, m2);
-        else update_tile<M1K, M2K, D, D_F16>(T, in, L1, L2, active, e0, vec, m1, m2);
+        if (T.param_dtype == D_F32) update_tile<M1K, M2K, D, D_F32>(T, in, L1, L2, tl, m1, m2);
+        else if (T.param_dtype == D_BF16) update_tile<M1K, M2K, D, D_BF16>(T, in, L1, L2, tl, m1, m2);
+        else update_tile<M1K, M2K, D, D_F16>(T, in, L1, L2, tl, m1, m2);
     } else {
-        update_tile<M1K, M2K, D, D>(T, in, L1, L2, active, e0, vec, m1, m2);
+        update_tile<M1K, M2K, D, D>(T, in, L1, L2, tl, m1, m2);
     }
-
-    auto finish = [&](const aw4_moment& M, const MomentTables& L, const float (&m)[16], auto kind) {
+    auto finish = [&](const aw4_moment& M, const MomentTables& L, const float (&m)[16], auto kind, auto nonneg) {
         constexpr int MK = decltype(kind)::value;
         if (moment_quantized<MK>(M)) {
-            if constexpr (MK != K_FP32) encode_moment<MK>(M, L, blk, j, active, m, upd[grp], pre[grp]);
-        } else if (active) {
+            if constexpr (MK != K_FP32)
+                encode_moment<MK, decltype(nonneg)::value>(M, L, tl, m, upd[tl.grp], pre[tl.grp]);
+        } else if (tl.active) {
+            const gptr<float> vals_tile = gaddr<float>(M.values) + tl.blk0 * kBlock;
 #pragma unroll
             for (int q = 0; q < 4; ++q)
                 __builtin_nontemporal_store(f32x4{m[4 * q], m[4 * q + 1], m[4 * q + 2], m[4 * q + 3]},
-                                            (f32x4*)((float*)M.values + e0 + 32 * q));
+                                            (gptr<f32x4>)(vals_tile + tl.voff + 32u * q));
         }
     };
-    finish(T.m1, L1, m1, std::integral_constant<int, M1K>());
-    finish(T.m2, L2, m2, std::integral_constant<int, M2K>());
+    finish(T.m1, L1, m1, std::integral_constant<int, M1K>(), std::false_type());
+    finish(T.m2, L2, m2, std::integral_constant<int, M2K>(), std::true_type());
 }
 
 // ---------------------------------------------------------------------------
@@ -338,19 +365,19 @@ __device__ __forceinline__ void compute_tile(const aw4_tensor& T, int64_t blk0, 
 // ---------------------------------------------------------------------------
 
 template <int D>
-__device__ __forceinline__ float load_value(const aw4_tensor& T, const void* base, int dtype, int64_t k) {
+__device__ __forceinline__ float load_value(const aw4_tensor& T, uint64_t base, int dtype, int64_t k) {
     const int dt = D == D_ANY ? dtype : D;
-    if (dt == D_F32) return ((const float*)base)[k];
-    const uint32_t h = ((const uint16_t*)base)[k];
+    if (dt == D_F32) return gaddr<const float>(base)[k];
+    const uint32_t h = gaddr<const uint16_t>(base)[k];
     return dt == D_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
 }
 
 template <int D>
 __device__ __forceinline__ void step_values_one(const aw4_tensor& T, int64_t k) {
-    float* v1 = (float*)T.m1.values;
-    float* v2 = (float*)T.m2.values;
-    const float g = load_value<D>(T, (const void*)T.grad, T.grad_dtype, k);
-    float p = load_value<D>(T, (const void*)T.param, T.param_dtype, k);
+    const gptr<float> v1 = gaddr<float>(T.m1.values);
+    const gptr<float> v2 = gaddr<float>(T.m2.values);
+    const float g = load_value<D>(T, T.grad, T.grad_dtype, k);
+    float p = load_value<D>(T, T.param, T.param_dtype, k);
     float a = v1[k], b = v2[k];
     const int lf = T.flags & (AW4_TENSOR_LERP1_LARGE | AW4_TENSOR_LERP2_LARGE);
     if (lf == 0) moments_update<false, false>(T, g, a, b);
@@ -360,13 +387,13 @@ __device__ __forceinline__ void step_values_one(const aw4_tensor& T, int64_t k) 
     const int dt = D == D_ANY ? T.param_dtype : D;
     if (dt == D_F32) {
         p = param_update<D_F32>(T, p, a, b);
-        ((float*)T.param)[k] = p;
+        gaddr<float>(T.param)[k] = p;
     } else if (dt == D_BF16) {
         p = param_update<D_BF16>(T, p, a, b);
-        ((uint16_t*)T.param)[k] = (uint16_t)f32_to_bf16(p);
+        gaddr<uint16_t>(T.param)[k] = (uint16_t)f32_to_bf16(p);
     } else {
         p = param_update<D_F16>(T, p, a, b);
-        ((uint16_t*)T.param)[k] = (uint16_t)f32_to_f16(p);
+        gaddr<uint16_t>(T.param)[k] = (uint16_t)f32_to_f16(p);
     }
     v1[k] = a;
     v2[k] = b;
@@ -386,12 +413,13 @@ __device__ void step_tile_values(const aw4_tensor& T, int64_t e_tile, int lane) 
 }
 
 // ---------------------------------------------------------------------------
-// The kernel: each wave walks a contiguous range of wave tiles; the inputs of the
-// next block-layout tile are loaded before the current tile is computed.
+// The kernel: each wave walks a contiguous range of wave tiles.  Latency is hidden by
+// occupancy (several waves per SIMD, each with a tile's loads in flight) rather than by
+// holding a second tile in registers, which would halve the waves that fit.
 // ---------------------------------------------------------------------------
 
 __device__ __forceinline__ bool values_only(const aw4_tensor& T) {
-    return !is_quantized(T.m1) && !is_quantized(T.m2);
+    return (!is_quantized(T.m1) && !is_quantized(T.m2)) || (T.numel & (kBlock - 1)) != 0;
 }
 
 template <int M1K, int M2K, int D, class LdsT>
@@ -412,41 +440,20 @@ __device__ __forceinline__ void run_tiles(const StepHeader* hdr, const LdsT& lds
         if (tile_start[mid] <= tile) lo = mid; else hi = mid - 1;
     }
     int ti = lo;
-
-    TileInputs<M1K, M2K, D> cur;
-    bool cur_loaded = false;
-    while (tile < end) {
+    for (; tile < end; ++tile) {
         while (tile >= tile_start[ti + 1]) ++ti;
         const aw4_tensor& T = tensors[ti];
         const int64_t local = tile - tile_start[ti];
-        if (values_only(T) || (T.numel & (kBlock - 1)) != 0) {
-            if constexpr (D == D_ANY) step_tile_values<D_ANY>(T, local * kWaveTile, lane);
-            else step_tile_values<D>(T, local * kWaveTile, lane);
-            ++tile;
-            cur_loaded = false;
+        if (values_only(T)) {
+            step_tile_values<D>(T, local * kWaveTile, lane);
             continue;
         }
-        if (!cur_loaded) load_tile(T, local * kBlocksPerWave, lane, cur);
-        // prefetch the next tile when it is a block-layout tile (specialised kernels only:
-        // the generic kernel's register budget has no room for a second tile)
-        constexpr bool kPrefetch = M1K != K_ANY && M2K != K_ANY && D != D_ANY;
-        const int64_t next = tile + 1;
-        TileInputs<M1K, M2K, D> nxt;
-        bool nxt_loaded = false;
-        if (kPrefetch && next < end) {
-            const int tn = next >= tile_start[ti + 1] ? ti + 1 : ti;
-            const aw4_tensor& N = tensors[tn];
-            if (!values_only(N) && (N.numel & (kBlock - 1)) == 0) {
-                load_tile(N, (next - tile_start[tn]) * kBlocksPerWave, lane, nxt);
-                nxt_loaded = true;
-            }
-        }
+        const TileLane tl = tile_lane(T, local * kBlocksPerWave, lane);
+        TileInputs<M1K, M2K, D> in;
+        load_tile(T, tl, in);
         const MomentTables L1 = lds_tables.moment(T.m1, 0);
         const MomentTables L2 = lds_tables.moment(T.m2, 1);
-        compute_tile(T, local * kBlocksPerWave, lane, cur, L1, L2, upd, pre);
-        cur = nxt;
-        cur_loaded = nxt_loaded;
-        tile = next;
+        compute_tile(T, tl, in, L1, L2, upd, pre);
     }
 }
 

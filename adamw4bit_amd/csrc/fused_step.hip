@@ -178,7 +178,9 @@ __global__ void __launch_bounds__(kThreads) quantize_kernel(const float* __restr
             if (active) v = *(const float4*)(values + blk * kBlock + 32 * q + 4 * j);
             m[4 * q] = v.x; m[4 * q + 1] = v.y; m[4 * q + 2] = v.z; m[4 * q + 3] = v.w;
         }
-        encode_block_any(M, L, blk, j, active, m, lds.scratch.upd[wslot][grp], lds.scratch.pre[wslot][grp]);
+        // stand-alone encodes accept any sign (a first moment or a caller's values)
+        encode_block_any<false>(M, L, tile * kBlocksPerWave, grp, j, active, m, lds.scratch.upd[wslot][grp],
+                                lds.scratch.pre[wslot][grp]);
     }
 }
 
@@ -197,10 +199,10 @@ __global__ void __launch_bounds__(kThreads) dequantize_kernel(aw4_moment M, int6
         const int64_t blk = tile * kBlocksPerWave + grp;
         if (blk >= nblocks) continue;
         uint32_t w[4];
-        const uint8_t* codes = (const uint8_t*)M.codes + blk * (kBlock / 2) + 2 * j;
+        const gptr<const uint8_t> codes = gaddr<const uint8_t>(M.codes) + blk * (kBlock / 2) + 2 * j;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) w[q] = *(const uint16_t*)(codes + 16 * q);
-        const float scale = ((const float*)M.scales)[blk];
+        for (int q = 0; q < 4; ++q) w[q] = *(gptr<const uint16_t>)(codes + 16 * q);
+        const float scale = gaddr<const float>(M.scales)[blk];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             float m[4];

@@ -130,14 +130,23 @@ def main():
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
     if args.copy_probe_gb > 0:
-        # A plain copy of known size: its FETCH_SIZE / WRITE_SIZE per dispatch calibrate the counters.
+        # A plain copy of known size: its FETCH_SIZE / WRITE_SIZE per dispatch calibrate the
+        # counters; copy and add timings give the streaming bandwidth torch's kernels reach.
         n = int(args.copy_probe_gb * 1e9) // 4
         src = torch.ones(n, device=device)
         dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(f"[bench] copy probe: 3 copies of {n * 4} bytes", file=sys.stderr, flush=True)
+        for name, fn, nbytes in (("copy", lambda: dst.copy_(src), 8 * n), ("add", lambda: dst.add_(src), 12 * n)):
+            fn()
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(5):
+                fn()
+            b.record()
+            torch.cuda.synchronize()
+            ms = a.elapsed_time(b) / 5
+            print(f"[bench] {name} probe: {nbytes} bytes in {ms:.3f} ms = {nbytes / ms / 1e6:.0f} GB/s",
+                  file=sys.stderr, flush=True)
         del src, dst
     shapes = CONFIGS[args.config]()
     numels = [math.prod(s) for s in shapes]
@@ -187,8 +196,9 @@ def main():
     achieved = algo_bytes / (mean_launch_ms * 1e-3) / 1e9
     ms_per_step = wall * 1e3 / args.steps
     value = total * len(recipes) * args.steps / wall / 1e9
-    print(f"[bench] timed {args.steps} steps in {wall:.3f} s; per-launch ms {per_recipe}",
-          file=sys.stderr, flush=True)
+    print(f"[bench] timed {args.steps} steps in {wall:.3f} s; per-launch ms mean "
+          f"{ {k: round(v, 3) for k, v in per_recipe.items()} } min "
+          f"{ {k: round(min(v), 3) for k, v in launch_ms.items()} }", file=sys.stderr, flush=True)
 
     baseline = None
     if not args.no_cpu_baseline:
