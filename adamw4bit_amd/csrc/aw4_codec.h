@@ -12,7 +12,8 @@
 namespace aw4 {
 
 constexpr int kBlock = AW4_BLOCK;
-constexpr int kPairs = 17;  // searchsorted-left results 0..16
+constexpr int kPairs = 17;          // searchsorted-left results 0..16
+constexpr int kBlocksPerWave = 8;   // a wave tile: 8 blocks, 8 lanes per block
 
 // Rounding kinds (AW4_ROUND_*) and "any": the kind is read from the descriptor at run time.
 enum : int { K_FP32 = AW4_ROUND_FP32, K_RTN = AW4_ROUND_RTN, K_SSR = AW4_ROUND_STATE_SR,
@@ -62,6 +63,23 @@ struct MomentTables {
     const PairEntry* pairs;
     const float2* dec;
     const LutEntry* lut;
+};
+
+// LDS scratch of one block's encode: update-SR tables of the block and the staging area
+// of its 64 code bytes (written a quarter at a time, stored to memory in one piece).
+struct BlockScratch {
+    UpdEntry* upd;      // kPairs entries (update-SR only)
+    float* pre;         // preconditioner of each of the 16 levels (update-SR only)
+    uint16_t* stage;    // 32 code words: word 8q + j is lane j's word of quarter q
+};
+
+// LDS scratch of one wave (8 blocks).
+struct WaveScratch {
+    UpdEntry upd[kBlocksPerWave][kPairs];
+    float pre[kBlocksPerWave][16];
+    uint16_t stage[kBlocksPerWave][32];
+
+    __device__ BlockScratch block(int grp) { return BlockScratch{upd[grp], pre[grp], stage[grp]}; }
 };
 
 // Bucket of an x >= -0 (second moments): only the magnitude half of the table.
@@ -136,8 +154,11 @@ __device__ __forceinline__ void draws4(const aw4_moment& M, int64_t blk0, uint32
 
 // Encode this lane's 16 values of block `blk` (_optimized_quantization.py:46-88):
 //   s = max(max|m|, 1e-12); x = m / s; codes by the rounding rule; [dyn4_nz floor]; [EDEN]
-// and store the 4 code words and (lane 0) the block scale.  Codes are produced a quarter
-// (4 values) at a time; the EDEN sums run in ATen's order (block_sum_cross).
+// and store the block's codes and (lane 0) its scale.  Codes are produced a quarter (4
+// values) at a time and staged in LDS, so that each lane then stores 8 contiguous code
+// bytes and a wave writes its tile's 512 code bytes as whole lines (16-byte pieces of a
+// block written a quarter at a time reach HBM as partial-sector writes).  The EDEN sums
+// run in ATen's order (block_sum_cross).
 //
 // kNonNeg: the values are >= +0 (second moments: a lerp of a non-negative state towards
 // g*g), so only the magnitude half of the lookup tables is indexed.
@@ -149,7 +170,7 @@ __device__ __forceinline__ void draws4(const aw4_moment& M, int64_t blk0, uint32
 // it), and its EDEN products vanish next to the block's |x| = 1 element.
 template <int KIND, bool kNonNeg>
 __device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTables& L, int64_t blk0, int grp, int j,
-                                             bool active, const float (&m)[16], UpdEntry* upd, float* pre) {
+                                             bool active, const float (&m)[16], BlockScratch sc) {
     uint32_t amax = 0u;
 #pragma unroll
     for (int i = 0; i < 16; ++i) amax = max(amax, f2u(m[i]) & 0x7fffffffu);  // NaN-propagating |m| max
@@ -160,11 +181,10 @@ __device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTa
     const bool eden = (M.flags & AW4_MOMENT_EDEN) != 0;
     const bool guards = (M.flags & AW4_MOMENT_GUARDS) != 0;
     const bool floor0 = (M.flags & AW4_MOMENT_ZERO_FLOOR) != 0;
-    if constexpr (KIND == K_USR) update_sr_tables(L, j, s, M.sr_bias, M.sr_bias_rcp, M.sr_eps, upd, pre);
+    if constexpr (KIND == K_USR) update_sr_tables(L, j, s, M.sr_bias, M.sr_bias_rcp, M.sr_eps, sc.upd, sc.pre);
+    wave_lds_sync();  // the stage's previous contents have been read
 
     float acc_xx[4] = {0.0f, 0.0f, 0.0f, 0.0f}, acc_xl[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    const gptr<uint8_t> codes = gaddr<uint8_t>(M.codes) + blk0 * (kBlock / 2);  // the tile's code bytes
-    const uint32_t coff = (uint32_t)(grp * (kBlock / 2) + 2 * j);
     const uint32_t voff = (uint32_t)(grp * kBlock + 4 * j);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -211,7 +231,7 @@ __device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTa
                 } else {
                     // P(lo) = (f(x) - f(b)) / max(f(a) - f(b), 1e-30), 1 unless b > a and f(a) > f(b),
                     // clamped; guards x<=a -> 1, x>=b -> 0 (_compiled_quantization.py:74-109).
-                    const UpdEntry ue = upd[idx];
+                    const UpdEntry ue = sc.upd[idx];
                     const float vh = clamp_min_nan(div_by_rcp(s * x[t], M.sr_bias, M.sr_bias_rcp), 0.0f);
                     const float fx = rcp_faithful(sqrt_faithful(vh) + M.sr_eps);
                     p = div_by_rcp(fx - ue.f_hi, ue.den, ue.den_rcp);
@@ -234,10 +254,14 @@ __device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTa
                 acc_xl[t] = acc_xl[t] + x[t] * lv[t];
             }
         }
-        if (active) {
-            const uint32_t w = code[0] | (code[1] << 4) | (code[2] << 8) | (code[3] << 12);
-            __builtin_nontemporal_store((uint16_t)w, (gptr<uint16_t>)(codes + coff + 16u * q));
-        }
+        sc.stage[8 * q + j] = (uint16_t)(code[0] | (code[1] << 4) | (code[2] << 8) | (code[3] << 12));
+    }
+    wave_lds_sync();
+    if (active) {
+        // lane j: code bytes 8j .. 8j+7 of its block; the tile's codes start at byte blk0 * 64
+        const u32x2 w = *(const u32x2*)(sc.stage + 4 * j);
+        const gptr<uint8_t> codes = gaddr<uint8_t>(M.codes) + blk0 * (kBlock / 2);
+        __builtin_nontemporal_store(w, (gptr<u32x2>)(codes + (uint32_t)(grp * (kBlock / 2) + 8 * j)));
     }
 
     float scale = s;
@@ -253,11 +277,10 @@ __device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTa
 // Runtime dispatch over the rounding kind (generic kernels).
 template <bool kNonNeg>
 __device__ __forceinline__ void encode_block_any(const aw4_moment& M, const MomentTables& L, int64_t blk0, int grp,
-                                                 int j, bool active, const float (&m)[16], UpdEntry* upd,
-                                                 float* pre) {
-    if (M.rounding == K_RTN) encode_block<K_RTN, kNonNeg>(M, L, blk0, grp, j, active, m, upd, pre);
-    else if (M.rounding == K_SSR) encode_block<K_SSR, kNonNeg>(M, L, blk0, grp, j, active, m, upd, pre);
-    else encode_block<K_USR, kNonNeg>(M, L, blk0, grp, j, active, m, upd, pre);
+                                                 int j, bool active, const float (&m)[16], BlockScratch sc) {
+    if (M.rounding == K_RTN) encode_block<K_RTN, kNonNeg>(M, L, blk0, grp, j, active, m, sc);
+    else if (M.rounding == K_SSR) encode_block<K_SSR, kNonNeg>(M, L, blk0, grp, j, active, m, sc);
+    else encode_block<K_USR, kNonNeg>(M, L, blk0, grp, j, active, m, sc);
 }
 
 }  // namespace aw4

@@ -9,7 +9,6 @@
 
 namespace aw4 {
 
-constexpr int kBlocksPerWave = 8;
 constexpr int kWaveTile = kBlock * kBlocksPerWave;  // 1024 values per wave tile
 constexpr int kThreads = 256;
 constexpr int kWavesPerGroup = kThreads / 64;
@@ -259,9 +258,9 @@ __device__ __forceinline__ void load_tile(const aw4_tensor& T, const TileLane& t
 
 template <int MK, bool kNonNeg>
 __device__ __forceinline__ void encode_moment(const aw4_moment& M, const MomentTables& L, const TileLane& tl,
-                                              const float (&m)[16], UpdEntry* upd, float* pre) {
-    if constexpr (MK == K_ANY) encode_block_any<kNonNeg>(M, L, tl.blk0, tl.grp, tl.j, tl.active, m, upd, pre);
-    else encode_block<MK, kNonNeg>(M, L, tl.blk0, tl.grp, tl.j, tl.active, m, upd, pre);
+                                              const float (&m)[16], BlockScratch sc) {
+    if constexpr (MK == K_ANY) encode_block_any<kNonNeg>(M, L, tl.blk0, tl.grp, tl.j, tl.active, m, sc);
+    else encode_block<MK, kNonNeg>(M, L, tl.blk0, tl.grp, tl.j, tl.active, m, sc);
 }
 
 // Decode, update and store one quarter (4 values) of this lane; the new moments go to m1/m2.
@@ -334,7 +333,7 @@ __device__ __forceinline__ void update_tile(const aw4_tensor& T, const TileInput
 template <int M1K, int M2K, int D>
 __device__ __forceinline__ void compute_tile(const aw4_tensor& T, const TileLane& tl,
                                              const TileInputs<M1K, M2K, D>& in, const MomentTables& L1,
-                                             const MomentTables& L2, UpdEntry (*upd)[kPairs], float (*pre)[16]) {
+                                             const MomentTables& L2, WaveScratch& ws) {
     float m1[16], m2[16];
     if constexpr (D == D_ANY) {
         if (T.param_dtype == D_F32) update_tile<M1K, M2K, D, D_F32>(T, in, L1, L2, tl, m1, m2);
@@ -347,7 +346,7 @@ __device__ __forceinline__ void compute_tile(const aw4_tensor& T, const TileLane
         constexpr int MK = decltype(kind)::value;
         if (moment_quantized<MK>(M)) {
             if constexpr (MK != K_FP32)
-                encode_moment<MK, decltype(nonneg)::value>(M, L, tl, m, upd[tl.grp], pre[tl.grp]);
+                encode_moment<MK, decltype(nonneg)::value>(M, L, tl, m, ws.block(tl.grp));
         } else if (tl.active) {
             const gptr<float> vals_tile = gaddr<float>(M.values) + tl.blk0 * kBlock;
 #pragma unroll
@@ -423,8 +422,7 @@ __device__ __forceinline__ bool values_only(const aw4_tensor& T) {
 }
 
 template <int M1K, int M2K, int D, class LdsT>
-__device__ __forceinline__ void run_tiles(const StepHeader* hdr, const LdsT& lds_tables, UpdEntry (*upd)[kPairs],
-                                          float (*pre)[16]) {
+__device__ __forceinline__ void run_tiles(const StepHeader* hdr, const LdsT& lds_tables, WaveScratch& ws) {
     const aw4_tensor* tensors = (const aw4_tensor*)(hdr + 1);
     const int64_t* tile_start = (const int64_t*)(tensors + hdr->count);
     const int lane = threadIdx.x & 63;
@@ -453,7 +451,7 @@ __device__ __forceinline__ void run_tiles(const StepHeader* hdr, const LdsT& lds
         load_tile(T, tl, in);
         const MomentTables L1 = lds_tables.moment(T.m1, 0);
         const MomentTables L2 = lds_tables.moment(T.m2, 1);
-        compute_tile(T, tl, in, L1, L2, upd, pre);
+        compute_tile(T, tl, in, L1, L2, ws);
     }
 }
 

@@ -75,12 +75,6 @@ __host__ __device__ inline int lut_id_of(int rounding, int codebook, int flags) 
 // LDS layouts
 // ---------------------------------------------------------------------------
 
-// Per-wave scratch of the update-SR tables (unused by kernels without update-SR).
-struct UpdScratch {
-    UpdEntry upd[kWavesPerGroup][kBlocksPerWave][kPairs];
-    float pre[kWavesPerGroup][kBlocksPerWave][16];
-};
-
 // Specialised kernels: the tables of the one codebook each moment uses.
 template <bool kUpd>
 struct LdsSlots {
@@ -88,7 +82,7 @@ struct LdsSlots {
     PairEntry pairs[2][kPairs];
     float2 dec[2][256];
     LutEntry lut[2][AW4_LUT_ENTRIES];
-    UpdScratch scratch;
+    WaveScratch scratch[kWavesPerGroup];
 
     __device__ MomentTables moment(const aw4_moment&, int which) const {
         return MomentTables{cb[which], pairs[which], dec[which], lut[which]};
@@ -109,7 +103,7 @@ struct LdsSlots {
 // Generic kernels: every table.
 struct LdsAll {
     Tables t;
-    UpdScratch scratch;
+    WaveScratch scratch[kWavesPerGroup];
 
     __device__ MomentTables moment(const aw4_moment& m, int) const {
         const int cbid = m.rounding == AW4_ROUND_FP32 ? 0 : m.codebook;
@@ -128,17 +122,21 @@ template <int M1K, int M2K, int D>
 struct KernelTraits {
     static constexpr bool kGeneric = M1K == K_ANY || M2K == K_ANY || D == D_ANY;
     static constexpr bool kUpd = M1K == K_USR || M2K == K_USR || M1K == K_ANY || M2K == K_ANY;
+    // Waves per SIMD the register allocation must allow (512 VGPRs per lane, granule 8):
+    // 5 keeps the round-to-nearest kernels at <= 96 VGPRs.
+    static constexpr int kMinWaves = (!kGeneric && !kUpd) ? 5 : 1;
     using Lds = typename std::conditional<kGeneric, LdsAll, LdsSlots<kUpd>>::type;
 };
 
 template <int M1K, int M2K, int D>
-__global__ void __launch_bounds__(kThreads) step_kernel(const StepHeader* __restrict__ hdr,
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(KernelTraits<M1K, M2K, D>::kMinWaves)))
+step_kernel(const StepHeader* __restrict__ hdr,
                                                          const Tables* __restrict__ tables) {
     using Lds = typename KernelTraits<M1K, M2K, D>::Lds;
     __shared__ Lds lds;
     lds.load(tables, hdr);
     const int wslot = threadIdx.x >> 6;
-    run_tiles<M1K, M2K, D>(hdr, lds, lds.scratch.upd[wslot], lds.scratch.pre[wslot]);
+    run_tiles<M1K, M2K, D>(hdr, lds, lds.scratch[wslot]);
 }
 
 // The instantiated kernels; the host picks the first whose combination matches the table.
@@ -179,8 +177,7 @@ __global__ void __launch_bounds__(kThreads) quantize_kernel(const float* __restr
             m[4 * q] = v.x; m[4 * q + 1] = v.y; m[4 * q + 2] = v.z; m[4 * q + 3] = v.w;
         }
         // stand-alone encodes accept any sign (a first moment or a caller's values)
-        encode_block_any<false>(M, L, tile * kBlocksPerWave, grp, j, active, m, lds.scratch.upd[wslot][grp],
-                                lds.scratch.pre[wslot][grp]);
+        encode_block_any<false>(M, L, tile * kBlocksPerWave, grp, j, active, m, lds.scratch[wslot].block(grp));
     }
 }
 
