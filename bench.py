@@ -8,10 +8,12 @@ log-normal(-7, 1) magnitudes.  One timed step = one ZE-EDEN step followed by one
 ZIP-SR step over all tensors (each recipe keeps its own moment state), i.e. two
 fused launches.
 
-Prints one JSON line: Gelem/s over the timed steps, the HBM roofline of the fused
-kernel (algorithmic bytes per launch / launch time, HIP events on the launch
-stream) and a CPU baseline: the oracle's restatement of the reference's eager
-chunk update timed on this host on a bounded sample.
+Prints one JSON line: Gelem/s over the timed steps, the HBM roofline of the dominant
+fused kernel (the recipe with the longest launches: algorithmic bytes per launch /
+mean launch time, HIP events recorded on the launch stream; measured HBM traffic per
+launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary of the workload)
+and a CPU baseline: the oracle's restatement of the reference's eager chunk update
+timed on this host on a bounded sample.
 """
 
 from __future__ import annotations
@@ -25,6 +27,8 @@ import sys
 import time
 
 HBM_PEAK_GBS = 8000.0
+HERE = os.path.dirname(os.path.abspath(__file__))
+RECIPE_KERNELS = {"ZE-EDEN": "step_kernel<RTN, RTN, F32>", "ZIP-SR": "step_kernel<RTN, UPDATE_SR, F32>"}
 
 
 def llama3_8b_shapes():
@@ -104,6 +108,22 @@ def cpu_baseline(seconds_target: float = 12.0):
     return {"value": n / per_step / 1e9, "unit": "Gelem/s", "cores": torch.get_num_threads(), "kind": "port",
             "sample": f"oracle ZE-EDEN eager chunk update, fp32 4096x4096 (16.8M values), median of {len(times)} "
                       f"steps, {per_step * 1e3:.1f} ms/step, {torch.get_num_threads()} threads"}
+
+
+def measured_traffic(config: str):
+    """HBM bytes per launch of each recipe's kernel from the committed rocprofv3 summary of
+    this workload (TCC FETCH_SIZE / WRITE_SIZE, scaled by a device copy of known size);
+    None where no summary covers the workload."""
+    path = os.path.join(HERE, "profiles", f"step_kernel_{config}_fp32_hbm_traffic.txt")
+    if not os.path.exists(path):
+        return None, None
+    out = {}
+    with open(path) as f:
+        for line in f:
+            if line.startswith("traffic_bytes_per_launch "):
+                _, recipe, value = line.split()
+                out[recipe] = float(value)
+    return out, os.path.relpath(path, HERE)
 
 
 def main():
@@ -192,8 +212,10 @@ def main():
     wall = time.perf_counter() - t0
     launch_ms = {name: [a.elapsed_time(b) for a, b in ev] for name, ev in events.items()}
     per_recipe = {name: statistics.mean(v) for name, v in launch_ms.items()}
-    mean_launch_ms = statistics.mean(x for v in launch_ms.values() for x in v)
-    achieved = algo_bytes / (mean_launch_ms * 1e-3) / 1e9
+    # The dominant kernel is the recipe with the longest launches; its roofline is reported.
+    dominant = max(per_recipe, key=per_recipe.get)
+    achieved = algo_bytes / (per_recipe[dominant] * 1e-3) / 1e9
+    traffic, traffic_source = measured_traffic(args.config)
     ms_per_step = wall * 1e3 / args.steps
     value = total * len(recipes) * args.steps / wall / 1e9
     print(f"[bench] timed {args.steps} steps in {wall:.3f} s; per-launch ms mean "
@@ -224,15 +246,19 @@ def main():
             "tensors": len(shapes), "values": total, "recipes": [n for n, _ in recipes],
             "launch_ms": {k: round(v, 4) for k, v in per_recipe.items()},
             "gelem_s_per_recipe": {k: round(total / (v * 1e-3) / 1e9, 2) for k, v in per_recipe.items()},
+            "hbm_frac_per_recipe": {k: round(algo_bytes / (v * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+                                    for k, v in per_recipe.items()},
             "algorithmic_gb_per_launch": round(algo_bytes / 1e9, 4),
         },
         "roofline": {
             "bound": "hbm",
+            "kernel": f"{RECIPE_KERNELS.get(dominant, dominant)} ({dominant})",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": (round(traffic[dominant]) if traffic and dominant in traffic else None),
+            "traffic_source": traffic_source,
         },
         "cpu_baseline": baseline,
     }
