@@ -10,6 +10,7 @@
 namespace aw4 {
 
 constexpr int kWaveTile = kBlock * kBlocksPerWave;  // 1024 values per wave tile
+constexpr int kTilesPerWave = 4;                    // consecutive wave tiles one wave processes
 constexpr int kThreads = 256;
 constexpr int kWavesPerGroup = kThreads / 64;
 
@@ -412,9 +413,10 @@ __device__ void step_tile_values(const aw4_tensor& T, int64_t e_tile, int lane) 
 }
 
 // ---------------------------------------------------------------------------
-// The kernel: each wave walks a contiguous range of wave tiles.  Latency is hidden by
-// occupancy (several waves per SIMD, each with a tile's loads in flight) rather than by
-// holding a second tile in registers, which would halve the waves that fit.
+// The kernel: each wave processes kTilesPerWave consecutive wave tiles (the header's
+// tiles_per_wave); the grid covers every tile.  Latency is hidden by occupancy (several
+// waves per SIMD, each with a tile's loads in flight) rather than by holding a second
+// tile in registers, which would halve the waves that fit.
 // ---------------------------------------------------------------------------
 
 __device__ __forceinline__ bool values_only(const aw4_tensor& T) {
@@ -426,7 +428,7 @@ __device__ __forceinline__ void run_tiles(const StepHeader* hdr, const LdsT& lds
     const aw4_tensor* tensors = (const aw4_tensor*)(hdr + 1);
     const int64_t* tile_start = (const int64_t*)(tensors + hdr->count);
     const int lane = threadIdx.x & 63;
-    const int64_t wave = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * kWavesPerGroup + (threadIdx.x >> 6)));
+    const int64_t wave = (int64_t)blockIdx.x * kWavesPerGroup + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t total = hdr->total_tiles;
     int64_t tile = wave * hdr->tiles_per_wave;
     const int64_t end = min(tile + hdr->tiles_per_wave, total);

@@ -7,11 +7,11 @@
 //     every parameter/gradient access is a 4-value vector (16 B for fp32) and each
 //     quarter q of a block is one contiguous 128 B segment across the 8 lanes.  The same
 //     split makes the reference's per-block sum order (ATen's 8-lane x 4-accumulator
-//     reduction) mostly lane-local (block_sum_aten in aw4_math.h).
-//   * Tiles of all tensors form one index space; each wave walks a contiguous range of
-//     it (grid sized to fill the machine at the kernel's occupancy), loading the next
-//     tile while it computes the current one.  One launch covers every parameter of
-//     the step, fp32-state tensors included.
+//     reduction) mostly lane-local (block_sum_cross in aw4_math.h).
+//   * Tiles of all tensors form one index space; each wave takes 4 consecutive tiles and
+//     the grid covers all of them, so the hardware dispatcher keeps the tiles in flight a
+//     narrow moving window of memory.  One launch covers every parameter of the step,
+//     fp32-state tensors included.
 //   * Kernels are specialised on (m1 rounding kind, m2 rounding kind, parameter dtype);
 //     a launch table whose tensors share one such combination (every recipe) runs the
 //     specialised kernel, any other table the generic one.
@@ -365,7 +365,6 @@ constexpr int kSlots = 4;
 struct DeviceState {
     Tables* tables = nullptr;
     int num_cus = 0;
-    int groups_per_cu[kNumVariants] = {};
     StagingSlot slots[kSlots];
     int next = 0;
 };
@@ -383,11 +382,6 @@ int device_state(DeviceState** out) {
         hipDeviceProp_t prop;
         AW4_HIP_CHECK(hipGetDeviceProperties(&prop, dev));
         ds.num_cus = prop.multiProcessorCount;
-        for (int v = 0; v < kNumVariants; ++v) {
-            int n = 0;
-            AW4_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kVariants[v].fn, kThreads, 0));
-            ds.groups_per_cu[v] = n > 0 ? n : 1;
-        }
         Tables* d = nullptr;
         AW4_HIP_CHECK(hipMalloc((void**)&d, sizeof(Tables)));
         hipError_t e = hipMemcpy(d, &ht.t, sizeof(Tables), hipMemcpyHostToDevice);
@@ -540,12 +534,15 @@ int aw4_fused_step(const aw4_tensor* tensors, int32_t count, void* stream) {
     StepHeader* h = (StepHeader*)slot.host;
     memset(h, 0, sizeof(*h));
     const int variant = select_variant(tensors, count, h);
-    // Enough waves to fill every CU at the kernel's occupancy, no more than the work.
-    const int64_t capacity = (int64_t)ds->num_cus * ds->groups_per_cu[variant] * kWavesPerGroup;
-    int64_t waves = total < capacity ? total : capacity;
-    const int64_t per_wave = (total + waves - 1) / waves;
-    waves = (total + per_wave - 1) / per_wave;
+    // A few tiles per wave and a grid covering all of them: the hardware dispatcher hands
+    // each free slot the next workgroup, so the tiles in flight stay a narrow, moving window
+    // of the index space (HBM page locality) and no CU waits on a static share at the end.
+    // Measured on MI355X against persistent grids of contiguous per-wave ranges, which
+    // stream from thousands of far-apart addresses at once and leave a load-imbalance tail.
+    const int64_t per_wave = kTilesPerWave;
+    const int64_t waves = (total + per_wave - 1) / per_wave;
     const int64_t groups = (waves + kWavesPerGroup - 1) / kWavesPerGroup;
+    if (groups > 0x7fffffff) return set_error(AW4_EINVAL, "aw4_fused_step: %lld tiles exceed one launch", (long long)total);
     h->count = count;
     h->total_tiles = total;
     h->tiles_per_wave = per_wave;
