@@ -19,6 +19,21 @@ constexpr int kBlocksPerWave = 8;   // a wave tile: 8 blocks, 8 lanes per block
 enum : int { K_FP32 = AW4_ROUND_FP32, K_RTN = AW4_ROUND_RTN, K_SSR = AW4_ROUND_STATE_SR,
              K_USR = AW4_ROUND_UPDATE_SR, K_ANY = 7 };
 
+// A moment's compile-time specification: its rounding kind and the AW4_MOMENT_* flags a
+// specialised kernel is built for (zero floor, EDEN, guards; external draws stay a run-time
+// choice).  kFlagsAtRunTime makes the encoder read the flags from the descriptor instead.
+constexpr int kFlagsAtRunTime = 0x80;
+constexpr int mspec(int kind, int flags = 0) { return kind | (flags << 4); }
+constexpr int kind_of(int spec) { return spec & 15; }
+constexpr int flags_of(int spec) { return spec >> 4; }
+// The flags that change what a kind computes (round-to-nearest: EDEN; the zero floor of
+// round-to-nearest lives in its lookup table).
+constexpr int spec_flags_mask(int kind) {
+    return kind == K_FP32 ? 0
+         : kind == K_RTN ? AW4_MOMENT_EDEN
+                         : (AW4_MOMENT_EDEN | AW4_MOMENT_GUARDS | AW4_MOMENT_ZERO_FLOOR);
+}
+
 // Lookup-table ids (aw4_encode_tables): round-to-nearest tables, then level-count tables.
 constexpr int kLutRtn[AW4_NUM_CODEBOOKS] = {0, 1, 2, 3, 4};
 constexpr int kLutRtnDyn4Floor = 5;
@@ -43,10 +58,10 @@ struct __align__(16) PairEntry {
 
 // Per-block update-SR quantities for each searchsorted index (update_sr_tables()).
 struct __align__(16) UpdEntry {
-    float f_hi;   // preconditioner at the upper level
-    float den;    // max(f(lo) - f(hi), 1e-30)
-    float den_rcp;
-    float valid;  // 1 when (b > a) & (f(lo) - f(hi) > 0), else 0
+    float f_hi;     // preconditioner at the upper level
+    float den;      // max(f(lo) - f(hi), 1e-30)
+    float den_rcp;  // RN(1 / den) where the interval is valid ((b > a) & (f(lo) - f(hi) > 0)), else -1
+    float b;        // the upper level
 };
 
 // All tables of all codebooks, built on the host and kept in device memory.
@@ -110,8 +125,8 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 // Per-block update-SR tables (_compiled_quantization.py:74-109): for every
-// searchsorted index i, f(hi), max(f(lo) - f(hi), 1e-30), its reciprocal and the
-// validity flag, with f(l) = 1 / (sqrt(max((s * l) / bias, 0)) + eps).
+// searchsorted index i, f(hi), max(f(lo) - f(hi), 1e-30), its reciprocal (negative
+// marks an invalid interval) and the upper level, with f(l) = 1 / (sqrt(max((s * l) / bias, 0)) + eps).
 __device__ __forceinline__ void update_sr_tables(const MomentTables& L, int j, float s, float bias, float bias_rcp,
                                                  float eps, UpdEntry* upd, float* pre) {
 #pragma unroll
@@ -132,8 +147,8 @@ __device__ __forceinline__ void update_sr_tables(const MomentTables& L, int j, f
             UpdEntry e;
             e.f_hi = fhi;
             e.den = dc;
-            e.den_rcp = 1.0f / dc;
-            e.valid = (pe.b > pe.a && den > 0.0f) ? 1.0f : 0.0f;
+            e.den_rcp = (pe.b > pe.a && den > 0.0f) ? 1.0f / dc : -1.0f;
+            e.b = pe.b;
             upd[i] = e;
         }
     }
@@ -168,7 +183,7 @@ __device__ __forceinline__ void draws4(const aw4_moment& M, int64_t blk0, uint32
 // rounding table resolves [-2^-10, 2^-10] to one code or to the level-0 threshold at the
 // smallest subnormal, the preconditioner of such an x equals the one of 0 (eps absorbs
 // it), and its EDEN products vanish next to the block's |x| = 1 element.
-template <int KIND, bool kNonNeg>
+template <int SPEC, bool kNonNeg>
 __device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTables& L, int64_t blk0, int grp, int j,
                                              bool active, const float (&m)[16], BlockScratch sc) {
     uint32_t amax = 0u;
@@ -178,9 +193,12 @@ __device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTa
     const float s = u2f(max(amax, 0x2B8CBCCCu));  // max(absmax, fp32(1e-12))
     const bool fast = s < 0x1p125f;                // otherwise huge, infinite or NaN: IEEE division
     const float y = 1.0f / s;
-    const bool eden = (M.flags & AW4_MOMENT_EDEN) != 0;
-    const bool guards = (M.flags & AW4_MOMENT_GUARDS) != 0;
-    const bool floor0 = (M.flags & AW4_MOMENT_ZERO_FLOOR) != 0;
+    constexpr int KIND = kind_of(SPEC), MF = flags_of(SPEC);
+    constexpr bool kDyn = (MF & kFlagsAtRunTime) != 0;
+    const int flags = kDyn ? M.flags : MF;
+    const bool eden = (flags & AW4_MOMENT_EDEN) != 0;
+    const bool guards = (flags & AW4_MOMENT_GUARDS) != 0;
+    const bool floor0 = (flags & AW4_MOMENT_ZERO_FLOOR) != 0;
     if constexpr (KIND == K_USR) update_sr_tables(L, j, s, M.sr_bias, M.sr_bias_rcp, M.sr_eps, sc.upd, sc.pre);
     wave_lds_sync();  // the stage's previous contents have been read
 
@@ -210,39 +228,36 @@ __device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTa
         } else {
             float u[4];
             draws4(M, blk0, voff + 32u * q, active, u);
+            // Both rules pick level lo = max(idx - 1, 0) or hi = min(idx, 15), idx = number of levels
+            // below x.  Since u is in [0, 1), u < clamp(P, 0, 1) == u < P for every P (NaN included),
+            // so the clamps of the reference never change a code and the guards become masks.
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const LutEntry le = L.lut[kNonNeg ? lut_bucket_unsigned(x[t]) : lut_bucket_signed(x[t])];
-                const uint32_t idx = le.base + (x[t] >= le.thr ? 1u : 0u);
-                const PairEntry pe = L.pairs[idx];
-                float p;
+                const int idx = (int)le.base + (x[t] >= le.thr ? 1 : 0);
+                bool lower;
                 if constexpr (KIND == K_SSR) {
-                    // P(hi) = (x - a) / max(b - a, 1e-12), 0 where b == a, clamped; guards x<=a -> 0,
-                    // x>=b -> 1 (_compiled_quantization.py:60-71); code = u < P ? hi : lo.
+                    // P(hi) = (x - a) / max(b - a, 1e-12), 0 where b == a (there lo == hi); guards
+                    // x <= a -> lo, x >= b -> hi (_compiled_quantization.py:60-71).
+                    const PairEntry pe = L.pairs[idx];
                     const float width = pe.b - pe.a;
-                    p = div_by_rcp(x[t] - pe.a, width < 1e-12f ? 1e-12f : width, pe.width_rcp);
-                    p = width > 0.0f ? p : 0.0f;
-                    p = clamp01_nan(p);
-                    if (guards) {
-                        p = x[t] >= pe.b ? 1.0f : p;
-                        p = x[t] <= pe.a ? 0.0f : p;
-                    }
-                    code[t] = u[t] < p ? (pe.lohi >> 8) : (pe.lohi & 0xffu);
+                    const float p = div_by_rcp(x[t] - pe.a, width < 1e-12f ? 1e-12f : width, pe.width_rcp);
+                    bool upper = u[t] < p;
+                    if (guards) upper = (upper || x[t] >= pe.b) && !(x[t] <= pe.a);
+                    lower = !upper;
                 } else {
-                    // P(lo) = (f(x) - f(b)) / max(f(a) - f(b), 1e-30), 1 unless b > a and f(a) > f(b),
-                    // clamped; guards x<=a -> 1, x>=b -> 0 (_compiled_quantization.py:74-109).
+                    // P(lo) = (f(x) - f(b)) / max(f(a) - f(b), 1e-30), 1 on invalid intervals; guards
+                    // x <= a -> lo, x >= b -> hi (_compiled_quantization.py:74-109).  x <= a holds
+                    // exactly when no level is below x (idx == 0).  For values >= +0 the clamp of
+                    // (s * x) / bias at 0 is the identity.
                     const UpdEntry ue = sc.upd[idx];
-                    const float vh = clamp_min_nan(div_by_rcp(s * x[t], M.sr_bias, M.sr_bias_rcp), 0.0f);
-                    const float fx = rcp_faithful(sqrt_faithful(vh) + M.sr_eps);
-                    p = div_by_rcp(fx - ue.f_hi, ue.den, ue.den_rcp);
-                    p = ue.valid != 0.0f ? p : 1.0f;
-                    p = clamp01_nan(p);
-                    if (guards) {
-                        p = x[t] >= pe.b ? 0.0f : p;
-                        p = x[t] <= pe.a ? 1.0f : p;
-                    }
-                    code[t] = u[t] < p ? (pe.lohi & 0xffu) : (pe.lohi >> 8);
+                    const float v = div_by_rcp(s * x[t], M.sr_bias, M.sr_bias_rcp);
+                    const float fx = rcp_faithful(sqrt_faithful(kNonNeg ? v : clamp_min_nan(v, 0.0f)) + M.sr_eps);
+                    const float p = div_by_rcp(fx - ue.f_hi, ue.den, ue.den_rcp);
+                    lower = !(ue.den_rcp > 0.0f) || u[t] < p;
+                    if (guards) lower = (lower && !(x[t] >= ue.b)) || idx == 0;
                 }
+                code[t] = (uint32_t)min(max(idx - (lower ? 1 : 0), 0), 15);
                 if (floor0) code[t] = max(code[t], 1u);
                 lv[t] = eden ? L.cb[code[t]] : 0.0f;
             }
@@ -278,9 +293,9 @@ __device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTa
 template <bool kNonNeg>
 __device__ __forceinline__ void encode_block_any(const aw4_moment& M, const MomentTables& L, int64_t blk0, int grp,
                                                  int j, bool active, const float (&m)[16], BlockScratch sc) {
-    if (M.rounding == K_RTN) encode_block<K_RTN, kNonNeg>(M, L, blk0, grp, j, active, m, sc);
-    else if (M.rounding == K_SSR) encode_block<K_SSR, kNonNeg>(M, L, blk0, grp, j, active, m, sc);
-    else encode_block<K_USR, kNonNeg>(M, L, blk0, grp, j, active, m, sc);
+    if (M.rounding == K_RTN) encode_block<mspec(K_RTN, kFlagsAtRunTime), kNonNeg>(M, L, blk0, grp, j, active, m, sc);
+    else if (M.rounding == K_SSR) encode_block<mspec(K_SSR, kFlagsAtRunTime), kNonNeg>(M, L, blk0, grp, j, active, m, sc);
+    else encode_block<mspec(K_USR, kFlagsAtRunTime), kNonNeg>(M, L, blk0, grp, j, active, m, sc);
 }
 
 }  // namespace aw4

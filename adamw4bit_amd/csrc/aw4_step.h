@@ -149,8 +149,9 @@ __device__ __forceinline__ float param_update(const aw4_tensor& T, float p, floa
 template <int M1K, int M2K, int D>
 struct TileInputs {
     static constexpr int kW = (D == D_F32 || D == D_ANY) ? 4 : 2;  // words per 4 values
-    static constexpr bool kQ1 = M1K != K_FP32, kV1 = M1K == K_FP32 || M1K == K_ANY;
-    static constexpr bool kQ2 = M2K != K_FP32, kV2 = M2K == K_FP32 || M2K == K_ANY;
+    static constexpr int K1 = kind_of(M1K), K2 = kind_of(M2K);
+    static constexpr bool kQ1 = K1 != K_FP32, kV1 = K1 == K_FP32 || K1 == K_ANY;
+    static constexpr bool kQ2 = K2 != K_FP32, kV2 = K2 == K_FP32 || K2 == K_ANY;
     uint32_t g[4 * kW];
     uint32_t p[4 * kW];
     uint32_t c1[kQ1 ? 4 : 1], c2[kQ2 ? 4 : 1];
@@ -162,8 +163,8 @@ __device__ __forceinline__ bool is_quantized(const aw4_moment& m) { return m.rou
 
 template <int MK>
 __device__ __forceinline__ bool moment_quantized(const aw4_moment& m) {
-    if constexpr (MK == K_ANY) return is_quantized(m);
-    else return MK != K_FP32;
+    if constexpr (kind_of(MK) == K_ANY) return is_quantized(m);
+    else return kind_of(MK) != K_FP32;
 }
 
 // Addressing of one lane within a wave tile: the tile's base pointers are wave-uniform
@@ -260,7 +261,7 @@ __device__ __forceinline__ void load_tile(const aw4_tensor& T, const TileLane& t
 template <int MK, bool kNonNeg>
 __device__ __forceinline__ void encode_moment(const aw4_moment& M, const MomentTables& L, const TileLane& tl,
                                               const float (&m)[16], BlockScratch sc) {
-    if constexpr (MK == K_ANY) encode_block_any<kNonNeg>(M, L, tl.blk0, tl.grp, tl.j, tl.active, m, sc);
+    if constexpr (kind_of(MK) == K_ANY) encode_block_any<kNonNeg>(M, L, tl.blk0, tl.grp, tl.j, tl.active, m, sc);
     else encode_block<MK, kNonNeg>(M, L, tl.blk0, tl.grp, tl.j, tl.active, m, sc);
 }
 
@@ -346,7 +347,7 @@ __device__ __forceinline__ void compute_tile(const aw4_tensor& T, const TileLane
     auto finish = [&](const aw4_moment& M, const MomentTables& L, const float (&m)[16], auto kind, auto nonneg) {
         constexpr int MK = decltype(kind)::value;
         if (moment_quantized<MK>(M)) {
-            if constexpr (MK != K_FP32)
+            if constexpr (kind_of(MK) != K_FP32)
                 encode_moment<MK, decltype(nonneg)::value>(M, L, tl, m, ws.block(tl.grp));
         } else if (tl.active) {
             const gptr<float> vals_tile = gaddr<float>(M.values) + tl.blk0 * kBlock;

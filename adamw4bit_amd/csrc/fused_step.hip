@@ -120,8 +120,9 @@ struct LdsAll {
 
 template <int M1K, int M2K, int D>
 struct KernelTraits {
-    static constexpr bool kGeneric = M1K == K_ANY || M2K == K_ANY || D == D_ANY;
-    static constexpr bool kUpd = M1K == K_USR || M2K == K_USR || M1K == K_ANY || M2K == K_ANY;
+    static constexpr int K1 = kind_of(M1K), K2 = kind_of(M2K);
+    static constexpr bool kGeneric = K1 == K_ANY || K2 == K_ANY || D == D_ANY;
+    static constexpr bool kUpd = K1 == K_USR || K2 == K_USR || K1 == K_ANY || K2 == K_ANY;
     // Waves per SIMD the register allocation must allow (512 VGPRs per lane, granule 8):
     // 5 keeps the round-to-nearest kernels at <= 96 VGPRs.
     static constexpr int kMinWaves = (!kGeneric && !kUpd) ? 5 : 1;
@@ -139,16 +140,21 @@ step_kernel(const StepHeader* __restrict__ hdr,
     run_tiles<M1K, M2K, D>(hdr, lds, lds.scratch[wslot]);
 }
 
-// The instantiated kernels; the host picks the first whose combination matches the table.
+// The instantiated kernels; the host picks the first whose moment specs and dtype match
+// every tensor of the table.  ZE-EDEN: NF4 round-to-nearest m1, Dyn4 round-to-nearest m2
+// with EDEN; ZIP-SR: NF4 round-to-nearest m1, Dyn4 update-SR m2 with the optimized path's
+// exact-level guards.
+constexpr int kRtn = mspec(K_RTN), kRtnEden = mspec(K_RTN, AW4_MOMENT_EDEN);
+constexpr int kUsrGuarded = mspec(K_USR, AW4_MOMENT_GUARDS);
 struct KernelVariant {
     int m1, m2, dtype;
     const void* fn;
 };
 const KernelVariant kVariants[] = {
-    {K_RTN, K_RTN, D_F32, (const void*)&step_kernel<K_RTN, K_RTN, D_F32>},
-    {K_RTN, K_USR, D_F32, (const void*)&step_kernel<K_RTN, K_USR, D_F32>},
-    {K_RTN, K_RTN, D_BF16, (const void*)&step_kernel<K_RTN, K_RTN, D_BF16>},
-    {K_RTN, K_USR, D_BF16, (const void*)&step_kernel<K_RTN, K_USR, D_BF16>},
+    {kRtn, kRtnEden, D_F32, (const void*)&step_kernel<kRtn, kRtnEden, D_F32>},
+    {kRtn, kUsrGuarded, D_F32, (const void*)&step_kernel<kRtn, kUsrGuarded, D_F32>},
+    {kRtn, kRtnEden, D_BF16, (const void*)&step_kernel<kRtn, kRtnEden, D_BF16>},
+    {kRtn, kUsrGuarded, D_BF16, (const void*)&step_kernel<kRtn, kUsrGuarded, D_BF16>},
     {K_ANY, K_ANY, D_ANY, (const void*)&step_kernel<K_ANY, K_ANY, D_ANY>},
 };
 constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
@@ -457,10 +463,12 @@ int select_variant(const aw4_tensor* ts, int32_t count, StepHeader* h) {
         if (dtype < 0) dtype = t.param_dtype;
         else if (dtype != t.param_dtype) uniform = false;
         if (host_values_only(t)) continue;
-        const int k1 = t.m1.rounding, k2 = t.m2.rounding;
-        const int c1 = k1 == AW4_ROUND_FP32 ? -1 : t.m1.codebook, c2 = k2 == AW4_ROUND_FP32 ? -1 : t.m2.codebook;
-        const int l1 = k1 == AW4_ROUND_FP32 ? -1 : lut_id_of(k1, c1, t.m1.flags);
-        const int l2 = k2 == AW4_ROUND_FP32 ? -1 : lut_id_of(k2, c2, t.m2.flags);
+        const int k1 = mspec(t.m1.rounding, t.m1.flags & spec_flags_mask(t.m1.rounding));
+        const int k2 = mspec(t.m2.rounding, t.m2.flags & spec_flags_mask(t.m2.rounding));
+        const bool f1 = t.m1.rounding == AW4_ROUND_FP32, f2 = t.m2.rounding == AW4_ROUND_FP32;
+        const int c1 = f1 ? -1 : t.m1.codebook, c2 = f2 ? -1 : t.m2.codebook;
+        const int l1 = f1 ? -1 : lut_id_of(t.m1.rounding, c1, t.m1.flags);
+        const int l2 = f2 ? -1 : lut_id_of(t.m2.rounding, c2, t.m2.flags);
         if (m1 < 0) {
             m1 = k1; m2 = k2; cb1 = c1; cb2 = c2; lut1 = l1; lut2 = l2;
         } else if (m1 != k1 || m2 != k2 || cb1 != c1 || cb2 != c2 || lut1 != l1 || lut2 != l2) {
