@@ -97,15 +97,17 @@ struct WaveScratch {
     __device__ BlockScratch block(int grp) { return BlockScratch{upd[grp], pre[grp], stage[grp]}; }
 };
 
-// Bucket of an x >= -0 (second moments): only the magnitude half of the table.
-__device__ __forceinline__ int lut_bucket_unsigned(float x) {
-    return min(max((int)__builtin_amdgcn_ubfe(f2u(x), 20, 11) - (AW4_LUT_EXP0 - 1), 0), AW4_LUT_HALF - 1);
+// Exponent and top 3 mantissa bits of x, clamped to the table's range (one med3).
+__device__ __forceinline__ int lut_field(uint32_t u) {
+    return min(max((int)__builtin_amdgcn_ubfe(u, 20, 11), AW4_LUT_EXP0 - 1), AW4_LUT_EXP0 - 2 + AW4_LUT_HALF);
 }
+
+// Bucket of an x >= -0 (second moments): only the magnitude half of the table.
+__device__ __forceinline__ int lut_bucket_unsigned(float x) { return lut_field(f2u(x)) - (AW4_LUT_EXP0 - 1); }
 
 __device__ __forceinline__ int lut_bucket_signed(float x) {
     const uint32_t u = f2u(x);
-    const int k = min(max((int)__builtin_amdgcn_ubfe(u, 20, 11) - (AW4_LUT_EXP0 - 1), 0), AW4_LUT_HALF - 1);
-    return k + (int)(u >> 31) * AW4_LUT_HALF;
+    return lut_field(u) - (AW4_LUT_EXP0 - 1) + (int)(u >> 31) * AW4_LUT_HALF;
 }
 
 // Decode the 4 values of one 16-bit code word: two LDS reads of level pairs.
@@ -136,22 +138,23 @@ __device__ __forceinline__ void update_sr_tables(const MomentTables& L, int j, f
         pre[k] = rcp_faithful(sqrt_faithful(vh) + eps);
     }
     wave_lds_sync();
+    // Entries 1..16 in two rounds of the block's 8 lanes; entry 0 (no level below x) has
+    // lo == hi and is always invalid.
 #pragma unroll
-    for (int h = 0; h < 3; ++h) {
-        const int i = j + 8 * h;
-        if (i < kPairs) {
-            const PairEntry pe = L.pairs[i];
-            const float flo = pre[pe.lohi & 0xffu], fhi = pre[pe.lohi >> 8];
-            const float den = flo - fhi;
-            const float dc = clamp_min_nan(den, 1e-30f);
-            UpdEntry e;
-            e.f_hi = fhi;
-            e.den = dc;
-            e.den_rcp = (pe.b > pe.a && den > 0.0f) ? 1.0f / dc : -1.0f;
-            e.b = pe.b;
-            upd[i] = e;
-        }
+    for (int h = 0; h < 2; ++h) {
+        const int i = 1 + j + 8 * h;
+        const PairEntry pe = L.pairs[i];
+        const float flo = pre[pe.lohi & 0xffu], fhi = pre[pe.lohi >> 8];
+        const float den = flo - fhi;
+        const float dc = clamp_min_nan(den, 1e-30f);
+        UpdEntry e;
+        e.f_hi = fhi;
+        e.den = dc;
+        e.den_rcp = (pe.b > pe.a && den > 0.0f) ? div_cr(1.0f, dc) : -1.0f;  // dc >= 1e-30: normal
+        e.b = pe.b;
+        upd[i] = e;
     }
+    if (j == 0) upd[0] = UpdEntry{0.0f, 1.0f, -1.0f, L.cb[0]};
     wave_lds_sync();
 }
 
@@ -192,7 +195,7 @@ __device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTa
     amax = block_max_u32(amax);
     const float s = u2f(max(amax, 0x2B8CBCCCu));  // max(absmax, fp32(1e-12))
     const bool fast = s < 0x1p125f;                // otherwise huge, infinite or NaN: IEEE division
-    const float y = 1.0f / s;
+    const float y = div_cr(1.0f, s);               // RN(1 / s): normal on the fast path
     constexpr int KIND = kind_of(SPEC), MF = flags_of(SPEC);
     constexpr bool kDyn = (MF & kFlagsAtRunTime) != 0;
     const int flags = kDyn ? M.flags : MF;
@@ -284,7 +287,7 @@ __device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTa
         // s' = s * (sum x*x / max(sum x*cb[code], 1e-12))  (_optimized_quantization.py:81-85)
         const float num = block_sum_cross(acc_xx);
         const float den = block_sum_cross(acc_xl);
-        scale = s * (num / clamp_min_nan(den, 1e-12f));
+        scale = s * div_cr(num, clamp_min_nan(den, 1e-12f));  // num in [1, 128]: a normal quotient
     }
     if (active && j == 0) __builtin_nontemporal_store(scale, gaddr<float>(M.scales) + blk0 + grp);
 }
