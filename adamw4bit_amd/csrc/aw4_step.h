@@ -196,26 +196,30 @@ template <int M1K, int M2K, int D>
 __device__ __forceinline__ void load_tile(const aw4_tensor& T, const TileLane& tl, TileInputs<M1K, M2K, D>& in) {
     using In = TileInputs<M1K, M2K, D>;
     const bool vec = D != D_ANY || (T.flags & AW4_TENSOR_VEC_ALIGNED) != 0;  // specialised kernels: host-checked
+    // Lanes past a tensor's last block (only in its last tile; the test is wave-uniform)
+    // load nothing and compute on zeros; they store nothing.
+    if (tl.blk0 + kBlocksPerWave > (T.numel >> 7)) {
 #pragma unroll
-    for (int i = 0; i < 4 * In::kW; ++i) in.g[i] = in.p[i] = 0u;
-    in.s1 = in.s2 = 0.0f;
-    if constexpr (In::kQ1) {
+        for (int i = 0; i < 4 * In::kW; ++i) in.g[i] = in.p[i] = 0u;
+        in.s1 = in.s2 = 0.0f;
+        if constexpr (In::kQ1) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) in.c1[q] = 0u;
+            for (int q = 0; q < 4; ++q) in.c1[q] = 0u;
+        }
+        if constexpr (In::kQ2) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) in.c2[q] = 0u;
+        }
+        if constexpr (In::kV1) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) in.v1[i] = 0.0f;
+        }
+        if constexpr (In::kV2) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) in.v2[i] = 0.0f;
+        }
+        if (!tl.active) return;
     }
-    if constexpr (In::kQ2) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) in.c2[q] = 0u;
-    }
-    if constexpr (In::kV1) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) in.v1[i] = 0.0f;
-    }
-    if constexpr (In::kV2) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) in.v2[i] = 0.0f;
-    }
-    if (!tl.active) return;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const uint32_t off = tl.voff + 32u * q;
