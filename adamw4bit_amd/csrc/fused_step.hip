@@ -36,7 +36,9 @@
 #include <map>
 #include <mutex>
 #include <string>
+#include <algorithm>
 #include <type_traits>
+#include <vector>
 
 #include "adamw4bit_hip.h"
 #include "aw4_step.h"
@@ -452,37 +454,63 @@ bool host_values_only(const aw4_tensor& t) {
     return (t.m1.rounding == AW4_ROUND_FP32 && t.m2.rounding == AW4_ROUND_FP32) || t.numel % kBlock != 0;
 }
 
-// Pick the kernel: a specialised one when every tensor shares its moment kinds,
-// codebooks, lookup tables and dtype; the generic one otherwise.
-int select_variant(const aw4_tensor* ts, int32_t count, StepHeader* h) {
-    int m1 = -1, m2 = -1, cb1 = -1, cb2 = -1, lut1 = -1, lut2 = -1, dtype = -1;
-    bool uniform = true;
-    for (int i = 0; i < count && uniform; ++i) {
+// One launch of a step: a kernel variant, the tables its LDS slots load, and its tensors.
+struct LaunchGroup {
+    int variant = kGenericVariant;
+    int cb1 = -1, lut1 = -1, cb2 = -1, lut2 = -1;
+    std::vector<int> members;
+};
+
+// Split a step's tensors into launches: tensors that share a specialised kernel and its
+// tables form one launch each; fp32-state tensors join a specialised launch of their
+// dtype; everything else (other scheme mixes, fp16, mixed dtypes) runs in one launch of
+// the generic kernel.  A recipe's table is one launch.
+std::vector<LaunchGroup> plan_launches(const aw4_tensor* ts, int32_t count) {
+    std::vector<LaunchGroup> groups;
+    LaunchGroup generic;
+    std::vector<int> values;
+    for (int i = 0; i < count; ++i) {
         const aw4_tensor& t = ts[i];
-        if (t.param_dtype != t.grad_dtype) uniform = false;
-        if (dtype < 0) dtype = t.param_dtype;
-        else if (dtype != t.param_dtype) uniform = false;
-        if (host_values_only(t)) continue;
-        const int k1 = mspec(t.m1.rounding, t.m1.flags & spec_flags_mask(t.m1.rounding));
-        const int k2 = mspec(t.m2.rounding, t.m2.flags & spec_flags_mask(t.m2.rounding));
+        if (t.param_dtype != t.grad_dtype) { generic.members.push_back(i); continue; }
+        if (host_values_only(t)) { values.push_back(i); continue; }
+        const int s1 = mspec(t.m1.rounding, t.m1.flags & spec_flags_mask(t.m1.rounding));
+        const int s2 = mspec(t.m2.rounding, t.m2.flags & spec_flags_mask(t.m2.rounding));
+        int v = kGenericVariant;
+        for (int k = 0; k < kGenericVariant; ++k)
+            if (kVariants[k].dtype == t.param_dtype && kVariants[k].m1 == s1 && kVariants[k].m2 == s2) { v = k; break; }
+        if (v == kGenericVariant) { generic.members.push_back(i); continue; }
         const bool f1 = t.m1.rounding == AW4_ROUND_FP32, f2 = t.m2.rounding == AW4_ROUND_FP32;
         const int c1 = f1 ? -1 : t.m1.codebook, c2 = f2 ? -1 : t.m2.codebook;
         const int l1 = f1 ? -1 : lut_id_of(t.m1.rounding, c1, t.m1.flags);
         const int l2 = f2 ? -1 : lut_id_of(t.m2.rounding, c2, t.m2.flags);
-        if (m1 < 0) {
-            m1 = k1; m2 = k2; cb1 = c1; cb2 = c2; lut1 = l1; lut2 = l2;
-        } else if (m1 != k1 || m2 != k2 || cb1 != c1 || cb2 != c2 || lut1 != l1 || lut2 != l2) {
-            uniform = false;
+        LaunchGroup* g = nullptr;
+        for (LaunchGroup& c : groups)
+            if (c.variant == v && c.cb1 == c1 && c.lut1 == l1 && c.cb2 == c2 && c.lut2 == l2) { g = &c; break; }
+        if (!g) {
+            groups.emplace_back();
+            g = &groups.back();
+            g->variant = v; g->cb1 = c1; g->lut1 = l1; g->cb2 = c2; g->lut2 = l2;
         }
+        g->members.push_back(i);
     }
-    h->cb1 = cb1; h->cb2 = cb2; h->lut1 = lut1; h->lut2 = lut2;
-    if (!uniform) return kGenericVariant;
-    for (int v = 0; v < kGenericVariant; ++v) {
-        const KernelVariant& kv = kVariants[v];
-        // a table of fp32-state tensors only runs on any variant of its dtype
-        if (kv.dtype == dtype && (m1 < 0 || (kv.m1 == m1 && kv.m2 == m2))) return v;
+    for (int i : values) {
+        LaunchGroup* g = nullptr;
+        for (LaunchGroup& c : groups)
+            if (kVariants[c.variant].dtype == ts[i].param_dtype) { g = &c; break; }
+        if (!g && !generic.members.empty()) g = &generic;
+        if (!g) {
+            for (int k = 0; k < kGenericVariant && !g; ++k) {
+                if (kVariants[k].dtype != ts[i].param_dtype) continue;
+                groups.emplace_back();
+                g = &groups.back();
+                g->variant = k;
+            }
+        }
+        (g ? g : &generic)->members.push_back(i);
     }
-    return kGenericVariant;
+    if (!generic.members.empty()) groups.push_back(std::move(generic));
+    for (LaunchGroup& g : groups) std::sort(g.members.begin(), g.members.end());
+    return groups;
 }
 
 }  // namespace
@@ -507,19 +535,24 @@ int aw4_fused_step(const aw4_tensor* tensors, int32_t count, void* stream) {
     g_error.clear();
     if (count < 0 || (count > 0 && !tensors)) return set_error(AW4_EINVAL, "aw4_fused_step: bad tensor list");
     if (count == 0) return AW4_OK;
-    int64_t total = 0;
     for (int i = 0; i < count; ++i) {
         const int rc = check_tensor(tensors[i], i);
         if (rc) return rc;
-        total += (tensors[i].numel + kWaveTile - 1) / kWaveTile;
     }
+    const std::vector<LaunchGroup> plan = plan_launches(tensors, count);
+    // Launch table of each group, 256-byte aligned: header, tensors[n], tile_start[n + 1].
+    std::vector<size_t> offset(plan.size());
+    size_t bytes = 0;
+    for (size_t g = 0; g < plan.size(); ++g) {
+        const size_t n = plan[g].members.size();
+        offset[g] = bytes;
+        bytes += (sizeof(StepHeader) + sizeof(aw4_tensor) * n + sizeof(int64_t) * (n + 1) + 255) & ~(size_t)255;
+    }
+
     std::lock_guard<std::mutex> lock(g_mutex);
     DeviceState* ds = nullptr;
     int rc = device_state(&ds);
     if (rc) return rc;
-
-    const size_t bytes =
-        sizeof(StepHeader) + sizeof(aw4_tensor) * (size_t)count + sizeof(int64_t) * (size_t)(count + 1);
     StagingSlot& slot = ds->slots[ds->next];
     ds->next = (ds->next + 1) % kSlots;
     if (slot.pending) {
@@ -539,36 +572,45 @@ int aw4_fused_step(const aw4_tensor* tensors, int32_t count, void* stream) {
     }
     if (!slot.done) AW4_HIP_CHECK(hipEventCreateWithFlags(&slot.done, hipEventDisableTiming));
 
-    StepHeader* h = (StepHeader*)slot.host;
-    memset(h, 0, sizeof(*h));
-    const int variant = select_variant(tensors, count, h);
     // A few tiles per wave and a grid covering all of them: the hardware dispatcher hands
     // each free slot the next workgroup, so the tiles in flight stay a narrow, moving window
     // of the index space (HBM page locality) and no CU waits on a static share at the end.
     // Measured on MI355X against persistent grids of contiguous per-wave ranges, which
     // stream from thousands of far-apart addresses at once and leave a load-imbalance tail.
-    const int64_t per_wave = kTilesPerWave;
-    const int64_t waves = (total + per_wave - 1) / per_wave;
-    const int64_t groups = (waves + kWavesPerGroup - 1) / kWavesPerGroup;
-    if (groups > 0x7fffffff) return set_error(AW4_EINVAL, "aw4_fused_step: %lld tiles exceed one launch", (long long)total);
-    h->count = count;
-    h->total_tiles = total;
-    h->tiles_per_wave = per_wave;
-    memcpy(h + 1, tensors, sizeof(aw4_tensor) * (size_t)count);
-    int64_t* starts = (int64_t*)((aw4_tensor*)(h + 1) + count);
-    int64_t acc = 0;
-    for (int i = 0; i < count; ++i) {
-        starts[i] = acc;
-        acc += (tensors[i].numel + kWaveTile - 1) / kWaveTile;
+    std::vector<int64_t> grid(plan.size());
+    for (size_t g = 0; g < plan.size(); ++g) {
+        const LaunchGroup& lg = plan[g];
+        const int n = (int)lg.members.size();
+        StepHeader* h = (StepHeader*)((char*)slot.host + offset[g]);
+        memset(h, 0, sizeof(*h));
+        aw4_tensor* rows = (aw4_tensor*)(h + 1);
+        int64_t* starts = (int64_t*)(rows + n);
+        int64_t acc = 0;
+        for (int k = 0; k < n; ++k) {
+            rows[k] = tensors[lg.members[k]];
+            starts[k] = acc;
+            acc += (rows[k].numel + kWaveTile - 1) / kWaveTile;
+        }
+        starts[n] = acc;
+        const int64_t waves = (acc + kTilesPerWave - 1) / kTilesPerWave;
+        grid[g] = (waves + kWavesPerGroup - 1) / kWavesPerGroup;
+        if (grid[g] > 0x7fffffff)
+            return set_error(AW4_EINVAL, "aw4_fused_step: %lld tiles exceed one launch", (long long)acc);
+        h->count = n;
+        h->cb1 = lg.cb1; h->lut1 = lg.lut1; h->cb2 = lg.cb2; h->lut2 = lg.lut2;
+        h->total_tiles = acc;
+        h->tiles_per_wave = kTilesPerWave;
     }
-    starts[count] = acc;
 
     hipStream_t s = (hipStream_t)stream;
     AW4_HIP_CHECK(hipMemcpyAsync(slot.dev, slot.host, bytes, hipMemcpyHostToDevice, s));
-    const StepHeader* dh = (const StepHeader*)slot.dev;
     const Tables* dt = (const Tables*)ds->tables;
-    void* args[] = {(void*)&dh, (void*)&dt};
-    AW4_HIP_CHECK(hipLaunchKernel(kVariants[variant].fn, dim3((unsigned)groups), dim3(kThreads), args, 0, s));
+    for (size_t g = 0; g < plan.size(); ++g) {
+        if (grid[g] == 0) continue;
+        const StepHeader* dh = (const StepHeader*)((const char*)slot.dev + offset[g]);
+        void* args[] = {(void*)&dh, (void*)&dt};
+        AW4_HIP_CHECK(hipLaunchKernel(kVariants[plan[g].variant].fn, dim3((unsigned)grid[g]), dim3(kThreads), args, 0, s));
+    }
     AW4_HIP_CHECK(hipEventRecord(slot.done, s));
     slot.pending = true;
     return AW4_OK;

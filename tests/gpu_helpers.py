@@ -117,11 +117,13 @@ ULP16 = {torch.bfloat16: 2.0 ** -7, torch.float16: 2.0 ** -10}
 
 
 def assert_params_close(got: torch.Tensor, expect: torch.Tensor, what: str, rtol: float = PARAM_RTOL,
-                        steps: int = 1) -> float:
+                        steps: int = 1, exclude: torch.Tensor = None) -> float:
     """Parameters within 1e-6 relative to the parameter scale: |got - expect| <= 1e-6 * (|expect| +
     rms(expect)) elementwise (a value that drifted close to zero keeps the one-ulp difference it
     picked up while it was of the tensor's typical size).  16-bit parameters: one storage ulp per
-    step at that scale, since each step rounds twice to 16 bits.  Returns the bit-exact fraction."""
+    step at that scale, since each step rounds twice to 16 bits.  `exclude` (bool, one per value)
+    drops values whose stochastic codes took the other level at some step (their trajectories
+    legitimately part).  Returns the bit-exact fraction."""
     exact = float((bits(got) == bits(expect)).double().mean())
     g = got.detach().cpu().double()
     e = expect.detach().cpu().double()
@@ -129,9 +131,20 @@ def assert_params_close(got: torch.Tensor, expect: torch.Tensor, what: str, rtol
     scale = e.abs() + e.pow(2).mean().sqrt()
     tol = (ULP16[got.dtype] * steps if got.dtype in ULP16 else rtol) * scale
     bad = err > tol
+    if exclude is not None:
+        bad &= ~exclude.reshape(bad.shape)
     assert not bool(bad.any()), (f"{what}: {int(bad.sum())} of {e.numel()} values exceed the tolerance; "
                                  f"worst error {float((err / tol).max()):.3g} x tolerance; bit-exact {exact:.6f}")
     return exact
+
+
+def code_diff_mask(a: torch.Tensor, b: torch.Tensor, numel: int) -> torch.Tensor:
+    """Per value: whether two packed code tensors hold different 4-bit codes."""
+    a = a.cpu()
+    b = b.cpu()
+    lo = (a & 0x0F) != (b & 0x0F)
+    hi = (a >> 4) != (b >> 4)
+    return torch.stack([lo, hi], dim=-1).reshape(-1)[:numel]
 
 
 def code_mismatch(a: torch.Tensor, b: torch.Tensor) -> int:

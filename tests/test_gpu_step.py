@@ -215,6 +215,9 @@ def run_pair(make_opt, shapes, dtype, steps, *, seed=0, grad_seed=1, m1_override
                         seed=seed, optimized=opt._optimized,
                         chunk=hp.get("max_chunk_numel", ref.CHUNK_NUMEL),
                         draw_fn=H.PhiloxMirror(opt, H.DEVICE), **(oracle_kwargs or {}))
+    # Values whose stochastic codes took the other level at some step (a draw between two
+    # probabilities one square-root ulp apart); their later states and parameters part ways.
+    parted = [torch.zeros(p.numel(), dtype=torch.bool) for p in params]
     for _ in range(steps):
         grads = []
         for s in shapes:
@@ -227,32 +230,45 @@ def run_pair(make_opt, shapes, dtype, steps, *, seed=0, grad_seed=1, m1_override
             p.grad = g.to(H.DEVICE)
         opt.step()
         oracle.step(grads)
+        for i, p in enumerate(params):
+            st = H.state_of(opt, p)
+            for m, ms in (("m1", oracle.states[i].m1), ("m2", oracle.states[i].m2)):
+                if ref.is_stochastic(ms.scheme):
+                    parted[i] |= H.code_diff_mask(st[f"{m}_code"], ms.codes, p.numel())
     torch.cuda.synchronize()
-    return opt, params, oracle, cpu_params
+    return opt, params, oracle, cpu_params, parted
 
 
-def compare_pair(opt, params, oracle, cpu_params, what, sr_moments=(), steps=1):
-    total_flips = 0
+def compare_pair(opt, params, oracle, cpu_params, parted, what, steps=1):
+    """Round-to-nearest moments and fp32 state bit-exact; stochastic moments within the flip
+    budget (values that parted at any step count once); parameters within tolerance except
+    where a stochastic code parted."""
+    total_parted = 0
     total_codes = 0
     for i, (p, cp) in enumerate(zip(params, cpu_params)):
         st = H.state_of(opt, p)
         ost = H.oracle_state((oracle.states[i].m1, oracle.states[i].m2))
         assert set(st) - {"step"} == set(ost), (what, i, sorted(st), sorted(ost))
-        for m in ("m1", "m2"):
+        for m, ms in (("m1", oracle.states[i].m1), ("m2", oracle.states[i].m2)):
             if f"{m}_code" in ost:
                 flips = H.code_mismatch(st[f"{m}_code"], ost[f"{m}_code"])
-                total_flips += flips
-                total_codes += p.numel()
-                if m not in sr_moments:
-                    assert flips == 0, f"{what} p{i} {m}: {flips} flips"
+                if ref.is_stochastic(ms.scheme):
+                    total_codes += p.numel()
+                    if flips:
+                        log(f"  p{i} {m} ({ms.scheme}): {flips} codes differ at the last step")
+                else:
+                    # the two moments evolve independently: a parted stochastic moment leaves this one exact
+                    assert flips == 0, f"{what} p{i} {m} ({ms.scheme}): {flips} flips"
                     assert torch.equal(H.bits(st[f"{m}_scale"]), H.bits(ost[f"{m}_scale"])), (what, i, m)
             else:
                 assert torch.equal(H.bits(st[f"{m}_fp32"].reshape(-1)), H.bits(ost[f"{m}_fp32"])), (what, i, m)
-        exact = H.assert_params_close(p, cp, f"{what} p{i}", steps=steps)
-        log(f"  p{i} {tuple(p.shape)}: parameters bit-exact {exact:.6f}")
-    log(f"  code flips {total_flips} of {total_codes}")
-    assert total_flips <= SR_BUDGET * max(total_codes, 1) + 0.5, f"{what}: {total_flips} flips of {total_codes}"
-    return total_flips
+        n_parted = int(parted[i].sum())
+        total_parted += n_parted
+        exact = H.assert_params_close(p, cp, f"{what} p{i}", steps=steps, exclude=parted[i])
+        log(f"  p{i} {tuple(p.shape)}: parameters bit-exact {exact:.6f}; values parted by a stochastic code {n_parted}")
+    log(f"  parted values {total_parted} of {total_codes} stochastic codes")
+    assert total_parted <= SR_BUDGET * max(total_codes, 1) + 0.5, f"{what}: {total_parted} of {total_codes}"
+    return total_parted
 
 
 def test_zeeden_1024x1024_matches_oracle():
@@ -267,14 +283,14 @@ def test_zipsr_philox_matches_oracle():
     args = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True, quant_rng_seed=0)
     out = run_pair(lambda ps: aw.ZIPSRAdamW4Bit(ps, **args), [(512, 1024), (256, 128)], torch.float32, 6, seed=0,
                    m1_override=([1], "nf4_sr"))
-    compare_pair(*out, "zipsr philox", sr_moments=("m1", "m2"))
+    compare_pair(*out, "zipsr philox")
 
 
 def test_zipsr_4096x4096_matches_oracle():
     log("zipsr 4096x4096 x 2 steps (full size)")
     args = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True, quant_rng_seed=0)
     out = run_pair(lambda ps: aw.ZIPSRAdamW4Bit(ps, **args), [(4096, 4096)], torch.float32, 2, seed=0)
-    compare_pair(*out, "zipsr 4096^2", sr_moments=("m2",))
+    compare_pair(*out, "zipsr 4096^2")
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -285,7 +301,7 @@ def test_mixed_list_16bit(dtype):
     args = dict(lr=2e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True, quant_rng_seed=3)
     out = run_pair(lambda ps: aw.ZIPSRAdamW4Bit(ps, **args), shapes, dtype, 4, seed=3, m1_override=([8], "nf4_sr"),
                    zero_block_frac=0.05)
-    compare_pair(*out, f"mixed {dtype}", sr_moments=("m1", "m2"), steps=4)
+    compare_pair(*out, f"mixed {dtype}", steps=4)
 
 
 def test_scheme_groups_reference_step():
@@ -301,7 +317,27 @@ def test_scheme_groups_reference_step():
         return aw.QuantizedAdamW(groups, lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1,
                                  m1_quant_scheme="nf4", m2_quant_scheme="dyn4_nz", quant_rng_seed=9, optimized=False)
     out = run_pair(make, [(8192,)] * len(pairs), torch.float32, 3, seed=9, zero_block_frac=0.02)
-    compare_pair(*out, "scheme groups", sr_moments=("m1", "m2"))
+    compare_pair(*out, "scheme groups")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_mixed_recipes_split_launches(dtype):
+    """One optimizer whose tensors need different kernels (ZE-EDEN and ZIP-SR recipe schemes, an
+    nf4_sr head, an fp32 second moment, fp32-state vectors): the step splits into one launch per
+    specialised kernel plus one generic launch, and every tensor still matches the oracle."""
+    log(f"mixed recipes, split launches, {dtype}")
+    pairs = [("nf4", "dyn4_nz", True), ("nf4", "dyn4_upd_sr_fp32read", False), ("nf4", "dyn4_nz", True),
+             ("nf4", "dyn4_upd_sr_fp32read", False), ("nf4", "fp32", False), ("nf4", "dyn4_nz", True),
+             ("nf4", "dyn4_upd_sr_fp32read", False)]
+    shapes = [(256, 512), (384, 256), (768,), (1000,), (128, 256), (64, 1024), (96, 512)]
+
+    def make(ps):
+        groups = [dict(params=[p], m1_quant_scheme=a, m2_quant_scheme=b, use_eden_m2=e)
+                  for p, (a, b, e) in zip(ps, pairs)]
+        return aw.QuantizedAdamW(groups, lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1,
+                                 m1_quant_scheme="nf4", m2_quant_scheme="dyn4_nz", quant_rng_seed=5, optimized=True)
+    out = run_pair(make, shapes, dtype, 4, seed=5, m1_override=([6], "nf4_sr"), zero_block_frac=0.02)
+    compare_pair(*out, f"mixed recipes {dtype}", steps=4)
 
 
 def test_lerp_large_weight_betas():
