@@ -127,7 +127,7 @@ struct KernelTraits {
     static constexpr bool kUpd = K1 == K_USR || K2 == K_USR || K1 == K_ANY || K2 == K_ANY;
     // Waves per SIMD the register allocation must allow (512 VGPRs per lane, granule 8):
     // 5 keeps the round-to-nearest kernels at <= 96 VGPRs.
-    static constexpr int kMinWaves = (!kGeneric && !kUpd) ? 5 : 1;
+    static constexpr int kMinWaves = (K1 == K_RTN && K2 == K_RTN) ? 5 : 1;
     using Lds = typename std::conditional<kGeneric, LdsAll, LdsSlots<kUpd>>::type;
 };
 
@@ -142,23 +142,29 @@ step_kernel(const StepHeader* __restrict__ hdr,
     run_tiles<M1K, M2K, D>(hdr, lds, lds.scratch[wslot]);
 }
 
-// The instantiated kernels; the host picks the first whose moment specs and dtype match
-// every tensor of the table.  ZE-EDEN: NF4 round-to-nearest m1, Dyn4 round-to-nearest m2
-// with EDEN; ZIP-SR: NF4 round-to-nearest m1, Dyn4 update-SR m2 with the optimized path's
-// exact-level guards.
-constexpr int kRtn = mspec(K_RTN), kRtnEden = mspec(K_RTN, AW4_MOMENT_EDEN);
+// The instantiated kernels; the host groups a step's tensors by the variant whose moment
+// specs and dtype they match (optimized-path flags).  ZE-EDEN: NF4 round-to-nearest m1,
+// Dyn4 round-to-nearest m2 with EDEN.  ZIP-SR: NF4 round-to-nearest m1, Dyn4 update-SR m2
+// with the exact-level guards; its nf4_sr head (value-space SR m1).  QuantizedAdamW
+// ablations of ZIP-SR: an fp32 m2, EDEN on the update-SR m2.
+constexpr int kRtn = mspec(K_RTN), kRtnEden = mspec(K_RTN, AW4_MOMENT_EDEN), kFp32 = mspec(K_FP32);
+constexpr int kSsrGuarded = mspec(K_SSR, AW4_MOMENT_GUARDS);
 constexpr int kUsrGuarded = mspec(K_USR, AW4_MOMENT_GUARDS);
+constexpr int kUsrGuardedEden = mspec(K_USR, AW4_MOMENT_GUARDS | AW4_MOMENT_EDEN);
 struct KernelVariant {
     int m1, m2, dtype;
     const void* fn;
 };
+#define AW4_VARIANT(M1, M2, D) {M1, M2, D, (const void*)&step_kernel<M1, M2, D>}
 const KernelVariant kVariants[] = {
-    {kRtn, kRtnEden, D_F32, (const void*)&step_kernel<kRtn, kRtnEden, D_F32>},
-    {kRtn, kUsrGuarded, D_F32, (const void*)&step_kernel<kRtn, kUsrGuarded, D_F32>},
-    {kRtn, kRtnEden, D_BF16, (const void*)&step_kernel<kRtn, kRtnEden, D_BF16>},
-    {kRtn, kUsrGuarded, D_BF16, (const void*)&step_kernel<kRtn, kUsrGuarded, D_BF16>},
-    {K_ANY, K_ANY, D_ANY, (const void*)&step_kernel<K_ANY, K_ANY, D_ANY>},
+    AW4_VARIANT(kRtn, kRtnEden, D_F32),           AW4_VARIANT(kRtn, kUsrGuarded, D_F32),
+    AW4_VARIANT(kRtn, kRtnEden, D_BF16),          AW4_VARIANT(kRtn, kUsrGuarded, D_BF16),
+    AW4_VARIANT(kSsrGuarded, kUsrGuarded, D_F32), AW4_VARIANT(kSsrGuarded, kUsrGuarded, D_BF16),
+    AW4_VARIANT(kRtn, kFp32, D_F32),              AW4_VARIANT(kRtn, kFp32, D_BF16),
+    AW4_VARIANT(kRtn, kUsrGuardedEden, D_F32),    AW4_VARIANT(kRtn, kUsrGuardedEden, D_BF16),
+    AW4_VARIANT(K_ANY, K_ANY, D_ANY),
 };
+#undef AW4_VARIANT
 constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 constexpr int kGenericVariant = kNumVariants - 1;
 

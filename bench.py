@@ -51,18 +51,36 @@ def gpt2_small_shapes():
 
 CONFIGS = {
     "llama3-8b": llama3_8b_shapes,
+    "llama3-8b-bf16-mixed": llama3_8b_shapes,
     "gpt2-small": gpt2_small_shapes,
     "1024x1024": lambda: [(1024, 1024)],
     "4096x4096": lambda: [(4096, 4096)],
 }
 
 
-def bytes_per_value(numel: int, param_bytes: int = 4, grad_bytes: int = 4) -> float:
+def bytes_per_value(numel: int, param_bytes: int = 4, grad_bytes: int = 4, m1: str = "nf4", m2: str = "dyn4") -> float:
     """Algorithmic HBM bytes per value of one step: p read+write, g read, and per moment
     either 4-bit codes read+write plus one fp32 scale per 128 values read+write, or fp32
-    state read+write (tensors below 4096 values or not a multiple of 128)."""
-    moment = 2 * 0.5 + 2 * 4 / 128 if (numel >= 4096 and numel % 128 == 0) else 8.0
-    return 2 * param_bytes + grad_bytes + 2 * moment
+    state read+write (an fp32 scheme, or tensors below 4096 values or not a multiple of 128)."""
+    eligible = numel >= 4096 and numel % 128 == 0
+    moment = [2 * 0.5 + 2 * 4 / 128 if (eligible and m != "fp32") else 8.0 for m in (m1, m2)]
+    return 2 * param_bytes + grad_bytes + sum(moment)
+
+
+def mixed_bf16_groups(params):
+    """The mixed-scheme stress case on the Llama-3-8B shapes: ZIP-SR schemes everywhere, every
+    tenth tensor an ablation of QuantizedAdamW (alternately an fp32 second moment and ZIP-SR with
+    EDEN on m2), the LM head's first moment stochastically rounded (nf4_sr)."""
+    groups, schemes = [], []
+    for i, p in enumerate(params):
+        if i % 10 == 5:
+            m2, eden = ("fp32", False) if (i // 10) % 2 == 0 else ("dyn4_upd_sr_fp32read", True)
+        else:
+            m2, eden = "dyn4_upd_sr_fp32read", False
+        groups.append(dict(params=[p], m1_quant_scheme="nf4", m2_quant_scheme=m2, use_eden_m2=eden))
+        schemes.append(["nf4", m2])
+    schemes[-1][0] = "nf4_sr"  # LM head
+    return groups, schemes
 
 
 def make_grads(shapes, device, seed):
@@ -171,38 +189,54 @@ def main():
     shapes = CONFIGS[args.config]()
     numels = [math.prod(s) for s in shapes]
     total = sum(numels)
-    algo_bytes = sum(n * bytes_per_value(n) for n in numels)
+    mixed = args.config == "llama3-8b-bf16-mixed"
+    dtype = torch.bfloat16 if mixed else torch.float32
+    esize = 2 if mixed else 4
 
-    print(f"[bench] {args.config}: {len(shapes)} tensors, {total:,} values, "
-          f"{algo_bytes / 1e9:.2f} GB algorithmic per launch", file=sys.stderr, flush=True)
     gen = torch.Generator(device=device).manual_seed(1234)
-    params = [torch.nn.Parameter(torch.randn(s, generator=gen, device=device) * 0.02) for s in shapes]
+    params = [torch.nn.Parameter((torch.randn(s, generator=gen, device=device) * 0.02).to(dtype)) for s in shapes]
     grads = make_grads(shapes, device, seed=5678)
     for p, g in zip(params, grads):
-        p.grad = g
+        if mixed and g.numel() % 128 == 0:  # 1% of gradient blocks zero (dyn4 zero-inclusive path)
+            nb = g.numel() // 128
+            g.view(nb, 128)[torch.rand(nb, generator=gen, device=device) < 0.01] = 0.0
+        p.grad = g.to(dtype)
     del grads
-    recipes = []
-    for r in args.recipes.split(","):
-        if r == "zeeden":
-            recipes.append(("ZE-EDEN", aw.ZEEDENAdamW4Bit(params, optimized=True)))
-        elif r == "zipsr":
-            recipes.append(("ZIP-SR", aw.ZIPSRAdamW4Bit(params, optimized=True, quant_rng_seed=0)))
-        else:
-            raise SystemExit(f"unknown recipe {r}")
+    recipes = []  # (name, optimizer, algorithmic bytes per launch)
+    if mixed:
+        groups, schemes = mixed_bf16_groups(params)
+        opt = aw.QuantizedAdamW(groups, m1_quant_scheme="nf4", m2_quant_scheme="dyn4_upd_sr_fp32read",
+                                optimized=True, quant_rng_seed=0)
+        opt.set_m1_quant_scheme_for_parameters([params[-1]], "nf4_sr")
+        algo = sum(n * bytes_per_value(n, esize, esize, *sc) for n, sc in zip(numels, schemes))
+        recipes.append(("mixed", opt, algo))
+    else:
+        algo = sum(n * bytes_per_value(n) for n in numels)
+        for r in args.recipes.split(","):
+            if r == "zeeden":
+                recipes.append(("ZE-EDEN", aw.ZEEDENAdamW4Bit(params, optimized=True), algo))
+            elif r == "zipsr":
+                recipes.append(("ZIP-SR", aw.ZIPSRAdamW4Bit(params, optimized=True, quant_rng_seed=0), algo))
+            else:
+                raise SystemExit(f"unknown recipe {r}")
+    algo_bytes = {name: a for name, _, a in recipes}
+    print(f"[bench] {args.config}: {len(shapes)} tensors, {total:,} values, "
+          f"{ {k: round(v / 1e9, 2) for k, v in algo_bytes.items()} } GB algorithmic per launch",
+          file=sys.stderr, flush=True)
     torch.cuda.synchronize()
     print(f"[bench] allocated {torch.cuda.memory_allocated() / 1e9:.1f} GB; warmup {args.warmup}",
           file=sys.stderr, flush=True)
 
     stream = torch.cuda.current_stream(device)
     for _ in range(args.warmup):
-        for _, opt in recipes:
+        for _, opt, _ in recipes:
             opt.step()
     torch.cuda.synchronize()
 
-    events = {name: [] for name, _ in recipes}
+    events = {name: [] for name, _, _ in recipes}
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        for name, opt in recipes:
+        for name, opt, _ in recipes:
             start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             start.record(stream)
             opt.step()
@@ -214,7 +248,7 @@ def main():
     per_recipe = {name: statistics.mean(v) for name, v in launch_ms.items()}
     # The dominant kernel is the recipe with the longest launches; its roofline is reported.
     dominant = max(per_recipe, key=per_recipe.get)
-    achieved = algo_bytes / (per_recipe[dominant] * 1e-3) / 1e9
+    achieved = algo_bytes[dominant] / (per_recipe[dominant] * 1e-3) / 1e9
     traffic, traffic_source = measured_traffic(args.config)
     ms_per_step = wall * 1e3 / args.steps
     value = total * len(recipes) * args.steps / wall / 1e9
@@ -238,21 +272,25 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic: Student-t(3) x per-row log-normal(-7,1) gradients, N(0,0.02) parameters",
+        "dtype": "bf16" if mixed else "f32",
+        "data": "synthetic: Student-t(3) x per-row log-normal(-7,1) gradients, N(0,0.02) parameters"
+                + (", 1% zero gradient blocks" if mixed else ""),
         "config": {
-            "workload": f"{args.config} fp32 parameter set, one {' + one '.join(n for n, _ in recipes)} step "
-                        f"per timed step ({len(recipes)} fused launches)",
-            "tensors": len(shapes), "values": total, "recipes": [n for n, _ in recipes],
+            "workload": (f"{args.config}: Llama-3-8B bf16 parameter set, ZIP-SR schemes, nf4_sr LM head, every "
+                         "tenth tensor an fp32-m2 / EDEN-m2 ablation, one optimizer step per timed step"
+                         if mixed else
+                         f"{args.config} fp32 parameter set, one {' + one '.join(n for n, _, _ in recipes)} step "
+                         f"per timed step ({len(recipes)} fused launches)"),
+            "tensors": len(shapes), "values": total, "recipes": [n for n, _, _ in recipes],
             "launch_ms": {k: round(v, 4) for k, v in per_recipe.items()},
             "gelem_s_per_recipe": {k: round(total / (v * 1e-3) / 1e9, 2) for k, v in per_recipe.items()},
-            "hbm_frac_per_recipe": {k: round(algo_bytes / (v * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+            "hbm_frac_per_recipe": {k: round(algo_bytes[k] / (v * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
                                     for k, v in per_recipe.items()},
-            "algorithmic_gb_per_launch": round(algo_bytes / 1e9, 4),
+            "algorithmic_gb_per_launch": {k: round(v / 1e9, 4) for k, v in algo_bytes.items()},
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": f"{RECIPE_KERNELS.get(dominant, dominant)} ({dominant})",
+            "kernel": f"{RECIPE_KERNELS.get(dominant, 'step_kernel launches')} ({dominant})",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

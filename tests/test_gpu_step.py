@@ -328,8 +328,8 @@ def test_mixed_recipes_split_launches(dtype):
     log(f"mixed recipes, split launches, {dtype}")
     pairs = [("nf4", "dyn4_nz", True), ("nf4", "dyn4_upd_sr_fp32read", False), ("nf4", "dyn4_nz", True),
              ("nf4", "dyn4_upd_sr_fp32read", False), ("nf4", "fp32", False), ("nf4", "dyn4_nz", True),
-             ("nf4", "dyn4_upd_sr_fp32read", False)]
-    shapes = [(256, 512), (384, 256), (768,), (1000,), (128, 256), (64, 1024), (96, 512)]
+             ("nf4", "dyn4_upd_sr_fp32read", False), ("nf4", "dyn4_upd_sr_fp32read", True)]
+    shapes = [(256, 512), (384, 256), (768,), (1000,), (128, 256), (64, 1024), (96, 512), (160, 256)]
 
     def make(ps):
         groups = [dict(params=[p], m1_quant_scheme=a, m2_quant_scheme=b, use_eden_m2=e)
