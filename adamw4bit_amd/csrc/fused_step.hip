@@ -125,15 +125,11 @@ struct KernelTraits {
     static constexpr int K1 = kind_of(M1K), K2 = kind_of(M2K);
     static constexpr bool kGeneric = K1 == K_ANY || K2 == K_ANY || D == D_ANY;
     static constexpr bool kUpd = K1 == K_USR || K2 == K_USR || K1 == K_ANY || K2 == K_ANY;
-    // Waves per SIMD the register allocation must allow (512 VGPRs per lane, granule 8):
-    // 5 keeps the round-to-nearest kernels at <= 96 VGPRs.
-    static constexpr int kMinWaves = (K1 == K_RTN && K2 == K_RTN) ? 5 : 1;
     using Lds = typename std::conditional<kGeneric, LdsAll, LdsSlots<kUpd>>::type;
 };
 
 template <int M1K, int M2K, int D>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(KernelTraits<M1K, M2K, D>::kMinWaves)))
-step_kernel(const StepHeader* __restrict__ hdr,
+__global__ void __launch_bounds__(kThreads) step_kernel(const StepHeader* __restrict__ hdr,
                                                          const Tables* __restrict__ tables) {
     using Lds = typename KernelTraits<M1K, M2K, D>::Lds;
     __shared__ Lds lds;
