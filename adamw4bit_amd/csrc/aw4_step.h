@@ -196,33 +196,15 @@ template <int M1K, int M2K, int D>
 __device__ __forceinline__ void load_tile(const aw4_tensor& T, const TileLane& tl, TileInputs<M1K, M2K, D>& in) {
     using In = TileInputs<M1K, M2K, D>;
     const bool vec = D != D_ANY || (T.flags & AW4_TENSOR_VEC_ALIGNED) != 0;  // specialised kernels: host-checked
-    // Lanes past a tensor's last block (only in its last tile; the test is wave-uniform)
-    // load nothing and compute on zeros; they store nothing.
-    if (tl.blk0 + kBlocksPerWave > (T.numel >> 7)) {
-#pragma unroll
-        for (int i = 0; i < 4 * In::kW; ++i) in.g[i] = in.p[i] = 0u;
-        in.s1 = in.s2 = 0.0f;
-        if constexpr (In::kQ1) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) in.c1[q] = 0u;
-        }
-        if constexpr (In::kQ2) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) in.c2[q] = 0u;
-        }
-        if constexpr (In::kV1) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) in.v1[i] = 0.0f;
-        }
-        if constexpr (In::kV2) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) in.v2[i] = 0.0f;
-        }
-        if (!tl.active) return;
-    }
+    // Lanes past a tensor's last block (only in its last tile) read the tile's first block,
+    // which always exists, so every register holds loaded data without a fill or a masked
+    // load; their results are never stored, and every block statistic stays within one
+    // block's 8 lanes.
+    const uint32_t voff = tl.active ? tl.voff : 4u * (uint32_t)tl.j;
+    const int grp = tl.active ? tl.grp : 0;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const uint32_t off = tl.voff + 32u * q;
+        const uint32_t off = voff + 32u * q;
         if constexpr (D == D_ANY) {
             const int64_t e = tl.blk0 * kBlock + off;
             load_words_any(T.grad_dtype, T.grad, e, vec, &in.g[4 * q]);
@@ -239,18 +221,18 @@ __device__ __forceinline__ void load_tile(const aw4_tensor& T, const TileLane& t
         if (quantized) {
             if constexpr (kQ) {
                 const gptr<const uint8_t> codes = gaddr<const uint8_t>(M.codes) + tl.blk0 * (kBlock / 2);
-                const uint32_t coff = (uint32_t)(tl.grp * (kBlock / 2) + 2 * tl.j);
+                const uint32_t coff = (uint32_t)(grp * (kBlock / 2) + 2 * tl.j);
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
                     c[q] = __builtin_nontemporal_load((gptr<const uint16_t>)(codes + coff + 16u * q));
-                s = (gaddr<const float>(M.scales) + tl.blk0)[tl.grp];
+                s = (gaddr<const float>(M.scales) + tl.blk0)[grp];
             }
         } else {
             if constexpr (kV) {
                 const gptr<const float> vals_tile = gaddr<const float>(M.values) + tl.blk0 * kBlock;
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    const f32x4 x = __builtin_nontemporal_load((gptr<const f32x4>)(vals_tile + tl.voff + 32u * q));
+                    const f32x4 x = __builtin_nontemporal_load((gptr<const f32x4>)(vals_tile + voff + 32u * q));
                     v[4 * q] = x.x; v[4 * q + 1] = x.y; v[4 * q + 2] = x.z; v[4 * q + 3] = x.w;
                 }
             }
