@@ -33,7 +33,7 @@ import numpy as np
 import torch
 from torch.optim.optimizer import Optimizer
 
-from . import _lib
+from . import _lib, _ops
 from ._rng import PhiloxStream
 from .quantization import (
     NEXT_BIAS_SCHEMES,
@@ -86,6 +86,46 @@ def _byte_range(t: torch.Tensor) -> Tuple[str, int, int]:
 
 def _overlaps(a, b) -> bool:
     return a[0] == b[0] and a[1] < b[2] and b[1] < a[2]
+
+
+class _StepConstants:
+    """The fp32 step constants of one (group, step), computed in float64 and rounded once to
+    fp32 as the reference does (``_optimized.py:168-173``)."""
+
+    __slots__ = ("lerp_flags", "w1", "w2", "decay", "step_coef", "bc2_sqrt", "bc2_sqrt_rcp", "eps", "storage_bias",
+                 "rows")
+
+    def __init__(self, group, step: int, m2_scheme: str):
+        beta1, beta2 = group["betas"]
+        lr, wd, eps = group["lr"], group["weight_decay"], group["eps"]
+        bias1, bias2 = 1 - beta1 ** step, 1 - beta2 ** step
+        self.storage_bias = 1 - beta2 ** (step + 1) if m2_scheme in NEXT_BIAS_SCHEMES else bias2
+        flags = 0
+        w1, w2 = np.float32(1 - beta1), np.float32(1 - beta2)
+        if not abs(w1) < 0.5:  # ATen lerp switches formulas at |weight| >= 0.5
+            flags |= _lib.TENSOR_LERP1_LARGE
+            w1 = w1 - np.float32(1.0)
+        if not abs(w2) < 0.5:
+            flags |= _lib.TENSOR_LERP2_LARGE
+            w2 = w2 - np.float32(1.0)
+        self.lerp_flags = flags
+        self.w1, self.w2 = float(w1), float(w2)
+        self.decay = _f32(1 - lr * wd)
+        self.step_coef = _f32(-lr / bias1)
+        self.bc2_sqrt = _f32(math.sqrt(bias2))
+        self.bc2_sqrt_rcp = _rcp32(self.bc2_sqrt)
+        self.eps = _f32(eps)
+
+
+def _step_constants(group, step: int, m2_scheme: str) -> _StepConstants:
+    return _StepConstants(group, step, m2_scheme)
+
+
+def _vec_aligned(p: torch.Tensor, grad: torch.Tensor) -> bool:
+    """Parameter and gradient allow 4-value vector access."""
+    psize = 4 * p.element_size()
+    gsize = 4 * grad.element_size()
+    return p.data_ptr() % psize == 0 and grad.data_ptr() % gsize == 0
 
 
 def _moment_tensors(state: Dict[str, Any]) -> List[torch.Tensor]:
@@ -232,6 +272,7 @@ class QuantizedAdamW(Optimizer):
         # Test hook: callable(param, moment, numel, device) -> fp32 uniforms used instead of the
         # on-device Philox draws of a stochastic write (bit-exact comparisons with fed draws).
         self._draw_provider = None
+        self._launch_plan: Optional[_LaunchPlan] = None
         if optimized:
             for group in self.param_groups:
                 group.setdefault(_CHUNK_KEY, _CHUNK_NUMEL)
@@ -255,6 +296,7 @@ class QuantizedAdamW(Optimizer):
             raise ValueError("runtime m1 retargeting received parameters outside optimizer")
         for p in selected:
             self._m1_quant_scheme_overrides[id(p)] = scheme
+        self._launch_plan = None
 
     @staticmethod
     def _eligible_for_quantized_state(p: torch.Tensor, block_size: int) -> bool:
@@ -369,6 +411,7 @@ class QuantizedAdamW(Optimizer):
             restore_hook.remove()
         self._quant_generators = {"m1": {}, "m2": {}}
         self._pending_quant_rng_states = {"m1": {}, "m2": {}}
+        self._launch_plan = None
         if rng_payload is not None:
             if not isinstance(rng_payload, Mapping):
                 raise ValueError("Invalid quantization RNG checkpoint payload")
@@ -430,18 +473,25 @@ class QuantizedAdamW(Optimizer):
         if closure is not None:
             with torch.enable_grad():
                 loss = closure()
-        per_device: Dict[torch.device, List[Tuple]] = {}
-        keep: List[torch.Tensor] = []
+        plan = self._launch_plan
+        if plan is not None and plan.step(self):
+            return loss
+        # per device: launch rows, parameters, written states, read inputs (gradients, draws)
+        per_device: Dict[torch.device, Tuple[List[Tuple], List[torch.Tensor], List[torch.Tensor],
+                                             List[torch.Tensor]]] = {}
+        info: list = []
         for group in self.param_groups:
             for p in group["params"]:
                 if p.grad is None:
                     continue
-                row = self._prepare(p, group, keep)
-                per_device.setdefault(p.device, []).append(row)
-        for device, rows in per_device.items():
-            table = np.array(rows, dtype=_lib.TENSOR)
-            with torch.cuda.device(device):
-                _lib.fused_step(table, torch.cuda.current_stream(device).cuda_stream)
+                rows, params, written, read = per_device.setdefault(p.device, ([], [], [], []))
+                rows.append(self._prepare(p, group, read, written, info))
+                params.append(p)
+        tables = {}
+        for device, (rows, params, written, read) in per_device.items():
+            tables[device] = np.array(rows, dtype=_lib.TENSOR)
+            _ops.fused_step_(params, written, read, torch.from_numpy(tables[device].view(np.uint8)))
+        self._launch_plan = _LaunchPlan.build(self, per_device, tables, info)
         return loss
 
     def _plan_accepts(self, p: torch.Tensor, grad: torch.Tensor, group, requested, schemes, state) -> bool:
@@ -470,7 +520,8 @@ class QuantizedAdamW(Optimizer):
         align = _lib.BLOCK if any(s != "fp32" for s in schemes) else 1
         return limit // align * align
 
-    def _prepare(self, p: torch.Tensor, group, keep: List[torch.Tensor]) -> Tuple:
+    def _prepare(self, p: torch.Tensor, group, keep: List[torch.Tensor], written: List[torch.Tensor],
+                 info: Optional[list] = None) -> Tuple:
         if not p.is_cuda:
             raise NotImplementedError("the fused 4-bit step runs on HIP devices only; move the parameters to the GPU")
         if p.dtype not in _DTYPES:
@@ -529,29 +580,17 @@ class QuantizedAdamW(Optimizer):
         state["step"] = int(state["step"]) + 1
         step = state["step"]
 
-        beta1, beta2 = group["betas"]
-        lr, wd, eps = group["lr"], group["weight_decay"], group["eps"]
-        bias1, bias2 = 1 - beta1 ** step, 1 - beta2 ** step
-        storage_bias = 1 - beta2 ** (step + 1) if schemes[1] in NEXT_BIAS_SCHEMES else bias2
-        flags = 0
-        w1, w2 = np.float32(1 - beta1), np.float32(1 - beta2)
-        if not abs(w1) < 0.5:  # ATen lerp switches formulas at |weight| >= 0.5
-            flags |= _lib.TENSOR_LERP1_LARGE
-            w1 = w1 - np.float32(1.0)
-        if not abs(w2) < 0.5:
-            flags |= _lib.TENSOR_LERP2_LARGE
-            w2 = w2 - np.float32(1.0)
-        psize = 4 * (4 if p.dtype == torch.float32 else 2)
-        gsize = 4 * (4 if grad.dtype == torch.float32 else 2)
-        if p.data_ptr() % psize == 0 and grad.data_ptr() % gsize == 0:
+        c = _step_constants(group, step, schemes[1])
+        flags = c.lerp_flags
+        if _vec_aligned(p, grad):
             flags |= _lib.TENSOR_VEC_ALIGNED
-        bc2_sqrt = _f32(math.sqrt(bias2))
-        m1 = self._moment_row(p, state, "m1", schemes[0], False, optimized, 1.0, 1e-8, keep)
+        m1 = self._moment_row(p, state, "m1", schemes[0], False, optimized, 1.0, 1e-8, keep, written)
         m2 = self._moment_row(p, state, "m2", schemes[1], group["use_eden_m2"], optimized,
-                              storage_bias, eps, keep)
+                              c.storage_bias, group["eps"], keep, written)
+        if info is not None:
+            info.append((p, optimized, schemes))
         return (p.data_ptr(), grad.data_ptr(), n, _DTYPES[p.dtype], _DTYPES[grad.dtype], flags,
-                float(w1), float(w2), _f32(1 - lr * wd), _f32(-lr / bias1), bc2_sqrt, _rcp32(bc2_sqrt),
-                _f32(eps), m1, m2)
+                c.w1, c.w2, c.decay, c.step_coef, c.bc2_sqrt, c.bc2_sqrt_rcp, c.eps, m1, m2)
 
     def _init_moment(self, p, state, moment, scheme, size, eden, chunk) -> None:
         """Zero state (``_moment_buffer.py:89-126`` / ``adamw.py:524-545``)."""
@@ -604,9 +643,10 @@ class QuantizedAdamW(Optimizer):
         state[f"{moment}_code"] = codes
         meta.packed = True
 
-    def _moment_row(self, p, state, moment, scheme, eden, optimized, bias, eps, keep) -> Tuple:
+    def _moment_row(self, p, state, moment, scheme, eden, optimized, bias, eps, keep, written) -> Tuple:
         n = p.numel()
         if scheme == "fp32":
+            written.append(state[moment])
             return (0, 0, state[moment].data_ptr(), 0, 0, 0, 0, _lib.ROUND_FP32, 0, 1.0, 1.0, _f32(1e-8))
         codebook, rounding, floor_zero = SCHEMES[scheme]
         flags = (_lib.MOMENT_ZERO_FLOOR if floor_zero else 0) | (_lib.MOMENT_EDEN if eden else 0)
@@ -625,8 +665,157 @@ class QuantizedAdamW(Optimizer):
                 draws = u.data_ptr()
                 flags |= _lib.MOMENT_EXT_DRAWS
         sr_bias = _f32(max(float(bias), 1e-12))
+        written.append(state[f"{moment}_code"])
+        written.append(state[f"{moment}_quant_state"].absmax)
         return (state[f"{moment}_code"].data_ptr(), state[f"{moment}_quant_state"].absmax.data_ptr(), 0, draws,
                 seed, offset, codebook, rounding, flags, sr_bias, _rcp32(sr_bias), _f32(eps))
+
+
+class _LaunchPlan:
+    """Launch tables of the last full step, reused by the next steps while only per-step values
+    change: gradient addresses, step counts, the fp32 step constants (one per group and step,
+    computed by the same code as the full path), random-stream positions and the update-SR
+    storage bias.  Any structural change -- other parameters with gradients, new state
+    objects, other schemes or chunking in a group, an m1 retarget, a checkpoint load, a draw
+    provider, a gradient that is not contiguous or overlaps its parameter or state -- sends
+    the step through the full path, which rebuilds the plan.  (A gradient always has its
+    parameter's dtype, shape and device: the ``.grad`` setter enforces it.)
+    """
+
+    _STRUCTURE_KEYS = ("m1_quant_scheme", "m2_quant_scheme", "use_eden_m2", "block_size", _CHUNK_KEY)
+    _STATE_KEYS = ("m1", "m2", "m1_code", "m2_code", "m1_quant_state", "m2_quant_state")
+    _MAX_RANGES = 5  # a parameter and its writable moment tensors
+
+    def __init__(self):
+        self.groups: list = []     # (group, structure, parameter count)
+        self.params: List[torch.Tensor] = []
+        self.devices: list = []    # per device: table, params, written, rows
+
+    @classmethod
+    def _state_ids(cls, state) -> tuple:
+        ids = [id(state.get(k)) for k in cls._STATE_KEYS]
+        for k in ("m1_quant_state", "m2_quant_state"):
+            q = state.get(k)
+            ids.append(id(q.absmax) if isinstance(q, QuantState) else 0)
+        ids.append(state.get(_FALLBACK_KEY, False))
+        return tuple(ids)
+
+    @classmethod
+    def build(cls, opt: "QuantizedAdamW", per_device, tables, info) -> Optional["_LaunchPlan"]:
+        if opt._draw_provider is not None:
+            return None
+        plan = cls()
+        meta = {id(p): schemes for p, _, schemes in info}
+        group_of = {}
+        for gi, group in enumerate(opt.param_groups):
+            plan.groups.append((group, tuple(group.get(k) for k in cls._STRUCTURE_KEYS), len(group["params"])))
+            for p in group["params"]:
+                group_of[id(p)] = gi
+        for device, (rows, params, written, read) in per_device.items():
+            n = len(params)
+            lo = np.zeros((n, cls._MAX_RANGES), dtype=np.int64)
+            hi = np.zeros((n, cls._MAX_RANGES), dtype=np.int64)
+            entries = []
+            for i, p in enumerate(params):
+                state = opt.state[p]
+                schemes = meta[id(p)]
+                ranges = [_byte_range(t)[1:] for t in [p] + _moment_tensors(state)]
+                if len(ranges) > cls._MAX_RANGES:
+                    return None
+                # The full path decided this parameter's semantics with this gradient; the plan
+                # repeats that decision only for contiguous gradients that overlap nothing.
+                g = p.grad
+                g0 = g.data_ptr()
+                g1 = g0 + g.numel() * g.element_size()
+                if not g.is_contiguous() or any(a < g1 and g0 < b for a, b in ranges):
+                    return None
+                for k, (a, b) in enumerate(ranges):
+                    lo[i, k], hi[i, k] = a, b
+                sr = tuple((moment, opt._stream(moment, p.device))
+                           for moment, scheme in (("m1", schemes[0]), ("m2", schemes[1]))
+                           if scheme != "fp32" and SCHEMES[scheme][1] in (ROUND_STATE_SR, ROUND_UPDATE_SR))
+                entries.append((p, state, cls._state_ids(state), group_of[id(p)], schemes[1], sr, p.numel()))
+            table = tables[device]
+            gbytes = np.array([p.numel() * p.element_size() for p in params], dtype=np.int64)
+            pvec = np.array([p.data_ptr() % (4 * p.element_size()) == 0 for p in params], dtype=bool)
+            gvec = np.array([4 * p.element_size() for p in params], dtype=np.int64)
+            plan.devices.append((table, list(params), list(written), entries, lo, hi, gbytes, pvec, gvec))
+            plan.params.extend(params)
+        return plan
+
+    def _valid(self, opt: "QuantizedAdamW"):
+        """Per-device gradient addresses if the plan still describes this step, else None."""
+        if opt._draw_provider is not None or len(self.groups) != len(opt.param_groups):
+            return None
+        params = self.params
+        i = 0
+        for (group, structure, count), current in zip(self.groups, opt.param_groups):
+            if current is not group or len(group["params"]) != count:
+                return None
+            if tuple(group.get(k) for k in self._STRUCTURE_KEYS) != structure:
+                return None
+            for p in group["params"]:
+                if p.grad is None:
+                    continue
+                if i >= len(params) or p is not params[i]:
+                    return None
+                i += 1
+        if i != len(params):
+            return None
+        state_ids = self._state_ids
+        state_map = opt.state
+        strided = torch.strided
+        out = []
+        for table, dparams, written, entries, lo, hi, gbytes, pvec, gvec in self.devices:
+            for p, state, ids, _, _, _, _ in entries:
+                if state_map.get(p) is not state or type(state.get("step")) is not int or state_ids(state) != ids:
+                    return None
+                g = p.grad
+                if g.layout != strided or not g.is_contiguous():
+                    return None
+            g0 = np.fromiter((p.grad.data_ptr() for p in dparams), dtype=np.int64, count=len(dparams))
+            g1 = g0 + gbytes
+            if bool(((lo < g1[:, None]) & (g0[:, None] < hi)).any()):
+                return None
+            out.append(g0)
+        return out
+
+    def step(self, opt: "QuantizedAdamW") -> bool:
+        """Launch the step from the cached tables; False (nothing changed) if the plan is stale."""
+        grads = self._valid(opt)
+        if grads is None:
+            return False
+        constants: Dict[Tuple[int, int], _StepConstants] = {}
+        for (table, params, written, entries, lo, hi, gbytes, pvec, gvec), g0 in zip(self.devices, grads):
+            per_row = []
+            offsets = {"m1": table["m1"]["rng_offset"].copy(), "m2": table["m2"]["rng_offset"].copy()}
+            for i, (p, state, _, gi, m2_scheme, sr, numel) in enumerate(entries):
+                step = state["step"] + 1
+                state["step"] = step
+                c = constants.get((gi, step))
+                if c is None:
+                    c = constants[(gi, step)] = _StepConstants(self.groups[gi][0], step, m2_scheme)
+                    sr_bias = _f32(max(float(c.storage_bias), 1e-12))
+                    c.rows = (c.w1, c.w2, c.decay, c.step_coef, c.bc2_sqrt, c.bc2_sqrt_rcp, c.eps,
+                              sr_bias, _rcp32(sr_bias), c.eps, c.lerp_flags)
+                per_row.append(c.rows)
+                for moment, stream in sr:
+                    offsets[moment][i] = stream.take(numel)
+            cols = np.array(per_row, dtype=np.float64).T
+            table["grad"] = g0.astype(np.uint64)
+            aligned = pvec & (g0 % gvec == 0)
+            table["flags"] = cols[10].astype(np.int32) | np.where(aligned, _lib.TENSOR_VEC_ALIGNED, 0)
+            for k, name in enumerate(("w1", "w2", "decay", "step_coef", "bc2_sqrt", "bc2_sqrt_rcp", "eps")):
+                table[name] = cols[k].astype(np.float32)
+            m1, m2 = table["m1"], table["m2"]  # views into the table
+            quantized = m2["rounding"] != _lib.ROUND_FP32
+            for k, name in enumerate(("sr_bias", "sr_bias_rcp", "sr_eps")):
+                m2[name] = np.where(quantized, cols[7 + k].astype(np.float32), m2[name])
+            m1["rng_offset"] = offsets["m1"]
+            m2["rng_offset"] = offsets["m2"]
+            read = [p.grad for p in params]
+            _ops.fused_step_(params, written, read, torch.from_numpy(table.view(np.uint8)))
+        return True
 
 
 class AdamW8bit(QuantizedAdamW):

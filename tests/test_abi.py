@@ -221,3 +221,21 @@ def test_aten_elementwise_semantics():
     t1, t2 = m.numpy(), np.abs(g.numpy()) + np.float32(1e-3)
     got = torch.from_numpy(np.ones_like(t1)).addcdiv_(m, torch.from_numpy(t2), value=-1e-3).numpy()
     assert np.array_equal(got, np.float32(1) + (np.float32(-1e-3) * t1) / t2)
+
+
+def test_torch_custom_op_schema_and_argument_checks():
+    """The launch is the torch operator adamw4bit_hip::fused_step_: it declares the tensors it
+    writes (parameters, moment states) and reads (gradients, draws), and checks its table."""
+    import torch
+
+    import adamw4bit_amd  # noqa: F401  (registers the operator)
+
+    op = torch.ops.adamw4bit_hip.fused_step_
+    schema = str(op.default._schema)
+    assert schema.startswith("adamw4bit_hip::fused_step_(Tensor(a0!)[] params, Tensor(a1!)[] states, "
+                             "Tensor[] inputs, Tensor table)")
+    op([], [], [], torch.zeros(0, dtype=torch.uint8))  # nothing to launch
+    with pytest.raises(ValueError, match="CPU uint8 tensor"):
+        op([torch.zeros(4)], [], [], torch.zeros(208, dtype=torch.float32))
+    with pytest.raises(ValueError, match="HIP devices only"):
+        op([torch.zeros(4)], [], [], torch.zeros(208, dtype=torch.uint8))

@@ -320,6 +320,19 @@ def test_scheme_groups_reference_step():
     compare_pair(*out, "scheme groups")
 
 
+def test_gpt2_small_shaped_list_zeeden():
+    """GPT-2-small shapes (full 50257x768 embedding, 1024x768 positions, two full-width layers):
+    matrices take the 4-bit path and the 768/2304/3072 LayerNorm and bias vectors the fp32-state
+    path, in one launch."""
+    log("gpt2-small-shaped list, ZE-EDEN x 3 steps")
+    d = 768
+    layer = [(d,), (d,), (d, 3 * d), (3 * d,), (d, d), (d,), (d,), (d,), (d, 4 * d), (4 * d,), (4 * d, d), (d,)]
+    shapes = [(50257, d), (1024, d)] + layer * 2 + [(d,), (d,)]
+    args = dict(lr=6e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True)
+    out = run_pair(lambda ps: aw.ZEEDENAdamW4Bit(ps, **args), shapes, torch.float32, 3, seed=None)
+    compare_pair(*out, "gpt2-small shapes", steps=3)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_mixed_recipes_split_launches(dtype):
     """One optimizer whose tensors need different kernels (ZE-EDEN and ZIP-SR recipe schemes, an
@@ -338,6 +351,47 @@ def test_mixed_recipes_split_launches(dtype):
                                  m1_quant_scheme="nf4", m2_quant_scheme="dyn4_nz", quant_rng_seed=5, optimized=True)
     out = run_pair(make, shapes, dtype, 4, seed=5, m1_override=([6], "nf4_sr"), zero_block_frac=0.02)
     compare_pair(*out, f"mixed recipes {dtype}", steps=4)
+
+
+def test_launch_plan_reuse_matches_full_path():
+    """Steps reusing the previous step's launch tables are bit-identical to steps that rebuild
+    them, through a learning-rate change, a parameter without gradient, and an m1 retarget."""
+    log("launch plan reuse vs full path")
+    shapes = [(256, 512), (768,), (64, 1024), (1000,), (128, 384)]
+    gen = torch.Generator().manual_seed(21)
+    init = [torch.randn(s, generator=gen) * 0.02 for s in shapes]
+    pa = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
+    pb = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
+    args = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True, quant_rng_seed=4)
+    oa, ob = aw.ZIPSRAdamW4Bit(pa, **args), aw.ZIPSRAdamW4Bit(pb, **args)
+    reused = 0
+    for k in range(7):
+        for a, b, s in zip(pa, pb, shapes):
+            g = H.heavy_tailed(s, gen).to(H.DEVICE)
+            a.grad, b.grad = g.clone(), g.clone()
+        if k == 3:
+            pa[2].grad = pb[2].grad = None
+        if k == 4:
+            for o in (oa, ob):
+                o.param_groups[0]["lr"] = 5e-4
+        if k == 5:
+            oa.set_m1_quant_scheme_for_parameters([pa[0]], "nf4_sr")
+            ob.set_m1_quant_scheme_for_parameters([pb[0]], "nf4_sr")
+        before = oa._launch_plan
+        oa.step()
+        reused += int(before is not None and oa._launch_plan is before)
+        ob._launch_plan = None  # always the full path
+        ob.step()
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(pa, pb)):
+            assert torch.equal(H.bits(a), H.bits(b)), (k, i)
+            sa, sb = H.state_of(oa, a), H.state_of(ob, b)
+            assert sa.keys() == sb.keys() and sa["step"] == sb["step"], (k, i)
+            for key in sa:
+                if key != "step":
+                    assert torch.equal(H.bits(sa[key]), H.bits(sb[key])), (k, i, key)
+    log(f"  plan reused on {reused} of 7 steps")
+    assert reused >= 3
 
 
 def test_lerp_large_weight_betas():
