@@ -123,9 +123,17 @@ def cpu_baseline(seconds_target: float = 12.0):
         times.append(time.perf_counter() - t0)
     per_step = statistics.median(times)
     n = p.numel()
+    cpu = "unknown CPU"
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu = next(line.split(":", 1)[1].strip() for line in f if line.startswith("model name"))
+    except (OSError, StopIteration):
+        pass
     return {"value": n / per_step / 1e9, "unit": "Gelem/s", "cores": torch.get_num_threads(), "kind": "port",
             "sample": f"oracle ZE-EDEN eager chunk update, fp32 4096x4096 (16.8M values), median of {len(times)} "
-                      f"steps, {per_step * 1e3:.1f} ms/step, {torch.get_num_threads()} threads"}
+                      f"steps, {per_step * 1e3:.1f} ms/step, {torch.get_num_threads()} threads "
+                      f"(os.cpu_count {os.cpu_count()}, OMP_NUM_THREADS {os.environ.get('OMP_NUM_THREADS')}), "
+                      f"{cpu}, ATen {torch.backends.cpu.get_cpu_capability()}"}
 
 
 def measured_traffic(config: str):

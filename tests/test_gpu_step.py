@@ -455,6 +455,35 @@ def test_state_dict_resume_is_exact(tmp_path):
                 assert torch.equal(H.bits(sa[key]), H.bits(sc[key])), key
 
 
+def test_legacy_unpacked_codes_are_repacked():
+    """Quantized state holding one code per byte (unpacked, as older checkpoints store it,
+    _moment_buffer.py:127-141) is packed on the next step and continues bit-exactly."""
+    log("legacy unpacked codes")
+    gen = torch.Generator().manual_seed(8)
+    shape = (128, 256)
+    init = torch.randn(shape, generator=gen) * 0.02
+    grads = [H.heavy_tailed(shape, gen) for _ in range(4)]
+    a = torch.nn.Parameter(init.clone().to(H.DEVICE))
+    b = torch.nn.Parameter(init.clone().to(H.DEVICE))
+    oa, ob = aw.ZEEDENAdamW4Bit([a], optimized=True), aw.ZEEDENAdamW4Bit([b], optimized=True)
+    for k in range(4):
+        if k == 2:
+            st = ob.state[b]
+            for m in ("m1", "m2"):
+                st[f"{m}_code"] = q.unpack_4bit_codes(st[f"{m}_code"], numel=b.numel()).to(torch.uint8)
+                st[f"{m}_quant_state"].packed = False
+        for p, o in ((a, oa), (b, ob)):
+            p.grad = grads[k].to(H.DEVICE)
+            o.step()
+    torch.cuda.synchronize()
+    assert torch.equal(H.bits(a), H.bits(b))
+    sa, sb = H.state_of(oa, a), H.state_of(ob, b)
+    for key in sa:
+        if key != "step":
+            assert torch.equal(H.bits(sa[key]), H.bits(sb[key])), key
+    assert ob.state[b]["m1_code"].numel() == (b.numel() + 1) // 2 and ob.state[b]["m1_quant_state"].packed
+
+
 def test_reference_checkpoint_loads_on_gpu():
     """A state_dict written by the reference (CPU) loads onto GPU parameters; its CPU RNG
     streams cannot move to another device type, as in the reference (adamw.py:306-320)."""
