@@ -39,8 +39,9 @@ constexpr int kLutRtn[AW4_NUM_CODEBOOKS] = {0, 1, 2, 3, 4};
 constexpr int kLutRtnDyn4Floor = 5;
 constexpr int kLutLevels[AW4_NUM_CODEBOOKS] = {6, 7, 8, 9, 10};
 
-// Bucket of x -> code = base + (x >= thr).  For round-to-nearest tables lv_lo/lv_hi are
-// the levels of codes base and base + 1 (what EDEN multiplies by).
+// Bucket of x -> code = base + (x >= thr); lv_lo / lv_hi are cb[min(code, 15)] of the two
+// outcomes: the code's level in round-to-nearest tables (what EDEN multiplies by), the
+// upper neighbour b of x in level-count tables.
 struct __align__(16) LutEntry {
     float thr;
     uint32_t base;
@@ -57,11 +58,10 @@ struct __align__(16) PairEntry {
 };
 
 // Per-block update-SR quantities for each searchsorted index (update_sr_tables()).
-struct __align__(16) UpdEntry {
-    float f_hi;     // preconditioner at the upper level
-    float den;      // max(f(lo) - f(hi), 1e-30)
-    float den_rcp;  // RN(1 / den) where the interval is valid ((b > a) & (f(lo) - f(hi) > 0)), else -1
-    float b;        // the upper level
+struct __align__(8) UpdEntry {
+    float f_hi;   // preconditioner at the upper level
+    float den_u;  // max(f(lo) - f(hi), 1e-30) * 2^-24 where the interval is valid
+                  // ((b > a) & (f(lo) - f(hi) > 0)), else -1
 };
 
 // All tables of all codebooks, built on the host and kept in device memory.
@@ -127,8 +127,8 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 // Per-block update-SR tables (_compiled_quantization.py:74-109): for every
-// searchsorted index i, f(hi), max(f(lo) - f(hi), 1e-30), its reciprocal (negative
-// marks an invalid interval) and the upper level, with f(l) = 1 / (sqrt(max((s * l) / bias, 0)) + eps).
+// searchsorted index i, f(hi) and max(f(lo) - f(hi), 1e-30) / 2^24 (negative marks an
+// invalid interval), with f(l) = 1 / (sqrt(max((s * l) / bias, 0)) + eps).
 __device__ __forceinline__ void update_sr_tables(const MomentTables& L, int j, float s, float bias, float bias_rcp,
                                                  float eps, UpdEntry* upd, float* pre) {
 #pragma unroll
@@ -149,24 +149,23 @@ __device__ __forceinline__ void update_sr_tables(const MomentTables& L, int j, f
         const float dc = clamp_min_nan(den, 1e-30f);
         UpdEntry e;
         e.f_hi = fhi;
-        e.den = dc;
-        e.den_rcp = (pe.b > pe.a && den > 0.0f) ? div_cr(1.0f, dc) : -1.0f;  // dc >= 1e-30: normal
-        e.b = pe.b;
+        e.den_u = (pe.b > pe.a && den > 0.0f) ? dc * 0x1p-24f : -1.0f;  // dc >= 1e-30: stays normal
         upd[i] = e;
     }
-    if (j == 0) upd[0] = UpdEntry{0.0f, 1.0f, -1.0f, L.cb[0]};
+    if (j == 0) upd[0] = UpdEntry{0.0f, -1.0f};
     wave_lds_sync();
 }
 
 // Uniforms of this lane's 4 values at offset `off` from value blk0 * 128 of one write of
-// moment M (stream position rng_offset + value index).
+// moment M (stream position rng_offset + value index), scaled by 2^24: U = u * 2^24 is
+// exact for every float u, and an integer in [0, 2^24) for the generator's 24-bit draws.
 __device__ __forceinline__ void draws4(const aw4_moment& M, int64_t blk0, uint32_t off, bool active, float (&u)[4]) {
     if (M.flags & AW4_MOMENT_EXT_DRAWS) {
         f32x4 v = {0.f, 0.f, 0.f, 0.f};
         if (active) v = *(gptr<const f32x4>)(gaddr<const float>(M.draws) + blk0 * kBlock + off);
-        u[0] = v.x; u[1] = v.y; u[2] = v.z; u[3] = v.w;
+        u[0] = v.x * 0x1p24f; u[1] = v.y * 0x1p24f; u[2] = v.z * 0x1p24f; u[3] = v.w * 0x1p24f;
     } else {
-        uniforms4(M.rng_seed, M.rng_offset + (uint64_t)blk0 * kBlock + off, u);
+        uniforms4_scaled(M.rng_seed, M.rng_offset + (uint64_t)blk0 * kBlock + off, u);
     }
 }
 
@@ -186,15 +185,38 @@ __device__ __forceinline__ void draws4(const aw4_moment& M, int64_t blk0, uint32
 // rounding table resolves [-2^-10, 2^-10] to one code or to the level-0 threshold at the
 // smallest subnormal, the preconditioner of such an x equals the one of 0 (eps absorbs
 // it), and its EDEN products vanish next to the block's |x| = 1 element.
+// Update-SR draw test u < P(lo) for one value, with U = u * 2^24 and the table entry of
+// its interval: P(lo) = RN(d / den), d = RN(f(x) - f(b)),
+// f(x) = 1 / (sqrt(max((s * x) / bias, 0)) + eps)  (_compiled_quantization.py:74-97).
+// f(x) and d are rounded as the reference rounds them: where eps dominates the square
+// root, f is nearly flat and P is mostly the rounding of f(x), so that rounding is kept.
+// The final quotient is not formed: u < d / den  <=>  fma(U, den / 2^24, -d) < 0, the
+// exact sign of u * den - d, which differs from u < RN(d / den) only for a draw on the
+// rounding of P itself (about 2^-24 of the values).  Fast form: (s * x) / bias from
+// RN(1 / bias), exact for normal quotients (taken when every block of the wave has a
+// scale below 2^125 and s / bias far from overflow); slow form: IEEE division.
+template <bool kFast, bool kNonNeg>
+__device__ __forceinline__ bool usr_draw_lower(const aw4_moment& M, const UpdEntry& ue, float s, float x, float U) {
+    float v;
+    if constexpr (kFast) v = div_by_rcp(s * x, M.sr_bias, M.sr_bias_rcp);
+    else v = (s * x) / M.sr_bias;
+    if (!kNonNeg || !kFast) v = clamp_min_nan(v, 0.0f);
+    const float z = sqrt_faithful(v) + M.sr_eps;
+    const float fx = kFast ? rcp_faithful(z) : 1.0f / z;
+    return __builtin_fmaf(U, ue.den_u, -(fx - ue.f_hi)) < 0.0f;  // (den / 2^24 is exact)
+}
+
 template <int SPEC, bool kNonNeg>
 __device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTables& L, int64_t blk0, int grp, int j,
                                              bool active, const float (&m)[16], BlockScratch sc) {
-    uint32_t amax = 0u;
+    // NaN-propagating max |m| (v_maximum3_f32 with |.| operands), then over the block's 8 lanes
+    // on the bit patterns (non-negative floats and NaNs order as unsigned integers).
+    float amf = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) amax = max(amax, f2u(m[i]) & 0x7fffffffu);  // NaN-propagating |m| max
-    amax = block_max_u32(amax);
+    for (int i = 0; i < 16; ++i) amf = __builtin_elementwise_maximum(amf, __builtin_fabsf(m[i]));
+    const uint32_t amax = block_max_u32(f2u(amf));
     const float s = u2f(max(amax, 0x2B8CBCCCu));  // max(absmax, fp32(1e-12))
-    const bool fast = s < 0x1p125f;                // otherwise huge, infinite or NaN: IEEE division
+    bool fast = s < 0x1p125f;                      // otherwise huge, infinite or NaN: IEEE division
     const float y = div_cr(1.0f, s);               // RN(1 / s): normal on the fast path
     constexpr int KIND = kind_of(SPEC), MF = flags_of(SPEC);
     constexpr bool kDyn = (MF & kFlagsAtRunTime) != 0;
@@ -202,7 +224,14 @@ __device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTa
     const bool eden = (flags & AW4_MOMENT_EDEN) != 0;
     const bool guards = (flags & AW4_MOMENT_GUARDS) != 0;
     const bool floor0 = (flags & AW4_MOMENT_ZERO_FLOOR) != 0;
-    if constexpr (KIND == K_USR) update_sr_tables(L, j, s, M.sr_bias, M.sr_bias_rcp, M.sr_eps, sc.upd, sc.pre);
+    if constexpr (KIND == K_USR) {
+        update_sr_tables(L, j, s, M.sr_bias, M.sr_bias_rcp, M.sr_eps, sc.upd, sc.pre);
+        fast = fast && s * M.sr_bias_rcp < 0x1p127f;  // (s * x) / bias stays far from overflow
+    }
+    // One branch for the whole wave: the IEEE forms are exact for every block, so a wave
+    // with any huge, infinite or NaN scale runs them for all of its blocks, and the common
+    // case is a scalar branch instead of a divergent one.
+    const bool wave_fast = __builtin_amdgcn_ballot_w64(!fast) == 0;
     wave_lds_sync();  // the stage's previous contents have been read
 
     float acc_xx[4] = {0.0f, 0.0f, 0.0f, 0.0f}, acc_xl[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -210,7 +239,7 @@ __device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTa
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         float x[4];
-        if (__builtin_expect(fast, 1)) {
+        if (__builtin_expect(wave_fast, 1)) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) x[t] = div_by_rcp(m[4 * q + t], s, y);
         } else {
@@ -229,38 +258,61 @@ __device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTa
                 lv[t] = up ? e.lv_hi : e.lv_lo;
             }
         } else {
-            float u[4];
+            float u[4];  // the uniforms times 2^24
             draws4(M, blk0, voff + 32u * q, active, u);
             // Both rules pick level lo = max(idx - 1, 0) or hi = min(idx, 15), idx = number of levels
             // below x.  Since u is in [0, 1), u < clamp(P, 0, 1) == u < P for every P (NaN included),
             // so the clamps of the reference never change a code and the guards become masks.
+            int idx[4];
+            float b[4];  // upper neighbour cb[min(idx, 15)]
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const LutEntry le = L.lut[kNonNeg ? lut_bucket_unsigned(x[t]) : lut_bucket_signed(x[t])];
-                const int idx = (int)le.base + (x[t] >= le.thr ? 1 : 0);
-                bool lower;
-                if constexpr (KIND == K_SSR) {
+                const bool up = x[t] >= le.thr;
+                idx[t] = (int)le.base + (up ? 1 : 0);
+                b[t] = up ? le.lv_hi : le.lv_lo;
+            }
+            bool lower[4];
+            if constexpr (KIND == K_SSR) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
                     // P(hi) = (x - a) / max(b - a, 1e-12), 0 where b == a (there lo == hi); guards
                     // x <= a -> lo, x >= b -> hi (_compiled_quantization.py:60-71).
-                    const PairEntry pe = L.pairs[idx];
+                    const PairEntry pe = L.pairs[idx[t]];
                     const float width = pe.b - pe.a;
                     const float p = div_by_rcp(x[t] - pe.a, width < 1e-12f ? 1e-12f : width, pe.width_rcp);
-                    bool upper = u[t] < p;
-                    if (guards) upper = (upper || x[t] >= pe.b) && !(x[t] <= pe.a);
-                    lower = !upper;
-                } else {
-                    // P(lo) = (f(x) - f(b)) / max(f(a) - f(b), 1e-30), 1 on invalid intervals; guards
-                    // x <= a -> lo, x >= b -> hi (_compiled_quantization.py:74-109).  x <= a holds
-                    // exactly when no level is below x (idx == 0).  For values >= +0 the clamp of
-                    // (s * x) / bias at 0 is the identity.
-                    const UpdEntry ue = sc.upd[idx];
-                    const float v = div_by_rcp(s * x[t], M.sr_bias, M.sr_bias_rcp);
-                    const float fx = rcp_faithful(sqrt_faithful(kNonNeg ? v : clamp_min_nan(v, 0.0f)) + M.sr_eps);
-                    const float p = div_by_rcp(fx - ue.f_hi, ue.den, ue.den_rcp);
-                    lower = !(ue.den_rcp > 0.0f) || u[t] < p;
-                    if (guards) lower = (lower && !(x[t] >= ue.b)) || idx == 0;
+                    bool upper = u[t] < p * 0x1p24f;
+                    if (guards) upper = (upper | (x[t] >= pe.b)) & !(x[t] <= pe.a);
+                    lower[t] = !upper;
                 }
-                code[t] = (uint32_t)min(max(idx - (lower ? 1 : 0), 0), 15);
+            } else {
+                // P(lo) = (f(x) - f(b)) / max(f(a) - f(b), 1e-30), 1 on invalid intervals
+                // (_compiled_quantization.py:74-109).  On a valid interval P is 0 at x == b, so
+                // x >= b picks hi with or without the guards; the guards add x <= a -> lo, which
+                // holds exactly when no level is below x (idx == 0), and let x >= b override an
+                // invalid interval.
+                UpdEntry ue[4];
+                bool dl[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) ue[t] = sc.upd[idx[t]];
+                if (__builtin_expect(wave_fast, 1)) {
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) dl[t] = usr_draw_lower<true, kNonNeg>(M, ue[t], s, x[t], u[t]);
+                } else {
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) dl[t] = usr_draw_lower<false, kNonNeg>(M, ue[t], s, x[t], u[t]);
+                }
+                // Bitwise operators: the operands are all computed, and short-circuit forms
+                // become per-value branches.
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const bool valid = ue[t].den_u > 0.0f, at_b = x[t] >= b[t];
+                    lower[t] = guards ? (((!valid) | dl[t]) & !at_b) | (idx[t] == 0) : (!valid) | (dl[t] & !at_b);
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                code[t] = (uint32_t)min(max(idx[t] - (lower[t] ? 1 : 0), 0), 15);
                 if (floor0) code[t] = max(code[t], 1u);
                 lv[t] = eden ? L.cb[code[t]] : 0.0f;
             }

@@ -188,4 +188,13 @@ __device__ __forceinline__ void uniforms4(uint64_t seed, uint64_t pos, float (&u
     for (int t = 0; t < 4; ++t) u[t] = (float)(r[t] >> 8) * 0x1p-24f;
 }
 
+// The same uniforms times 2^24: the integers r >> 8, as floats (exact).
+__device__ __forceinline__ void uniforms4_scaled(uint64_t seed, uint64_t pos, float (&u)[4]) {
+    const uint64_t ctr = pos >> 2;
+    uint32_t r[4];
+    philox4x32_10((uint32_t)ctr, (uint32_t)(ctr >> 32), (uint32_t)seed, (uint32_t)(seed >> 32), r);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) u[t] = (float)(r[t] >> 8);
+}
+
 }  // namespace aw4

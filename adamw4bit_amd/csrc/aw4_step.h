@@ -133,12 +133,16 @@ __device__ __forceinline__ void moments_update(const aw4_tensor& T, float g, flo
 }
 
 // p = p * (1 - lr*wd) [rounded to storage]; p = p + (-lr/bc1 * m1) / (sqrt(m2) / sqrt(bc2) + eps).
+// The denominator and the quotient are faithful: hardware square root and reciprocal
+// (<= 1 ulp each), so the update term is within 3 ulps of ATen's, whose square root is
+// itself only faithful.  The decayed parameter is exact; the update term is usually
+// far below its ulp.  Zero, infinite and NaN denominators give ATen's results
+// (x * rcp(0) = x / 0, x * rcp(inf) = 0 for finite x).
 template <int D>
 __device__ __forceinline__ float param_update(const aw4_tensor& T, float p, float m1, float m2) {
-    const float sq = sqrt_faithful(m2);
-    const float d = __builtin_amdgcn_div_fixupf(div_by_rcp(sq, T.bc2_sqrt, T.bc2_sqrt_rcp), T.bc2_sqrt, sq) + T.eps;
+    const float d = __builtin_fmaf(sqrt_faithful(m2), T.bc2_sqrt_rcp, T.eps);
     const float p1 = round_to_storage<D>(p * T.decay);
-    return p1 + div_cr(T.step_coef * m1, d);
+    return p1 + (T.step_coef * m1) * __builtin_amdgcn_rcpf(d);
 }
 
 // ---------------------------------------------------------------------------

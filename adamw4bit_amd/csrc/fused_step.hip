@@ -281,7 +281,8 @@ struct HostTables {
 
 // Build one lookup table: bucket -> (threshold, base) such that f(x) = base + (x >= threshold)
 // for every fp32 x of the bucket, where f is monotone non-decreasing in x.  Fails if a
-// bucket holds more than one change of f.  `cb` (optional) fills the entry's levels.
+// bucket holds more than one change of f.  The entry's levels are cb[min(f, 15)] for both
+// outcomes: the code's level (round-to-nearest) or the upper neighbour b of x (level count).
 template <class F>
 bool build_lut(LutEntry* out, F f, const float* cb, std::string& err) {
     for (int sign = 0; sign < 2; ++sign) {
@@ -320,8 +321,8 @@ bool build_lut(LutEntry* out, F f, const float* cb, std::string& err) {
                 err = buf;
                 return false;
             }
-            e.lv_lo = cb ? cb[base < 15 ? base : 15] : 0.0f;
-            e.lv_hi = cb ? cb[base + 1 < 15 ? base + 1 : 15] : 0.0f;
+            e.lv_lo = cb[base < 15 ? base : 15];
+            e.lv_hi = cb[base + 1 < 15 ? base + 1 : 15];
             out[k + sign * AW4_LUT_HALF] = e;
         }
     }
@@ -351,7 +352,7 @@ const HostTables& host_tables() {
         for (int c = 0; c < AW4_NUM_CODEBOOKS && ok; ++c) {
             const float* cb = t.codebook[c];
             ok = build_lut(t.lut[kLutRtn[c]], [cb](float x) { return rtn_code(cb, x, false); }, cb, h.error) &&
-                 build_lut(t.lut[kLutLevels[c]], [cb](float x) { return count_less(cb, x); }, nullptr, h.error);
+                 build_lut(t.lut[kLutLevels[c]], [cb](float x) { return count_less(cb, x); }, cb, h.error);
         }
         if (ok) {
             const float* cb = t.codebook[AW4_CB_DYN4];

@@ -159,8 +159,9 @@ int aw4_uniforms(uint64_t seed, uint64_t offset, int64_t n, float* out, void* st
  * out = 0 to query) or a negative error.  Layout: for each of AW4_NUM_LUTS
  * tables, AW4_LUT_ENTRIES entries {float threshold; uint32 base; float
  * level_lo; float level_hi}: a value x in bucket k (bucket function below)
- * encodes to base + (x >= threshold), whose codebook level is level_lo or
- * level_hi (round-to-nearest tables; 0 in the level-count tables).
+ * encodes to base + (x >= threshold); level_lo and level_hi are the levels
+ * cb[min(code, 15)] of the two outcomes (round-to-nearest tables: the code's
+ * level; level-count tables: the upper neighbour of x).
  * Tables 0..5: round-to-nearest codes for nf4, sdyn4, dyn4, lin4, lin4_nz,
  * dyn4 with the zero floor; tables 6..10: searchsorted-left counts
  * (number of levels < x) for nf4, sdyn4, dyn4, lin4, lin4_nz.

@@ -113,7 +113,8 @@ def lut_eval(tables, lut_id, x):
 
 
 def lut_level(tables, lut_id, x):
-    """Level of the encoded code as the kernel reads it from the entry."""
+    """Level the kernel reads from the entry: the code's level (round-to-nearest tables) or
+    the upper neighbour cb[min(count, 15)] (level-count tables)."""
     u = x.view(np.uint32).astype(np.int64)
     k = np.clip(((u & 0x7FFFFFFF) >> 20) - (_lib.LUT_EXP0 - 1), 0, _lib.LUT_HALF - 1)
     idx = k + (u >> 31) * _lib.LUT_HALF
@@ -163,6 +164,7 @@ def test_encode_tables_reproduce_rounding_rules(mode, cb_id):
     count, rtn = reference_rules(cb, x)
     assert np.array_equal(lut_eval(tables, cb_id, x), rtn)                 # round-to-nearest table
     assert np.array_equal(lut_eval(tables, 6 + cb_id, x), count)           # level-count table
+    assert np.array_equal(lut_level(tables, 6 + cb_id, x), cb[np.minimum(count, 15)])  # its upper level b
     assert np.array_equal(lut_level(tables, cb_id, x), cb[rtn])            # the level EDEN uses
     if mode == "dyn4":
         floored = np.maximum(rtn, 1)

@@ -3,10 +3,12 @@
 Bars (stated per comparison):
 * codes and block scales of round-to-nearest moments: bit-exact;
 * codes of stochastic moments fed the same uniforms: bit-exact up to draws that fall
-  between two probabilities one sqrt-ulp apart (budget 1e-5 of the codes);
+  between two probabilities a few ulps apart (faithful square root and reciprocal;
+  budget 1e-5 of the codes);
 * fp32-state moments: bit-exact;
 * parameters: within 1e-6 relative (fp32) / one storage ulp (bf16, fp16), because the
-  reference's CPU square root is up to 1 ulp below the correctly rounded one.
+  reference's CPU square root is up to 1 ulp below the correctly rounded one and the
+  kernel's update term is faithful (within 3 ulps).
 """
 
 from __future__ import annotations
