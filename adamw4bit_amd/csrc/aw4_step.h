@@ -322,11 +322,11 @@ __device__ __forceinline__ void update_tile(const aw4_tensor& T, const TileInput
     }
 }
 
+// Decode, update and store the parameters of one tile; the new moments go to m1/m2.
 template <int M1K, int M2K, int D>
-__device__ __forceinline__ void compute_tile(const aw4_tensor& T, const TileLane& tl,
-                                             const TileInputs<M1K, M2K, D>& in, const MomentTables& L1,
-                                             const MomentTables& L2, WaveScratch& ws) {
-    float m1[16], m2[16];
+__device__ __forceinline__ void update_tile_any(const aw4_tensor& T, const TileLane& tl,
+                                                const TileInputs<M1K, M2K, D>& in, const MomentTables& L1,
+                                                const MomentTables& L2, float (&m1)[16], float (&m2)[16]) {
     if constexpr (D == D_ANY) {
         if (T.param_dtype == D_F32) update_tile<M1K, M2K, D, D_F32>(T, in, L1, L2, tl, m1, m2);
         else if (T.param_dtype == D_BF16) update_tile<M1K, M2K, D, D_BF16>(T, in, L1, L2, tl, m1, m2);
@@ -334,21 +334,21 @@ __device__ __forceinline__ void compute_tile(const aw4_tensor& T, const TileLane
     } else {
         update_tile<M1K, M2K, D, D>(T, in, L1, L2, tl, m1, m2);
     }
-    auto finish = [&](const aw4_moment& M, const MomentTables& L, const float (&m)[16], auto kind, auto nonneg) {
-        constexpr int MK = decltype(kind)::value;
-        if (moment_quantized<MK>(M)) {
-            if constexpr (kind_of(MK) != K_FP32)
-                encode_moment<MK, decltype(nonneg)::value>(M, L, tl, m, ws.block(tl.grp));
-        } else if (tl.active) {
-            const gptr<float> vals_tile = gaddr<float>(M.values) + tl.blk0 * kBlock;
+}
+
+// Encode (or store, for an fp32-state moment) one moment of a tile.
+template <int MK, bool kNonNeg>
+__device__ __forceinline__ void finish_moment(const aw4_moment& M, const MomentTables& L, const TileLane& tl,
+                                              const float (&m)[16], WaveScratch& ws) {
+    if (moment_quantized<MK>(M)) {
+        if constexpr (kind_of(MK) != K_FP32) encode_moment<MK, kNonNeg>(M, L, tl, m, ws.block(tl.grp));
+    } else if (tl.active) {
+        const gptr<float> vals_tile = gaddr<float>(M.values) + tl.blk0 * kBlock;
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-                __builtin_nontemporal_store(f32x4{m[4 * q], m[4 * q + 1], m[4 * q + 2], m[4 * q + 3]},
-                                            (gptr<f32x4>)(vals_tile + tl.voff + 32u * q));
-        }
-    };
-    finish(T.m1, L1, m1, std::integral_constant<int, M1K>(), std::false_type());
-    finish(T.m2, L2, m2, std::integral_constant<int, M2K>(), std::true_type());
+        for (int q = 0; q < 4; ++q)
+            __builtin_nontemporal_store(f32x4{m[4 * q], m[4 * q + 1], m[4 * q + 2], m[4 * q + 3]},
+                                        (gptr<f32x4>)(vals_tile + tl.voff + 32u * q));
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -404,47 +404,93 @@ __device__ void step_tile_values(const aw4_tensor& T, int64_t e_tile, int lane) 
 }
 
 // ---------------------------------------------------------------------------
-// The kernel: each wave processes kTilesPerWave consecutive wave tiles (the header's
-// tiles_per_wave); the grid covers every tile.  Latency is hidden by occupancy (several
-// waves per SIMD, each with a tile's loads in flight) rather than by holding a second
-// tile in registers, which would halve the waves that fit.
+// The kernel: wave w of a grid of W waves processes tiles w, w + W, w + 2W, ... (at most
+// the header's tiles_per_wave; the grid covers every tile).  The waves resident at any
+// moment have consecutive indices, so the tiles in flight are adjacent in memory, while
+// each workgroup's table load is shared by several tiles per wave.  Latency is hidden by
+// occupancy (several waves per SIMD) and by issuing the next tile's loads as soon as the
+// current tile's inputs are dead (after the parameter update and the first moment's
+// encode): the second moment's encode then overlaps them, and its code and scale stores
+// queue behind them, so waiting for those loads does not wait for these stores (on gfx9
+// one counter covers both, in issue order).
 // ---------------------------------------------------------------------------
 
 __device__ __forceinline__ bool values_only(const aw4_tensor& T) {
     return (!is_quantized(T.m1) && !is_quantized(T.m2)) || (T.numel & (kBlock - 1)) != 0;
 }
 
-template <int M1K, int M2K, int D, class LdsT>
-__device__ __forceinline__ void run_tiles(const StepHeader* hdr, const LdsT& lds_tables, WaveScratch& ws) {
-    const aw4_tensor* tensors = (const aw4_tensor*)(hdr + 1);
-    const int64_t* tile_start = (const int64_t*)(tensors + hdr->count);
-    const int lane = threadIdx.x & 63;
-    const int64_t wave = (int64_t)blockIdx.x * kWavesPerGroup + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int64_t total = hdr->total_tiles;
-    int64_t tile = wave * hdr->tiles_per_wave;
-    const int64_t end = min(tile + hdr->tiles_per_wave, total);
-    if (tile >= end) return;
+// Tile order: grid order (wave w takes tiles w, w + W, ...) or consecutive tiles per wave
+// (w * K .. w * K + K - 1).  Prefetch: the next tile's loads are issued during the second
+// moment's encode.  Both keep the in-flight tiles of a memory-bound kernel adjacent and
+// its loads early; a kernel bound by its arithmetic (update-SR) pays for the prefetched
+// registers and runs the plain order.  The generic kernel (run-time kinds and dtype) has
+// the register pressure of every variant at once and loads each tile when it starts it.
+constexpr bool prefetch_next_tile(int m1k, int m2k, int d) {
+    return kind_of(m1k) != K_ANY && kind_of(m2k) != K_ANY && d != D_ANY && kind_of(m2k) != K_USR;
+}
+constexpr bool tile_order_grid(int m1k, int m2k, int d) { return prefetch_next_tile(m1k, m2k, d); }
 
-    int lo = 0, hi = hdr->count - 1;  // tensor of `tile`: last ti with tile_start[ti] <= tile
+// Index of the tensor holding `tile` >= tile_start[lo]: the last ti in [lo, count) with
+// tile_start[ti] <= tile (one load when it is still tensor lo, else a binary search).
+__device__ __forceinline__ int tensor_of(const int64_t* tile_start, int lo, int count, int64_t tile) {
+    if (tile < tile_start[lo + 1]) return lo;
+    ++lo;
+    int hi = count - 1;
     while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
         if (tile_start[mid] <= tile) lo = mid; else hi = mid - 1;
     }
-    int ti = lo;
-    for (; tile < end; ++tile) {
-        while (tile >= tile_start[ti + 1]) ++ti;
+    return lo;
+}
+
+template <int M1K, int M2K, int D, class LdsT>
+__device__ __forceinline__ void run_tiles(const StepHeader* hdr, const LdsT& lds_tables, WaveScratch& ws) {
+    const aw4_tensor* tensors = (const aw4_tensor*)(hdr + 1);
+    const int count = hdr->count;
+    const int64_t* tile_start = (const int64_t*)(tensors + count);
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = (int64_t)blockIdx.x * kWavesPerGroup + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // Tile order and prefetch of this variant (tile_order_grid, prefetch_next_tile).
+    constexpr bool kGridOrder = tile_order_grid(M1K, M2K, D), kPrefetch = prefetch_next_tile(M1K, M2K, D);
+    const int64_t stride = kGridOrder ? (int64_t)gridDim.x * kWavesPerGroup : 1;
+    const int64_t total = hdr->total_tiles;
+    const int64_t per_wave = hdr->tiles_per_wave;
+    int64_t tile = kGridOrder ? wave : wave * per_wave;
+    if (tile >= total) return;
+    int ti = tensor_of(tile_start, 0, count, tile);
+    TileInputs<M1K, M2K, D> in;
+    bool loaded = false;  // `in` holds this tile's inputs (prefetched by the previous one)
+    for (int64_t k = 0;;) {
         const aw4_tensor& T = tensors[ti];
         const int64_t local = tile - tile_start[ti];
+        const int64_t next = tile + stride;
+        const bool more = ++k < per_wave && next < total;
+        int tn = -1;  // tensor of `next`, once searched
         if (values_only(T)) {
             step_tile_values<D>(T, local * kWaveTile, lane);
-            continue;
+            loaded = false;
+        } else {
+            const TileLane tl = tile_lane(T, local * kBlocksPerWave, lane);
+            if (!loaded) load_tile(T, tl, in);
+            const MomentTables L1 = lds_tables.moment(T.m1, 0);
+            const MomentTables L2 = lds_tables.moment(T.m2, 1);
+            float m1[16], m2[16];
+            update_tile_any(T, tl, in, L1, L2, m1, m2);
+            finish_moment<M1K, false>(T.m1, L1, tl, m1, ws);
+            loaded = false;
+            if (kPrefetch && more) {
+                tn = tensor_of(tile_start, ti, count, next);
+                const aw4_tensor& Tn = tensors[tn];
+                if (!values_only(Tn)) {
+                    load_tile(Tn, tile_lane(Tn, (next - tile_start[tn]) * kBlocksPerWave, lane), in);
+                    loaded = true;
+                }
+            }
+            finish_moment<M2K, true>(T.m2, L2, tl, m2, ws);
         }
-        const TileLane tl = tile_lane(T, local * kBlocksPerWave, lane);
-        TileInputs<M1K, M2K, D> in;
-        load_tile(T, tl, in);
-        const MomentTables L1 = lds_tables.moment(T.m1, 0);
-        const MomentTables L2 = lds_tables.moment(T.m2, 1);
-        compute_tile(T, tl, in, L1, L2, ws);
+        if (!more) break;
+        ti = tn >= 0 ? tn : tensor_of(tile_start, ti, count, next);
+        tile = next;
     }
 }
 

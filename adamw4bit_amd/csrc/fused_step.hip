@@ -580,6 +580,8 @@ int aw4_fused_step(const aw4_tensor* tensors, int32_t count, void* stream) {
     // of the index space (HBM page locality) and no CU waits on a static share at the end.
     // Measured on MI355X against persistent grids of contiguous per-wave ranges, which
     // stream from thousands of far-apart addresses at once and leave a load-imbalance tail.
+    // The kernel picks which tiles a wave takes (consecutive ones, or one per grid-sized
+    // stride); either way the grid is ceil(tiles / kTilesPerWave) waves.
     std::vector<int64_t> grid(plan.size());
     for (size_t g = 0; g < plan.size(); ++g) {
         const LaunchGroup& lg = plan[g];
