@@ -17,7 +17,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIBRARY = os.path.join(HERE, "libadamw4bit_hip.so")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 BLOCK = 128
 
 # Error codes

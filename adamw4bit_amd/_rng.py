@@ -6,9 +6,12 @@ the reference gives that moment's ``torch.Generator``
 stochastic write of ``n`` values consumes stream positions
 ``offset .. offset + n - 1`` (element ``k`` of the write uses position
 ``offset + k``), and the stream then advances by ``n`` rounded up to a
-multiple of 4, exactly as the reference's generators advance by the ``n``
-uniforms ``_uniform_draws`` takes (``_optimized_quantization.py:37-43``).
-The draws therefore depend only on (seed, position), never on launch geometry.
+multiple of 128, as the reference's generators advance by the ``n`` uniforms
+``_uniform_draws`` takes (``_optimized_quantization.py:37-43``); every
+quantized write covers whole 128-value blocks, so nothing is skipped.  Writes
+start at multiples of 128: the kernels draw a block's uniforms from one
+position group.  The draws depend only on (seed, position), never on launch
+geometry.
 
 The checkpointed state is a 16-byte ``uint8`` tensor: the key and the position
 as little-endian uint64 (the layout of a CUDA ``torch.Generator`` state).
@@ -31,9 +34,9 @@ class PhiloxStream:
         self.offset = int(offset)
 
     def take(self, n: int) -> int:
-        """Reserve ``n`` positions and return the first (a multiple of 4)."""
+        """Reserve ``n`` positions and return the first (a multiple of 128)."""
         first = self.offset
-        self.offset += (int(n) + 3) // 4 * 4
+        self.offset += (int(n) + 127) // 128 * 128
         return first
 
     def advance(self, n: int) -> None:
@@ -49,6 +52,6 @@ class PhiloxStream:
                 "quantization RNG state must be a 16-byte uint8 tensor (Philox key and position), "
                 f"got {getattr(state, 'dtype', type(state))} with {getattr(state, 'numel', lambda: '?')()} elements")
         seed, offset = struct.unpack("<QQ", bytes(state.detach().cpu().contiguous().numpy().tobytes()))
-        if offset % 4:
-            raise ValueError(f"quantization RNG position {offset} is not a multiple of 4")
+        if offset % 128:
+            raise ValueError(f"quantization RNG position {offset} is not a multiple of 128")
         self.seed, self.offset = seed, offset

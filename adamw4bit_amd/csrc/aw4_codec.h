@@ -156,35 +156,26 @@ __device__ __forceinline__ void update_sr_tables(const MomentTables& L, int j, f
     wave_lds_sync();
 }
 
-// Uniforms of this lane's 4 values at offset `off` from value blk0 * 128 of one write of
-// moment M (stream position rng_offset + value index), scaled by 2^24: U = u * 2^24 is
-// exact for every float u, and an integer in [0, 2^24) for the generator's 24-bit draws.
-__device__ __forceinline__ void draws4(const aw4_moment& M, int64_t blk0, uint32_t off, bool active, float (&u)[4]) {
+// Uniforms of this lane's 4 values of quarter q in its block (block blk0 + grp of one write
+// of moment M), scaled by 2^24: U = u * 2^24 is exact for every float u, and an integer in
+// [0, 2^24) for the generator's 24-bit draws.  On-device draws: the block's values are
+// stream positions rng_offset + 128 * block + 32 q + 4 j + t (rng_offset a multiple of
+// 128), so the lane's 16 uniforms come from the three Philox calls of position group
+// rng_offset / 128 + block; call r is made at quarter r, into words 4r .. 4r+3 of `rw`, and
+// quarter q reads words 3q .. 3q+2.  The loop over q must be unrolled (constant indices).
+__device__ __forceinline__ void draws_quarter(const aw4_moment& M, int64_t blk0, int grp, int j, int q, bool active,
+                                              uint32_t (&rw)[12], float (&u)[4]) {
     if (M.flags & AW4_MOMENT_EXT_DRAWS) {
         f32x4 v = {0.f, 0.f, 0.f, 0.f};
-        if (active) v = *(gptr<const f32x4>)(gaddr<const float>(M.draws) + blk0 * kBlock + off);
+        if (active)
+            v = *(gptr<const f32x4>)(gaddr<const float>(M.draws) + (blk0 + grp) * kBlock + 32 * q + 4 * j);
         u[0] = v.x * 0x1p24f; u[1] = v.y * 0x1p24f; u[2] = v.z * 0x1p24f; u[3] = v.w * 0x1p24f;
     } else {
-        uniforms4_scaled(M.rng_seed, M.rng_offset + (uint64_t)blk0 * kBlock + off, u);
+        if (q < 3) philox_lane_call(M.rng_seed, (M.rng_offset >> 7) + (uint64_t)(blk0 + grp), j, q, &rw[4 * q]);
+        lane_fields4(&rw[3 * q], u);
     }
 }
 
-// Encode this lane's 16 values of block `blk` (_optimized_quantization.py:46-88):
-//   s = max(max|m|, 1e-12); x = m / s; codes by the rounding rule; [dyn4_nz floor]; [EDEN]
-// and store the block's codes and (lane 0) its scale.  Codes are produced a quarter (4
-// values) at a time and staged in LDS, so that each lane then stores 8 contiguous code
-// bytes and a wave writes its tile's 512 code bytes as whole lines (16-byte pieces of a
-// block written a quarter at a time reach HBM as partial-sector writes).  The EDEN sums
-// run in ATen's order (block_sum_cross).
-//
-// kNonNeg: the values are >= +0 (second moments: a lerp of a non-negative state towards
-// g*g), so only the magnitude half of the lookup tables is indexed.
-//
-// x is RN(m / s) computed from RN(1 / s).  When the quotient is subnormal (|m| < 2^-125 s)
-// it may differ from RN(m / s) by a few subnormal ulps; no output can see that: every
-// rounding table resolves [-2^-10, 2^-10] to one code or to the level-0 threshold at the
-// smallest subnormal, the preconditioner of such an x equals the one of 0 (eps absorbs
-// it), and its EDEN products vanish next to the block's |x| = 1 element.
 // Update-SR draw test u < P(lo) for one value, with U = u * 2^24 and the table entry of
 // its interval: P(lo) = RN(d / den), d = RN(f(x) - f(b)),
 // f(x) = 1 / (sqrt(max((s * x) / bias, 0)) + eps)  (_compiled_quantization.py:74-97).
@@ -235,7 +226,7 @@ __device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTa
     wave_lds_sync();  // the stage's previous contents have been read
 
     float acc_xx[4] = {0.0f, 0.0f, 0.0f, 0.0f}, acc_xl[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    const uint32_t voff = (uint32_t)(grp * kBlock + 4 * j);
+    uint32_t rw[12];  // Philox words of this lane's position group (stochastic kinds)
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         float x[4];
@@ -259,7 +250,7 @@ __device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTa
             }
         } else {
             float u[4];  // the uniforms times 2^24
-            draws4(M, blk0, voff + 32u * q, active, u);
+            draws_quarter(M, blk0, grp, j, q, active, rw, u);
             // Both rules pick level lo = max(idx - 1, 0) or hi = min(idx, 15), idx = number of levels
             // below x.  Since u is in [0, 1), u < clamp(P, 0, 1) == u < P for every P (NaN included),
             // so the clamps of the reference never change a code and the guards become masks.

@@ -152,12 +152,17 @@ __device__ __forceinline__ float block_sum_cross(const float (&acc)[4]) {
 }
 
 // ---------------------------------------------------------------------------
-// Philox4x32-10 (Salmon et al., SC'11): stream position k of key `seed` is word
-// k % 4 of Philox(counter = k / 4, key = seed), mapped to [0,1) with 24 bits.
+// Philox4x32-10 (Salmon et al., SC'11) streams.  Positions of key `seed` are grouped by
+// 128: position P = 128 B + 32 q + 4 j + t (q, t = 0..3, j = 0..7) is the 24-bit field
+// i = 4 q + t of the 384-bit little-endian string
+//   out(24 B + 3 j) || out(24 B + 3 j + 1) || out(24 B + 3 j + 2),
+// out(c) being the four words of Philox(counter = c, key = seed), mapped to [0,1) as
+// field * 2^-24.  The lane that owns offsets 32 q + 4 j + t of a 128-value block draws
+// its 16 uniforms from three Philox calls, every output bit used once.
 // ---------------------------------------------------------------------------
 
 __device__ __forceinline__ void philox4x32_10(uint32_t c0, uint32_t c1, uint32_t k0, uint32_t k1,
-                                              uint32_t (&out)[4]) {
+                                              uint32_t* out) {
     uint32_t c2 = 0u, c3 = 0u;
 #pragma unroll
     for (int r = 0; r < 10; ++r) {
@@ -179,22 +184,19 @@ __device__ __forceinline__ void philox4x32_10(uint32_t c0, uint32_t c1, uint32_t
     out[3] = c3;
 }
 
-// Uniforms at stream positions pos .. pos+3 (pos % 4 == 0).
-__device__ __forceinline__ void uniforms4(uint64_t seed, uint64_t pos, float (&u)[4]) {
-    const uint64_t ctr = pos >> 2;
-    uint32_t r[4];
-    philox4x32_10((uint32_t)ctr, (uint32_t)(ctr >> 32), (uint32_t)seed, (uint32_t)(seed >> 32), r);
-#pragma unroll
-    for (int t = 0; t < 4; ++t) u[t] = (float)(r[t] >> 8) * 0x1p-24f;
+// Call r (0..2) of lane j in position group B: words 4r .. 4r+3 of the lane's 384-bit string.
+__device__ __forceinline__ void philox_lane_call(uint64_t seed, uint64_t group, int j, int r, uint32_t* w) {
+    const uint64_t ctr = group * 24u + (uint64_t)(3 * j + r);
+    philox4x32_10((uint32_t)ctr, (uint32_t)(ctr >> 32), (uint32_t)seed, (uint32_t)(seed >> 32), w);
 }
 
-// The same uniforms times 2^24: the integers r >> 8, as floats (exact).
-__device__ __forceinline__ void uniforms4_scaled(uint64_t seed, uint64_t pos, float (&u)[4]) {
-    const uint64_t ctr = pos >> 2;
-    uint32_t r[4];
-    philox4x32_10((uint32_t)ctr, (uint32_t)(ctr >> 32), (uint32_t)seed, (uint32_t)(seed >> 32), r);
-#pragma unroll
-    for (int t = 0; t < 4; ++t) u[t] = (float)(r[t] >> 8);
+// Fields 4q .. 4q+3 of a lane's string (words 3q .. 3q+2), as exact floats in [0, 2^24):
+// the uniforms times 2^24.
+__device__ __forceinline__ void lane_fields4(const uint32_t* w, float (&u)[4]) {
+    u[0] = (float)(w[0] & 0xffffffu);
+    u[1] = (float)((w[0] >> 24) | ((w[1] & 0xffffu) << 8));
+    u[2] = (float)((w[1] >> 16) | ((w[2] & 0xffu) << 16));
+    u[3] = (float)(w[2] >> 8);
 }
 
 }  // namespace aw4

@@ -8,7 +8,8 @@
 //     quarter q of a block is one contiguous 128 B segment across the 8 lanes.  The same
 //     split makes the reference's per-block sum order (ATen's 8-lane x 4-accumulator
 //     reduction) mostly lane-local (block_sum_cross in aw4_math.h).
-//   * Tiles of all tensors form one index space; each wave takes 4 consecutive tiles and
+//   * Tiles of all tensors form one index space; each wave takes up to 4 tiles (in grid
+//     order for the memory-bound kernels, consecutive ones for the update-SR kernels) and
 //     the grid covers all of them, so the hardware dispatcher keeps the tiles in flight a
 //     narrow moving window of memory.  One launch covers every parameter of the step,
 //     fp32-state tensors included.
@@ -219,15 +220,27 @@ __global__ void __launch_bounds__(kThreads) dequantize_kernel(aw4_moment M, int6
     }
 }
 
+// Uniforms at positions offset .. offset+n-1 (n > 0): one thread per (position group, lane).
 __global__ void __launch_bounds__(kThreads) uniforms_kernel(uint64_t seed, uint64_t offset, int64_t n,
                                                             float* __restrict__ out) {
-    const int64_t stride = (int64_t)gridDim.x * kThreads * 4;
-    for (int64_t e = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * 4; e < n; e += stride) {
-        float u[4];
-        uniforms4(seed, offset + (uint64_t)e, u);
+    const uint64_t g0 = offset >> 7, end = offset + (uint64_t)n;
+    const int64_t lanes = (int64_t)(((end - 1) >> 7) - g0 + 1) * 8;
+    for (int64_t l = (int64_t)blockIdx.x * kThreads + threadIdx.x; l < lanes; l += (int64_t)gridDim.x * kThreads) {
+        const uint64_t group = g0 + (uint64_t)(l >> 3);
+        const int j = (int)(l & 7);
+        uint32_t w[12];
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
-            if (e + t < n) out[e + t] = u[t];
+        for (int r = 0; r < 3; ++r) philox_lane_call(seed, group, j, r, &w[4 * r]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            float u[4];
+            lane_fields4(&w[3 * q], u);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint64_t pos = group * kBlock + (uint64_t)(32 * q + 4 * j + t);
+                if (pos >= offset && pos < end) out[pos - offset] = u[t] * 0x1p-24f;
+            }
+        }
     }
 }
 
@@ -428,8 +441,8 @@ int check_moment(const aw4_moment& m, int64_t numel, int index, const char* name
         if (m.flags & AW4_MOMENT_EXT_DRAWS) {
             if (!m.draws || !aligned(m.draws, 16))
                 return set_error(AW4_EINVAL, "tensor %d: %s external draws missing or misaligned", index, name);
-        } else if (m.rng_offset % 4 != 0) {
-            return set_error(AW4_EINVAL, "tensor %d: %s rng_offset not a multiple of 4", index, name);
+        } else if (m.rng_offset % kBlock != 0) {
+            return set_error(AW4_EINVAL, "tensor %d: %s rng_offset not a multiple of 128", index, name);
         }
     }
     if (m.rounding == AW4_ROUND_UPDATE_SR && !(m.sr_bias > 0.0f))
@@ -666,9 +679,10 @@ int aw4_dequantize(const aw4_moment* m, int64_t numel, float* out, void* stream)
 
 int aw4_uniforms(uint64_t seed, uint64_t offset, int64_t n, float* out, void* stream) {
     g_error.clear();
-    if (!out || n < 0 || offset % 4 != 0) return set_error(AW4_EINVAL, "aw4_uniforms: bad arguments");
+    if (!out || n < 0 || offset > UINT64_MAX - (uint64_t)n) return set_error(AW4_EINVAL, "aw4_uniforms: bad arguments");
     if (n == 0) return AW4_OK;
-    int64_t groups = (n / 4 + kThreads - 1) / kThreads;
+    const int64_t lanes = (int64_t)(((offset + (uint64_t)n - 1) >> 7) - (offset >> 7) + 1) * 8;
+    int64_t groups = (lanes + kThreads - 1) / kThreads;
     if (groups > 4096) groups = 4096;
     hipLaunchKernelGGL(uniforms_kernel, dim3((unsigned)groups), dim3(kThreads), 0, (hipStream_t)stream, seed, offset,
                        n, out);

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define AW4_ABI_VERSION 1
+#define AW4_ABI_VERSION 2
 #define AW4_BLOCK 128 /* values per block scale (quantization.py:694-703, 4-bit default) */
 
 /* Error codes. */
@@ -85,7 +85,7 @@ typedef struct aw4_moment {
     uint64_t values;     /* device address, float[numel] or 0 */
     uint64_t draws;      /* device address, float[numel] uniforms (AW4_MOMENT_EXT_DRAWS) or 0 */
     uint64_t rng_seed;   /* Philox4x32-10 key: generator seed of this moment's stream */
-    uint64_t rng_offset; /* stream position of this write's first draw; multiple of 4 */
+    uint64_t rng_offset; /* stream position of this write's first draw; multiple of 128 */
     int32_t codebook;    /* AW4_CB_* (ignored for AW4_ROUND_FP32) */
     int32_t rounding;    /* AW4_ROUND_* */
     int32_t flags;       /* AW4_MOMENT_* */
@@ -146,10 +146,14 @@ int aw4_dequantize(const aw4_moment* m, int64_t numel, float* out, void* stream)
 /*
  * Fill `out` (device address, n floats) with the uniforms in [0,1) that a
  * stochastic write draws at stream positions offset .. offset+n-1 of the
- * Philox4x32-10 stream keyed by `seed` (offset a multiple of 4).  Draw k of a
- * write of moment m is the uniform at position m.rng_offset + k, k being the
- * element index; it replaces _optimized_quantization._uniform_draws (:37-43),
- * whose CPU mt19937 / CUDA Philox streams a device kernel cannot reproduce.
+ * Philox4x32-10 stream keyed by `seed`.  Positions are grouped by 128: position
+ * P = 128 B + 32 q + 4 j + t (q, t in 0..3, j in 0..7) is the 24-bit field
+ * 4 q + t of the 384-bit little-endian string formed by the outputs of
+ * Philox(counter = 24 B + 3 j + r, key = seed), r = 0, 1, 2, times 2^-24.  Draw
+ * k of a write of moment m is the uniform at position m.rng_offset + k, k being
+ * the element index; it replaces _optimized_quantization._uniform_draws
+ * (:37-43), whose CPU mt19937 / CUDA Philox streams a device kernel cannot
+ * reproduce.
  */
 int aw4_uniforms(uint64_t seed, uint64_t offset, int64_t n, float* out, void* stream);
 

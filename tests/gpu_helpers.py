@@ -80,7 +80,7 @@ class PhiloxMirror:
     def __call__(self, moment, n):
         seed = self.opt._stream(moment, self.device).seed
         off = self.offsets[moment]
-        self.offsets[moment] = off + (n + 3) // 4 * 4
+        self.offsets[moment] = off + (n + 127) // 128 * 128
         return torch.from_numpy(philox.uniforms(seed, off, n))
 
 

@@ -38,7 +38,7 @@ def test_library_exports_every_declared_symbol():
 def test_error_path_reports_message():
     # Invalid arguments are rejected on the host before any device work.
     lib = _lib.library()
-    rc = lib.aw4_uniforms(1, 2, 16, None, None)  # offset not a multiple of 4, null output
+    rc = lib.aw4_uniforms(1, 2, 16, None, None)  # null output
     assert rc == _lib.EINVAL
     assert b"aw4_uniforms" in lib.aw4_last_error()
     table = np.zeros(1, dtype=_lib.TENSOR)  # null pointers

@@ -55,7 +55,7 @@ def test_host_sqrt_rounding_report():
 # ---------------------------------------------------------------------------
 
 @pytest.mark.parametrize("seed,offset,n", [(0, 0, 4096), (0x1A2B3C4D, 128, 1000), ((1 << 63) - 5, 1 << 34, 8192),
-                                           (1584363401, 4 * 12345, 333)])
+                                           (1584363401, 4 * 12345, 333), (99, (1 << 40) + 100, 700)])
 def test_uniforms_match_cpu_philox(seed, offset, n):
     log(f"uniforms seed={seed} offset={offset} n={n}")
     got = H.uniforms_gpu(seed, offset, n).cpu().numpy()

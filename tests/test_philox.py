@@ -27,17 +27,30 @@ def test_random123_known_answers(counter, key, expect):
 
 
 def test_stream_positions_and_uniform_mapping():
-    """Position k of key seed is word k % 4 of Philox(k // 4 with its high half in word 1)."""
+    """Each lane of a position group reads its 16 fields from three Philox outputs: joining the
+    fields back in order must give exactly the 384 output bits (no bit dropped, repeated or
+    moved), for a group whose counters use both 32-bit counter words."""
     seed = 0x0123456789ABCDEF
     key = (seed & 0xFFFFFFFF, seed >> 32)
-    offset = (1 << 34) + 8  # counter crosses into the second 32-bit word
-    u = philox.uniforms(seed, offset, 10)
-    for k in range(10):
-        pos = offset + k
-        ctr = pos // 4
-        words = philox.philox4x32_10(np.array([[ctr & 0xFFFFFFFF, ctr >> 32, 0, 0]], dtype=np.uint32), key)[0]
-        assert u[k] == np.float32((int(words[pos % 4]) >> 8) * 2.0 ** -24)
+    group = (1 << 33) + 5  # counters 24 * group + ... exceed 2**32
+    u = philox.uniforms(seed, 128 * group, 128)
     assert u.dtype == np.float32 and (u >= 0).all() and (u < 1).all()
+    fields = (u.astype(np.float64) * 2.0 ** 24).astype(np.uint64)
+    assert np.array_equal(fields.astype(np.float64) * 2.0 ** -24, u.astype(np.float64))  # 24-bit grid
+    for j in range(8):
+        bits = 0
+        for q in range(4):
+            for t in range(4):
+                bits |= int(fields[32 * q + 4 * j + t]) << (24 * (4 * q + t))
+        expect = 0
+        for r in range(3):
+            ctr = 24 * group + 3 * j + r
+            words = philox.philox4x32_10(np.array([[ctr & 0xFFFFFFFF, ctr >> 32, 0, 0]], dtype=np.uint32), key)[0]
+            for w in range(4):
+                expect |= int(words[w]) << (32 * (4 * r + w))
+        assert bits == expect, j
+    # a write that starts inside a group reads the same positions
+    assert np.array_equal(philox.uniforms(seed, 128 * group + 40, 50), u[40:90])
 
 
 def test_uniforms_concatenate_across_writes():
