@@ -197,15 +197,43 @@ __device__ __forceinline__ bool usr_draw_lower(const aw4_moment& M, const UpdEnt
     return __builtin_fmaf(U, ue.den_u, -(fx - ue.f_hi)) < 0.0f;  // (den / 2^24 is exact)
 }
 
-template <int SPEC, bool kNonNeg>
-__device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTables& L, int64_t blk0, int grp, int j,
-                                             bool active, const float (&m)[16], BlockScratch sc) {
-    // NaN-propagating max |m| (v_maximum3_f32 with |.| operands), then over the block's 8 lanes
-    // on the bit patterns (non-negative floats and NaNs order as unsigned integers).
-    float amf = 0.0f;
+// NaN-propagating max(acc, |v|): v_maximum3_f32 with |.| operands.
+__device__ __forceinline__ float abs_max_acc(float acc, float v) {
+    return __builtin_elementwise_maximum(acc, __builtin_fabsf(v));
+}
+
+// The 16 values of this lane that a block encode reads, a quarter (4 values) at a time:
+// held in registers, or staged in LDS by the code that produced them (which also kept
+// their running max |v|), so that they occupy no registers until their quarter is encoded.
+struct RegValues {
+    const float (&m)[16];
+    __device__ float abs_max() const {
+        float a = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) amf = __builtin_elementwise_maximum(amf, __builtin_fabsf(m[i]));
-    const uint32_t amax = block_max_u32(f2u(amf));
+        for (int i = 0; i < 16; ++i) a = abs_max_acc(a, m[i]);
+        return a;
+    }
+    __device__ void quarter(int q, float (&v)[4]) const {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[t] = m[4 * q + t];
+    }
+};
+struct StagedValues {
+    const f32x4* lane_q0;  // this lane's quarter 0; quarter q is 64 entries further
+    float amax;            // max |v| over the 16 values (NaN-propagating)
+    __device__ float abs_max() const { return amax; }
+    __device__ void quarter(int q, float (&v)[4]) const {
+        const f32x4 x = lane_q0[64 * q];
+        v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+    }
+};
+
+template <int SPEC, bool kNonNeg, class Values>
+__device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTables& L, int64_t blk0, int grp, int j,
+                                             bool active, const Values& vals, BlockScratch sc) {
+    // max |m| over the lane's values, then over the block's 8 lanes on the bit patterns
+    // (non-negative floats and NaNs order as unsigned integers).
+    const uint32_t amax = block_max_u32(f2u(vals.abs_max()));
     const float s = u2f(max(amax, 0x2B8CBCCCu));  // max(absmax, fp32(1e-12))
     bool fast = s < 0x1p125f;                      // otherwise huge, infinite or NaN: IEEE division
     const float y = div_cr(1.0f, s);               // RN(1 / s): normal on the fast path
@@ -229,13 +257,14 @@ __device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTa
     uint32_t rw[12];  // Philox words of this lane's position group (stochastic kinds)
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        float x[4];
+        float x[4], mq[4];
+        vals.quarter(q, mq);
         if (__builtin_expect(wave_fast, 1)) {
 #pragma unroll
-            for (int t = 0; t < 4; ++t) x[t] = div_by_rcp(m[4 * q + t], s, y);
+            for (int t = 0; t < 4; ++t) x[t] = div_by_rcp(mq[t], s, y);
         } else {
 #pragma unroll
-            for (int t = 0; t < 4; ++t) x[t] = m[4 * q + t] / s;
+            for (int t = 0; t < 4; ++t) x[t] = mq[t] / s;
         }
         uint32_t code[4];
         float lv[4];
@@ -336,12 +365,12 @@ __device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTa
 }
 
 // Runtime dispatch over the rounding kind (generic kernels).
-template <bool kNonNeg>
+template <bool kNonNeg, class Values>
 __device__ __forceinline__ void encode_block_any(const aw4_moment& M, const MomentTables& L, int64_t blk0, int grp,
-                                                 int j, bool active, const float (&m)[16], BlockScratch sc) {
-    if (M.rounding == K_RTN) encode_block<mspec(K_RTN, kFlagsAtRunTime), kNonNeg>(M, L, blk0, grp, j, active, m, sc);
-    else if (M.rounding == K_SSR) encode_block<mspec(K_SSR, kFlagsAtRunTime), kNonNeg>(M, L, blk0, grp, j, active, m, sc);
-    else encode_block<mspec(K_USR, kFlagsAtRunTime), kNonNeg>(M, L, blk0, grp, j, active, m, sc);
+                                                 int j, bool active, const Values& v, BlockScratch sc) {
+    if (M.rounding == K_RTN) encode_block<mspec(K_RTN, kFlagsAtRunTime), kNonNeg>(M, L, blk0, grp, j, active, v, sc);
+    else if (M.rounding == K_SSR) encode_block<mspec(K_SSR, kFlagsAtRunTime), kNonNeg>(M, L, blk0, grp, j, active, v, sc);
+    else encode_block<mspec(K_USR, kFlagsAtRunTime), kNonNeg>(M, L, blk0, grp, j, active, v, sc);
 }
 
 }  // namespace aw4

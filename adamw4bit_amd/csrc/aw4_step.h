@@ -158,7 +158,7 @@ struct TileInputs {
     static constexpr bool kQ2 = K2 != K_FP32, kV2 = K2 == K_FP32 || K2 == K_ANY;
     uint32_t g[4 * kW];
     uint32_t p[4 * kW];
-    uint32_t c1[kQ1 ? 4 : 1], c2[kQ2 ? 4 : 1];
+    uint32_t c1[kQ1 ? 2 : 1], c2[kQ2 ? 2 : 1];  // code words of quarters 2h (low half) and 2h + 1 (high half)
     float s1, s2;
     float v1[kV1 ? 16 : 1], v2[kV2 ? 16 : 1];
 };
@@ -226,9 +226,13 @@ __device__ __forceinline__ void load_tile(const aw4_tensor& T, const TileLane& t
             if constexpr (kQ) {
                 const gptr<const uint8_t> codes = gaddr<const uint8_t>(M.codes) + tl.blk0 * (kBlock / 2);
                 const uint32_t coff = (uint32_t)(grp * (kBlock / 2) + 2 * tl.j);
+                // two 16-bit code words per register: 4 fewer registers per tile in flight
 #pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    c[q] = __builtin_nontemporal_load((gptr<const uint16_t>)(codes + coff + 16u * q));
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t lo = __builtin_nontemporal_load((gptr<const uint16_t>)(codes + coff + 32u * h));
+                    const uint32_t hi = __builtin_nontemporal_load((gptr<const uint16_t>)(codes + coff + 32u * h + 16u));
+                    c[h] = lo | (hi << 16);
+                }
                 s = (gaddr<const float>(M.scales) + tl.blk0)[grp];
             }
         } else {
@@ -248,25 +252,47 @@ __device__ __forceinline__ void load_tile(const aw4_tensor& T, const TileLane& t
                 std::integral_constant<bool, In::kV2>());
 }
 
-template <int MK, bool kNonNeg>
+template <int MK, bool kNonNeg, class Values>
 __device__ __forceinline__ void encode_moment(const aw4_moment& M, const MomentTables& L, const TileLane& tl,
-                                              const float (&m)[16], BlockScratch sc) {
-    if constexpr (kind_of(MK) == K_ANY) encode_block_any<kNonNeg>(M, L, tl.blk0, tl.grp, tl.j, tl.active, m, sc);
-    else encode_block<MK, kNonNeg>(M, L, tl.blk0, tl.grp, tl.j, tl.active, m, sc);
+                                              const Values& v, BlockScratch sc) {
+    if constexpr (kind_of(MK) == K_ANY) encode_block_any<kNonNeg>(M, L, tl.blk0, tl.grp, tl.j, tl.active, v, sc);
+    else encode_block<MK, kNonNeg>(M, L, tl.blk0, tl.grp, tl.j, tl.active, v, sc);
 }
 
+// Where the update puts the new second moments: registers, or this lane's slots of an LDS
+// stage (quarter-major, 64 lanes per quarter: conflict-free 16-byte accesses) with their
+// running max |v| for the encode.
+struct M2Regs {
+    float (&m)[16];
+    __device__ void put(int q, const float (&b)[4]) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) m[4 * q + t] = b[t];
+    }
+    __device__ RegValues values() const { return RegValues{m}; }
+};
+struct M2Staged {
+    f32x4* lane_q0;
+    float amax;
+    __device__ void put(int q, const float (&b)[4]) {
+        lane_q0[64 * q] = f32x4{b[0], b[1], b[2], b[3]};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) amax = abs_max_acc(amax, b[t]);
+    }
+    __device__ StagedValues values() const { return StagedValues{lane_q0, amax}; }
+};
+
 // Decode, update and store one quarter (4 values) of this lane; the new moments go to m1/m2.
-template <int M1K, int M2K, int D, int DP, bool kGenericLerp>
+template <int M1K, int M2K, int D, int DP, bool kGenericLerp, class M2Sink>
 __device__ __forceinline__ void update_quarter(const aw4_tensor& T, int q, const TileInputs<M1K, M2K, D>& in,
                                                const MomentTables& L1, const MomentTables& L2, const TileLane& tl,
-                                               float (&m1)[16], float (&m2)[16]) {
+                                               float (&m1)[16], M2Sink& m2) {
     using In = TileInputs<M1K, M2K, D>;
     constexpr int DC = D == D_ANY ? D_F32 : D;  // generic loads are already fp32 words
     float g[4], p[4], a[4], b[4];
     words_to_f32<DC>(&in.g[In::kW * q], g);
     words_to_f32<DC>(&in.p[In::kW * q], p);
     if (moment_quantized<M1K>(T.m1)) {
-        if constexpr (In::kQ1) decode4(L1.dec, in.c1[q], in.s1, a);
+        if constexpr (In::kQ1) decode4(L1.dec, in.c1[q >> 1] >> (16 * (q & 1)), in.s1, a);
     } else {
         if constexpr (In::kV1) {
 #pragma unroll
@@ -274,7 +300,7 @@ __device__ __forceinline__ void update_quarter(const aw4_tensor& T, int q, const
         }
     }
     if (moment_quantized<M2K>(T.m2)) {
-        if constexpr (In::kQ2) decode4(L2.dec, in.c2[q], in.s2, b);
+        if constexpr (In::kQ2) decode4(L2.dec, in.c2[q >> 1] >> (16 * (q & 1)), in.s2, b);
     } else {
         if constexpr (In::kV2) {
 #pragma unroll
@@ -293,8 +319,8 @@ __device__ __forceinline__ void update_quarter(const aw4_tensor& T, int q, const
         }
         p[t] = param_update<DP>(T, p[t], a[t], b[t]);
         m1[4 * q + t] = a[t];
-        m2[4 * q + t] = b[t];
     }
+    m2.put(q, b);
     if (tl.active) {
         const uint32_t off = tl.voff + 32u * q;
         if constexpr (D == D_ANY) {
@@ -309,10 +335,10 @@ __device__ __forceinline__ void update_quarter(const aw4_tensor& T, int q, const
     }
 }
 
-template <int M1K, int M2K, int D, int DP>
+template <int M1K, int M2K, int D, int DP, class M2Sink>
 __device__ __forceinline__ void update_tile(const aw4_tensor& T, const TileInputs<M1K, M2K, D>& in,
                                             const MomentTables& L1, const MomentTables& L2, const TileLane& tl,
-                                            float (&m1)[16], float (&m2)[16]) {
+                                            float (&m1)[16], M2Sink& m2) {
     if (__builtin_expect((T.flags & (AW4_TENSOR_LERP1_LARGE | AW4_TENSOR_LERP2_LARGE)) == 0, 1)) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) update_quarter<M1K, M2K, D, DP, false>(T, q, in, L1, L2, tl, m1, m2);
@@ -323,10 +349,10 @@ __device__ __forceinline__ void update_tile(const aw4_tensor& T, const TileInput
 }
 
 // Decode, update and store the parameters of one tile; the new moments go to m1/m2.
-template <int M1K, int M2K, int D>
+template <int M1K, int M2K, int D, class M2Sink>
 __device__ __forceinline__ void update_tile_any(const aw4_tensor& T, const TileLane& tl,
                                                 const TileInputs<M1K, M2K, D>& in, const MomentTables& L1,
-                                                const MomentTables& L2, float (&m1)[16], float (&m2)[16]) {
+                                                const MomentTables& L2, float (&m1)[16], M2Sink& m2) {
     if constexpr (D == D_ANY) {
         if (T.param_dtype == D_F32) update_tile<M1K, M2K, D, D_F32>(T, in, L1, L2, tl, m1, m2);
         else if (T.param_dtype == D_BF16) update_tile<M1K, M2K, D, D_BF16>(T, in, L1, L2, tl, m1, m2);
@@ -337,17 +363,19 @@ __device__ __forceinline__ void update_tile_any(const aw4_tensor& T, const TileL
 }
 
 // Encode (or store, for an fp32-state moment) one moment of a tile.
-template <int MK, bool kNonNeg>
+template <int MK, bool kNonNeg, class Values>
 __device__ __forceinline__ void finish_moment(const aw4_moment& M, const MomentTables& L, const TileLane& tl,
-                                              const float (&m)[16], WaveScratch& ws) {
+                                              const Values& v, WaveScratch& ws) {
     if (moment_quantized<MK>(M)) {
-        if constexpr (kind_of(MK) != K_FP32) encode_moment<MK, kNonNeg>(M, L, tl, m, ws.block(tl.grp));
+        if constexpr (kind_of(MK) != K_FP32) encode_moment<MK, kNonNeg>(M, L, tl, v, ws.block(tl.grp));
     } else if (tl.active) {
         const gptr<float> vals_tile = gaddr<float>(M.values) + tl.blk0 * kBlock;
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-            __builtin_nontemporal_store(f32x4{m[4 * q], m[4 * q + 1], m[4 * q + 2], m[4 * q + 3]},
-                                        (gptr<f32x4>)(vals_tile + tl.voff + 32u * q));
+        for (int q = 0; q < 4; ++q) {
+            float x[4];
+            v.quarter(q, x);
+            __builtin_nontemporal_store(f32x4{x[0], x[1], x[2], x[3]}, (gptr<f32x4>)(vals_tile + tl.voff + 32u * q));
+        }
     }
 }
 
@@ -426,9 +454,14 @@ __device__ __forceinline__ bool values_only(const aw4_tensor& T) {
 // registers and runs the plain order.  The generic kernel (run-time kinds and dtype) has
 // the register pressure of every variant at once and loads each tile when it starts it.
 constexpr bool prefetch_next_tile(int m1k, int m2k, int d) {
-    return kind_of(m1k) != K_ANY && kind_of(m2k) != K_ANY && d != D_ANY && kind_of(m2k) != K_USR;
+    return kind_of(m1k) != K_ANY && kind_of(m2k) != K_ANY && d != D_ANY;
 }
-constexpr bool tile_order_grid(int m1k, int m2k, int d) { return prefetch_next_tile(m1k, m2k, d); }
+constexpr bool tile_order_grid(int m1k, int m2k, int d) {
+    return prefetch_next_tile(m1k, m2k, d) && kind_of(m2k) != K_USR;
+}
+// Update-SR kernels stage the new second moments in LDS (M2Staged) so that the prefetched
+// inputs fit in the registers of four waves per SIMD.
+constexpr bool stage_m2(int m1k, int m2k, int d) { return prefetch_next_tile(m1k, m2k, d) && kind_of(m2k) == K_USR; }
 
 // Index of the tensor holding `tile` >= tile_start[lo]: the last ti in [lo, count) with
 // tile_start[ti] <= tile (one load when it is still tensor lo, else a binary search).
@@ -443,8 +476,12 @@ __device__ __forceinline__ int tensor_of(const int64_t* tile_start, int lo, int 
     return lo;
 }
 
-template <int M1K, int M2K, int D, class LdsT>
-__device__ __forceinline__ void run_tiles(const StepHeader* hdr, const LdsT& lds_tables, WaveScratch& ws) {
+// `load_tables` fills the workgroup's LDS tables and synchronises the workgroup: every wave
+// calls it exactly once, after issuing its first tile's loads, so those loads are in flight
+// during the table load.
+template <int M1K, int M2K, int D, class LdsT, class LoadTables>
+__device__ __forceinline__ void run_tiles(const StepHeader* hdr, const LdsT& lds_tables, WaveScratch& ws,
+                                          f32x4* m2_stage, LoadTables&& load_tables) {
     const aw4_tensor* tensors = (const aw4_tensor*)(hdr + 1);
     const int count = hdr->count;
     const int64_t* tile_start = (const int64_t*)(tensors + count);
@@ -456,10 +493,17 @@ __device__ __forceinline__ void run_tiles(const StepHeader* hdr, const LdsT& lds
     const int64_t total = hdr->total_tiles;
     const int64_t per_wave = hdr->tiles_per_wave;
     int64_t tile = kGridOrder ? wave : wave * per_wave;
-    if (tile >= total) return;
-    int ti = tensor_of(tile_start, 0, count, tile);
+    const bool any = tile < total;
+    int ti = any ? tensor_of(tile_start, 0, count, tile) : 0;
     TileInputs<M1K, M2K, D> in;
-    bool loaded = false;  // `in` holds this tile's inputs (prefetched by the previous one)
+    bool loaded = false;  // `in` holds this tile's inputs (issued earlier)
+    if (any && !values_only(tensors[ti])) {
+        const aw4_tensor& T = tensors[ti];
+        load_tile(T, tile_lane(T, (tile - tile_start[ti]) * kBlocksPerWave, lane), in);
+        loaded = true;
+    }
+    load_tables();
+    if (!any) return;
     for (int64_t k = 0;;) {
         const aw4_tensor& T = tensors[ti];
         const int64_t local = tile - tile_start[ti];
@@ -474,19 +518,32 @@ __device__ __forceinline__ void run_tiles(const StepHeader* hdr, const LdsT& lds
             if (!loaded) load_tile(T, tl, in);
             const MomentTables L1 = lds_tables.moment(T.m1, 0);
             const MomentTables L2 = lds_tables.moment(T.m2, 1);
-            float m1[16], m2[16];
-            update_tile_any(T, tl, in, L1, L2, m1, m2);
-            finish_moment<M1K, false>(T.m1, L1, tl, m1, ws);
-            loaded = false;
-            if (kPrefetch && more) {
-                tn = tensor_of(tile_start, ti, count, next);
-                const aw4_tensor& Tn = tensors[tn];
-                if (!values_only(Tn)) {
-                    load_tile(Tn, tile_lane(Tn, (next - tile_start[tn]) * kBlocksPerWave, lane), in);
-                    loaded = true;
+            auto prefetch = [&]() {
+                loaded = false;
+                if (kPrefetch && more) {
+                    tn = tensor_of(tile_start, ti, count, next);
+                    const aw4_tensor& Tn = tensors[tn];
+                    if (!values_only(Tn)) {
+                        load_tile(Tn, tile_lane(Tn, (next - tile_start[tn]) * kBlocksPerWave, lane), in);
+                        loaded = true;
+                    }
                 }
+            };
+            float m1[16];
+            if constexpr (stage_m2(M1K, M2K, D)) {
+                M2Staged m2{m2_stage + lane, 0.0f};
+                update_tile_any(T, tl, in, L1, L2, m1, m2);
+                finish_moment<M1K, false>(T.m1, L1, tl, RegValues{m1}, ws);
+                prefetch();
+                finish_moment<M2K, true>(T.m2, L2, tl, m2.values(), ws);
+            } else {
+                float m2v[16];
+                M2Regs m2{m2v};
+                update_tile_any(T, tl, in, L1, L2, m1, m2);
+                finish_moment<M1K, false>(T.m1, L1, tl, RegValues{m1}, ws);
+                prefetch();
+                finish_moment<M2K, true>(T.m2, L2, tl, m2.values(), ws);
             }
-            finish_moment<M2K, true>(T.m2, L2, tl, m2, ws);
         }
         if (!more) break;
         ti = tn >= 0 ? tn : tensor_of(tile_start, ti, count, next);

@@ -86,10 +86,12 @@ struct LdsSlots {
     float2 dec[2][256];
     LutEntry lut[2][AW4_LUT_ENTRIES];
     WaveScratch scratch[kWavesPerGroup];
+    f32x4 m2_stage[kUpd ? kWavesPerGroup * 4 * 64 : 1];  // second moments of a tile (update-SR kernels)
 
     __device__ MomentTables moment(const aw4_moment&, int which) const {
         return MomentTables{cb[which], pairs[which], dec[which], lut[which]};
     }
+    __device__ f32x4* wave_m2_stage(int wslot) { return kUpd ? &m2_stage[wslot * 4 * 64] : nullptr; }
     __device__ void load(const Tables* g, const StepHeader* h) {
         const int cbs[2] = {h->cb1, h->cb2}, luts[2] = {h->lut1, h->lut2};
         for (int w = 0; w < 2; ++w) {
@@ -113,6 +115,7 @@ struct LdsAll {
         return MomentTables{t.codebook[cbid], t.pairs[cbid], t.dec[cbid],
                             t.lut[m.rounding == AW4_ROUND_FP32 ? 0 : lut_id_of(m.rounding, cbid, m.flags)]};
     }
+    __device__ f32x4* wave_m2_stage(int) { return nullptr; }
     __device__ void load(const Tables* g, const StepHeader*) {
         const uint32_t* src = (const uint32_t*)g;
         uint32_t* dst = (uint32_t*)&t;
@@ -134,9 +137,8 @@ __global__ void __launch_bounds__(kThreads) step_kernel(const StepHeader* __rest
                                                          const Tables* __restrict__ tables) {
     using Lds = typename KernelTraits<M1K, M2K, D>::Lds;
     __shared__ Lds lds;
-    lds.load(tables, hdr);
     const int wslot = threadIdx.x >> 6;
-    run_tiles<M1K, M2K, D>(hdr, lds, lds.scratch[wslot]);
+    run_tiles<M1K, M2K, D>(hdr, lds, lds.scratch[wslot], lds.wave_m2_stage(wslot), [&] { lds.load(tables, hdr); });
 }
 
 // The instantiated kernels; the host groups a step's tensors by the variant whose moment
@@ -188,7 +190,7 @@ __global__ void __launch_bounds__(kThreads) quantize_kernel(const float* __restr
             m[4 * q] = v.x; m[4 * q + 1] = v.y; m[4 * q + 2] = v.z; m[4 * q + 3] = v.w;
         }
         // stand-alone encodes accept any sign (a first moment or a caller's values)
-        encode_block_any<false>(M, L, tile * kBlocksPerWave, grp, j, active, m, lds.scratch[wslot].block(grp));
+        encode_block_any<false>(M, L, tile * kBlocksPerWave, grp, j, active, RegValues{m}, lds.scratch[wslot].block(grp));
     }
 }
 
