@@ -27,6 +27,7 @@ OK, EINVAL, EHIP, EALIGN = 0, -1, -2, -3
 CB_NF4, CB_SDYN4, CB_DYN4, CB_LIN4, CB_LIN4_NZ = 0, 1, 2, 3, 4
 ROUND_FP32, ROUND_RTN, ROUND_STATE_SR, ROUND_UPDATE_SR = 0, 1, 2, 3
 MOMENT_ZERO_FLOOR, MOMENT_EDEN, MOMENT_GUARDS, MOMENT_EXT_DRAWS = 0x1, 0x2, 0x4, 0x8
+MOMENT_SAMPLED_READ, MOMENT_READ_RAW_SCALE = 0x10, 0x20
 F32, BF16, F16 = 0, 1, 2
 TENSOR_LERP1_LARGE, TENSOR_LERP2_LARGE, TENSOR_VEC_ALIGNED = 0x1, 0x2, 0x4
 

@@ -16,9 +16,12 @@ the backend's preflight would reject, and every parameter when
 ``optimized=False``, follow the reference step (``adamw.py:472-805``), which
 differs only in those two points.
 
+The reference-step m2 variants that read the stored m2 back for the current update
+(``dyn4_upd_sr``, ``lin4_upd_sr``, ``*_upd_sr_store_eden``, ``adamw.py:615-656``) run
+in the same launch, in the generic kernel's read-back instance.
+
 Outside this build (raise ``NotImplementedError`` on construction): 8-bit state
-(``linear``/``dynamic``, ``AdamW8bit``), the research m2 variants
-``*_upd_sr``, ``*_upd_sr_store_eden`` and the lookahead proxies, update
+(``linear``/``dynamic``, ``AdamW8bit``), the lookahead m2 variants, update
 clipping, diagnostics recording and telemetry callbacks.  Parameters must live
 on a HIP device; there is no CPU implementation.
 """
@@ -37,6 +40,8 @@ from . import _lib, _ops
 from ._rng import PhiloxStream
 from .quantization import (
     NEXT_BIAS_SCHEMES,
+    SAMPLED_READ_SCHEMES,
+    STORE_EDEN_SCHEMES,
     QuantState,
     ROUND_STATE_SR,
     ROUND_UPDATE_SR,
@@ -59,8 +64,6 @@ _OPT_M2_SCHEMES = {
 _DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
 _UNSUPPORTED_SCHEMES = {
     "linear": "8-bit linear state", "dynamic": "8-bit dynamic state",
-    "lin4_upd_sr": "update-unbiased SR with a sampled read", "dyn4_upd_sr": "update-unbiased SR with a sampled read",
-    "lin4_upd_sr_store_eden": "update-SR with store-side EDEN", "dyn4_upd_sr_store_eden": "update-SR with store-side EDEN",
     "dyn4_la_upd_sr": "oracle lookahead update-SR", "dyn4_proxy_la_upd_sr": "proxy lookahead update-SR",
     "dyn4_vproxy_la_upd_sr": "v-proxy lookahead update-SR",
 }
@@ -587,6 +590,19 @@ class QuantizedAdamW(Optimizer):
         m1 = self._moment_row(p, state, "m1", schemes[0], False, optimized, 1.0, 1e-8, keep, written)
         m2 = self._moment_row(p, state, "m2", schemes[1], group["use_eden_m2"], optimized,
                               c.storage_bias, group["eps"], keep, written)
+        if schemes[1] in STORE_EDEN_SCHEMES:
+            # Reads with the scale before EDEN; stores the calibrated scale and 1/denominator.
+            pre = state.get("m2_read_preconditioner")
+            if not (isinstance(pre, torch.Tensor) and pre.shape == p.shape and pre.dtype == torch.float32
+                    and pre.device == p.device and pre.is_contiguous()):
+                pre = state["m2_read_preconditioner"] = torch.empty(p.shape, dtype=torch.float32, device=p.device)
+            written.append(pre)
+            m2 = m2[:2] + (pre.data_ptr(),) + m2[3:8] + (
+                m2[8] | _lib.MOMENT_SAMPLED_READ | _lib.MOMENT_READ_RAW_SCALE | _lib.MOMENT_EDEN,) + m2[9:]
+        else:
+            state.pop("m2_read_preconditioner", None)  # adamw.py:568-686, _optimized.py:156
+            if schemes[1] in SAMPLED_READ_SCHEMES:
+                m2 = m2[:8] + (m2[8] | _lib.MOMENT_SAMPLED_READ,) + m2[9:]
         if info is not None:
             info.append((p, optimized, schemes))
         return (p.data_ptr(), grad.data_ptr(), n, _DTYPES[p.dtype], _DTYPES[grad.dtype], flags,
@@ -683,8 +699,8 @@ class _LaunchPlan:
     """
 
     _STRUCTURE_KEYS = ("m1_quant_scheme", "m2_quant_scheme", "use_eden_m2", "block_size", _CHUNK_KEY)
-    _STATE_KEYS = ("m1", "m2", "m1_code", "m2_code", "m1_quant_state", "m2_quant_state")
-    _MAX_RANGES = 5  # a parameter and its writable moment tensors
+    _STATE_KEYS = ("m1", "m2", "m1_code", "m2_code", "m1_quant_state", "m2_quant_state", "m2_read_preconditioner")
+    _MAX_RANGES = 6  # a parameter and its writable moment tensors
 
     def __init__(self):
         self.groups: list = []     # (group, structure, parameter count)
@@ -719,7 +735,9 @@ class _LaunchPlan:
             for i, p in enumerate(params):
                 state = opt.state[p]
                 schemes = meta[id(p)]
-                ranges = [_byte_range(t)[1:] for t in [p] + _moment_tensors(state)]
+                pre = state.get("m2_read_preconditioner")
+                extra = [pre] if isinstance(pre, torch.Tensor) else []
+                ranges = [_byte_range(t)[1:] for t in [p] + _moment_tensors(state) + extra]
                 if len(ranges) > cls._MAX_RANGES:
                     return None
                 # The full path decided this parameter's semantics with this gradient; the plan

@@ -228,9 +228,16 @@ struct StagedValues {
     }
 };
 
+// The scales a block encode produced: s = max(absmax, 1e-12) (every lane) and the stored
+// scale (s, or its EDEN calibration; valid in lane j == 0).
+struct BlockScales {
+    float raw;
+    float stored;
+};
+
 template <int SPEC, bool kNonNeg, class Values>
-__device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTables& L, int64_t blk0, int grp, int j,
-                                             bool active, const Values& vals, BlockScratch sc) {
+__device__ __forceinline__ BlockScales encode_block(const aw4_moment& M, const MomentTables& L, int64_t blk0, int grp,
+                                                    int j, bool active, const Values& vals, BlockScratch sc) {
     // max |m| over the lane's values, then over the block's 8 lanes on the bit patterns
     // (non-negative floats and NaNs order as unsigned integers).
     const uint32_t amax = block_max_u32(f2u(vals.abs_max()));
@@ -362,15 +369,18 @@ __device__ __forceinline__ void encode_block(const aw4_moment& M, const MomentTa
         scale = s * div_cr(num, clamp_min_nan(den, 1e-12f));  // num in [1, 128]: a normal quotient
     }
     if (active && j == 0) __builtin_nontemporal_store(scale, gaddr<float>(M.scales) + blk0 + grp);
+    return BlockScales{s, scale};
 }
 
 // Runtime dispatch over the rounding kind (generic kernels).
 template <bool kNonNeg, class Values>
-__device__ __forceinline__ void encode_block_any(const aw4_moment& M, const MomentTables& L, int64_t blk0, int grp,
-                                                 int j, bool active, const Values& v, BlockScratch sc) {
-    if (M.rounding == K_RTN) encode_block<mspec(K_RTN, kFlagsAtRunTime), kNonNeg>(M, L, blk0, grp, j, active, v, sc);
-    else if (M.rounding == K_SSR) encode_block<mspec(K_SSR, kFlagsAtRunTime), kNonNeg>(M, L, blk0, grp, j, active, v, sc);
-    else encode_block<mspec(K_USR, kFlagsAtRunTime), kNonNeg>(M, L, blk0, grp, j, active, v, sc);
+__device__ __forceinline__ BlockScales encode_block_any(const aw4_moment& M, const MomentTables& L, int64_t blk0,
+                                                        int grp, int j, bool active, const Values& v, BlockScratch sc) {
+    if (M.rounding == K_RTN)
+        return encode_block<mspec(K_RTN, kFlagsAtRunTime), kNonNeg>(M, L, blk0, grp, j, active, v, sc);
+    if (M.rounding == K_SSR)
+        return encode_block<mspec(K_SSR, kFlagsAtRunTime), kNonNeg>(M, L, blk0, grp, j, active, v, sc);
+    return encode_block<mspec(K_USR, kFlagsAtRunTime), kNonNeg>(M, L, blk0, grp, j, active, v, sc);
 }
 
 }  // namespace aw4

@@ -253,10 +253,10 @@ __device__ __forceinline__ void load_tile(const aw4_tensor& T, const TileLane& t
 }
 
 template <int MK, bool kNonNeg, class Values>
-__device__ __forceinline__ void encode_moment(const aw4_moment& M, const MomentTables& L, const TileLane& tl,
-                                              const Values& v, BlockScratch sc) {
-    if constexpr (kind_of(MK) == K_ANY) encode_block_any<kNonNeg>(M, L, tl.blk0, tl.grp, tl.j, tl.active, v, sc);
-    else encode_block<MK, kNonNeg>(M, L, tl.blk0, tl.grp, tl.j, tl.active, v, sc);
+__device__ __forceinline__ BlockScales encode_moment(const aw4_moment& M, const MomentTables& L, const TileLane& tl,
+                                                     const Values& v, BlockScratch sc) {
+    if constexpr (kind_of(MK) == K_ANY) return encode_block_any<kNonNeg>(M, L, tl.blk0, tl.grp, tl.j, tl.active, v, sc);
+    else return encode_block<MK, kNonNeg>(M, L, tl.blk0, tl.grp, tl.j, tl.active, v, sc);
 }
 
 // Where the update puts the new second moments: registers, or this lane's slots of an LDS
@@ -282,10 +282,12 @@ struct M2Staged {
 };
 
 // Decode, update and store one quarter (4 values) of this lane; the new moments go to m1/m2.
-template <int M1K, int M2K, int D, int DP, bool kGenericLerp, class M2Sink>
+// kDefer: the parameter update waits for the stored m2 (AW4_MOMENT_SAMPLED_READ); p1 receives
+// the decayed parameters and nothing is stored.
+template <int M1K, int M2K, int D, int DP, bool kGenericLerp, bool kDefer, class M2Sink>
 __device__ __forceinline__ void update_quarter(const aw4_tensor& T, int q, const TileInputs<M1K, M2K, D>& in,
                                                const MomentTables& L1, const MomentTables& L2, const TileLane& tl,
-                                               float (&m1)[16], M2Sink& m2) {
+                                               float (&m1)[16], M2Sink& m2, float* p1) {
     using In = TileInputs<M1K, M2K, D>;
     constexpr int DC = D == D_ANY ? D_F32 : D;  // generic loads are already fp32 words
     float g[4], p[4], a[4], b[4];
@@ -317,11 +319,12 @@ __device__ __forceinline__ void update_quarter(const aw4_tensor& T, int q, const
         } else {
             moments_update<false, false>(T, g[t], a[t], b[t]);
         }
-        p[t] = param_update<DP>(T, p[t], a[t], b[t]);
+        if constexpr (kDefer) p1[4 * q + t] = round_to_storage<DP>(p[t] * T.decay);
+        else p[t] = param_update<DP>(T, p[t], a[t], b[t]);
         m1[4 * q + t] = a[t];
     }
     m2.put(q, b);
-    if (tl.active) {
+    if (!kDefer && tl.active) {
         const uint32_t off = tl.voff + 32u * q;
         if constexpr (D == D_ANY) {
             const bool vec = (T.flags & AW4_TENSOR_VEC_ALIGNED) != 0;
@@ -335,39 +338,73 @@ __device__ __forceinline__ void update_quarter(const aw4_tensor& T, int q, const
     }
 }
 
-template <int M1K, int M2K, int D, int DP, class M2Sink>
+template <int M1K, int M2K, int D, int DP, bool kDefer, class M2Sink>
 __device__ __forceinline__ void update_tile(const aw4_tensor& T, const TileInputs<M1K, M2K, D>& in,
                                             const MomentTables& L1, const MomentTables& L2, const TileLane& tl,
-                                            float (&m1)[16], M2Sink& m2) {
+                                            float (&m1)[16], M2Sink& m2, float* p1) {
     if (__builtin_expect((T.flags & (AW4_TENSOR_LERP1_LARGE | AW4_TENSOR_LERP2_LARGE)) == 0, 1)) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) update_quarter<M1K, M2K, D, DP, false>(T, q, in, L1, L2, tl, m1, m2);
+        for (int q = 0; q < 4; ++q) update_quarter<M1K, M2K, D, DP, false, kDefer>(T, q, in, L1, L2, tl, m1, m2, p1);
     } else {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) update_quarter<M1K, M2K, D, DP, true>(T, q, in, L1, L2, tl, m1, m2);
+        for (int q = 0; q < 4; ++q) update_quarter<M1K, M2K, D, DP, true, kDefer>(T, q, in, L1, L2, tl, m1, m2, p1);
     }
 }
 
 // Decode, update and store the parameters of one tile; the new moments go to m1/m2.
-template <int M1K, int M2K, int D, class M2Sink>
+template <int M1K, int M2K, int D, bool kDefer = false, class M2Sink>
 __device__ __forceinline__ void update_tile_any(const aw4_tensor& T, const TileLane& tl,
                                                 const TileInputs<M1K, M2K, D>& in, const MomentTables& L1,
-                                                const MomentTables& L2, float (&m1)[16], M2Sink& m2) {
+                                                const MomentTables& L2, float (&m1)[16], M2Sink& m2,
+                                                float* p1 = nullptr) {
     if constexpr (D == D_ANY) {
-        if (T.param_dtype == D_F32) update_tile<M1K, M2K, D, D_F32>(T, in, L1, L2, tl, m1, m2);
-        else if (T.param_dtype == D_BF16) update_tile<M1K, M2K, D, D_BF16>(T, in, L1, L2, tl, m1, m2);
-        else update_tile<M1K, M2K, D, D_F16>(T, in, L1, L2, tl, m1, m2);
+        if (T.param_dtype == D_F32) update_tile<M1K, M2K, D, D_F32, kDefer>(T, in, L1, L2, tl, m1, m2, p1);
+        else if (T.param_dtype == D_BF16) update_tile<M1K, M2K, D, D_BF16, kDefer>(T, in, L1, L2, tl, m1, m2, p1);
+        else update_tile<M1K, M2K, D, D_F16, kDefer>(T, in, L1, L2, tl, m1, m2, p1);
     } else {
-        update_tile<M1K, M2K, D, D>(T, in, L1, L2, tl, m1, m2);
+        update_tile<M1K, M2K, D, D, kDefer>(T, in, L1, L2, tl, m1, m2, p1);
+    }
+}
+
+// Parameter update of a tile whose m2 is read back after its encode (AW4_MOMENT_SAMPLED_READ,
+// adamw.py:636-656): v = cb[code] * scale from the code words the encode left in the
+// block's LDS stage (scale: the stored one, or with AW4_MOMENT_READ_RAW_SCALE the one before
+// EDEN, adamw.py:615-635), d = sqrt(v) / sqrt(bc2) + eps, p = p1 + (step_coef * m1) / d
+// (correctly rounded divisions, as the reference's), and 1 / d to M.values when it is set
+// (m2_read_preconditioner, adamw.py:632).
+template <int DP>
+__device__ __forceinline__ void sampled_read_update(const aw4_tensor& T, const TileLane& tl, const MomentTables& L2,
+                                                    BlockScratch sc, BlockScales bs, const float (&m1)[16],
+                                                    const float (&p1)[16]) {
+    const float stored = __shfl(bs.stored, (int)(threadIdx.x & 63) & ~7);  // lane j == 0 of the block
+    const float scale = (T.m2.flags & AW4_MOMENT_READ_RAW_SCALE) ? bs.raw : stored;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        float v[4], p[4], pre[4];
+        decode4(L2.dec, sc.stage[8 * q + tl.j], scale, v);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const float sq = sqrt_faithful(v[t]);
+            const float d = __builtin_amdgcn_div_fixupf(div_by_rcp(sq, T.bc2_sqrt, T.bc2_sqrt_rcp), T.bc2_sqrt, sq) + T.eps;
+            p[t] = p1[4 * q + t] + div_cr(T.step_coef * m1[4 * q + t], d);
+            pre[t] = div_cr(1.0f, d);
+        }
+        if (tl.active) {
+            const uint32_t off = tl.voff + 32u * q;
+            const bool vec = (T.flags & AW4_TENSOR_VEC_ALIGNED) != 0;
+            store_f32<DP>(T.param, tl.blk0 * kBlock + off, vec, p);
+            if (T.m2.values)
+                *(gptr<f32x4>)(gaddr<float>(T.m2.values) + tl.blk0 * kBlock + off) = f32x4{pre[0], pre[1], pre[2], pre[3]};
+        }
     }
 }
 
 // Encode (or store, for an fp32-state moment) one moment of a tile.
 template <int MK, bool kNonNeg, class Values>
-__device__ __forceinline__ void finish_moment(const aw4_moment& M, const MomentTables& L, const TileLane& tl,
-                                              const Values& v, WaveScratch& ws) {
+__device__ __forceinline__ BlockScales finish_moment(const aw4_moment& M, const MomentTables& L, const TileLane& tl,
+                                                     const Values& v, WaveScratch& ws) {
     if (moment_quantized<MK>(M)) {
-        if constexpr (kind_of(MK) != K_FP32) encode_moment<MK, kNonNeg>(M, L, tl, v, ws.block(tl.grp));
+        if constexpr (kind_of(MK) != K_FP32) return encode_moment<MK, kNonNeg>(M, L, tl, v, ws.block(tl.grp));
     } else if (tl.active) {
         const gptr<float> vals_tile = gaddr<float>(M.values) + tl.blk0 * kBlock;
 #pragma unroll
@@ -377,6 +414,7 @@ __device__ __forceinline__ void finish_moment(const aw4_moment& M, const MomentT
             __builtin_nontemporal_store(f32x4{x[0], x[1], x[2], x[3]}, (gptr<f32x4>)(vals_tile + tl.voff + 32u * q));
         }
     }
+    return BlockScales{0.0f, 0.0f};
 }
 
 // ---------------------------------------------------------------------------
@@ -459,6 +497,9 @@ constexpr bool prefetch_next_tile(int m1k, int m2k, int d) {
 constexpr bool tile_order_grid(int m1k, int m2k, int d) {
     return prefetch_next_tile(m1k, m2k, d) && kind_of(m2k) != K_USR;
 }
+// The generic kernel instance for tensors whose m2 is read back after its encode
+// (AW4_MOMENT_SAMPLED_READ in the m2 spec's flags).
+constexpr bool sampled_read_kernel(int m2k) { return (flags_of(m2k) & AW4_MOMENT_SAMPLED_READ) != 0; }
 // Update-SR kernels stage the new second moments in LDS (M2Staged) so that the prefetched
 // inputs fit in the registers of four waves per SIMD.
 constexpr bool stage_m2(int m1k, int m2k, int d) { return prefetch_next_tile(m1k, m2k, d) && kind_of(m2k) == K_USR; }
@@ -530,7 +571,18 @@ __device__ __forceinline__ void run_tiles(const StepHeader* hdr, const LdsT& lds
                 }
             };
             float m1[16];
-            if constexpr (stage_m2(M1K, M2K, D)) {
+            if constexpr (sampled_read_kernel(M2K)) {
+                // every block tile of this kernel reads its m2 back (the host groups them)
+                float m2v[16], p1[16];
+                M2Regs m2{m2v};
+                update_tile_any<M1K, M2K, D, true>(T, tl, in, L1, L2, m1, m2, p1);
+                finish_moment<M1K, false>(T.m1, L1, tl, RegValues{m1}, ws);
+                prefetch();
+                const BlockScales bs = finish_moment<M2K, true>(T.m2, L2, tl, m2.values(), ws);
+                if (T.param_dtype == D_F32) sampled_read_update<D_F32>(T, tl, L2, ws.block(tl.grp), bs, m1, p1);
+                else if (T.param_dtype == D_BF16) sampled_read_update<D_BF16>(T, tl, L2, ws.block(tl.grp), bs, m1, p1);
+                else sampled_read_update<D_F16>(T, tl, L2, ws.block(tl.grp), bs, m1, p1);
+            } else if constexpr (stage_m2(M1K, M2K, D)) {
                 M2Staged m2{m2_stage + lane, 0.0f};
                 update_tile_any(T, tl, in, L1, L2, m1, m2);
                 finish_moment<M1K, false>(T.m1, L1, tl, RegValues{m1}, ws);

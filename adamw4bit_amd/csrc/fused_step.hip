@@ -150,6 +150,8 @@ constexpr int kRtn = mspec(K_RTN), kRtnEden = mspec(K_RTN, AW4_MOMENT_EDEN), kFp
 constexpr int kSsrGuarded = mspec(K_SSR, AW4_MOMENT_GUARDS);
 constexpr int kUsrGuarded = mspec(K_USR, AW4_MOMENT_GUARDS);
 constexpr int kUsrGuardedEden = mspec(K_USR, AW4_MOMENT_GUARDS | AW4_MOMENT_EDEN);
+// Any m2 kind, read back after its encode (dyn4_upd_sr / lin4_upd_sr / *_upd_sr_store_eden).
+constexpr int kAnySampledRead = mspec(K_ANY, AW4_MOMENT_SAMPLED_READ);
 struct KernelVariant {
     int m1, m2, dtype;
     const void* fn;
@@ -161,11 +163,14 @@ const KernelVariant kVariants[] = {
     AW4_VARIANT(kSsrGuarded, kUsrGuarded, D_F32), AW4_VARIANT(kSsrGuarded, kUsrGuarded, D_BF16),
     AW4_VARIANT(kRtn, kFp32, D_F32),              AW4_VARIANT(kRtn, kFp32, D_BF16),
     AW4_VARIANT(kRtn, kUsrGuardedEden, D_F32),    AW4_VARIANT(kRtn, kUsrGuardedEden, D_BF16),
+    AW4_VARIANT(K_ANY, kAnySampledRead, D_ANY),
     AW4_VARIANT(K_ANY, K_ANY, D_ANY),
 };
 #undef AW4_VARIANT
 constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 constexpr int kGenericVariant = kNumVariants - 1;
+constexpr int kSampledReadVariant = kNumVariants - 2;  // generic, for m2 read back after its encode
+constexpr int kNumSpecialised = kSampledReadVariant;
 
 // Stand-alone codec kernels (one wave tile per wave, grid-stride).
 __global__ void __launch_bounds__(kThreads) quantize_kernel(const float* __restrict__ values, int64_t numel,
@@ -449,6 +454,14 @@ int check_moment(const aw4_moment& m, int64_t numel, int index, const char* name
     }
     if (m.rounding == AW4_ROUND_UPDATE_SR && !(m.sr_bias > 0.0f))
         return set_error(AW4_EINVAL, "tensor %d: %s update-SR bias must be positive", index, name);
+    if (m.flags & (AW4_MOMENT_SAMPLED_READ | AW4_MOMENT_READ_RAW_SCALE)) {
+        if (strcmp(name, "m2") != 0)
+            return set_error(AW4_EINVAL, "tensor %d: only m2 can be read back after its encode", index);
+        if (!(m.flags & AW4_MOMENT_SAMPLED_READ))
+            return set_error(AW4_EINVAL, "tensor %d: m2 READ_RAW_SCALE without SAMPLED_READ", index);
+        if (m.values && !aligned(m.values, 16))
+            return set_error(AW4_EALIGN, "tensor %d: m2 preconditioner output not 16-byte aligned", index);
+    }
     return AW4_OK;
 }
 
@@ -485,16 +498,22 @@ struct LaunchGroup {
 // the generic kernel.  A recipe's table is one launch.
 std::vector<LaunchGroup> plan_launches(const aw4_tensor* ts, int32_t count) {
     std::vector<LaunchGroup> groups;
-    LaunchGroup generic;
+    LaunchGroup generic, sampled;
+    generic.variant = kGenericVariant;
+    sampled.variant = kSampledReadVariant;
     std::vector<int> values;
     for (int i = 0; i < count; ++i) {
         const aw4_tensor& t = ts[i];
+        if (host_values_only(t)) {
+            if (t.param_dtype != t.grad_dtype) generic.members.push_back(i); else values.push_back(i);
+            continue;
+        }
+        if (t.m2.flags & AW4_MOMENT_SAMPLED_READ) { sampled.members.push_back(i); continue; }
         if (t.param_dtype != t.grad_dtype) { generic.members.push_back(i); continue; }
-        if (host_values_only(t)) { values.push_back(i); continue; }
         const int s1 = mspec(t.m1.rounding, t.m1.flags & spec_flags_mask(t.m1.rounding));
         const int s2 = mspec(t.m2.rounding, t.m2.flags & spec_flags_mask(t.m2.rounding));
         int v = kGenericVariant;
-        for (int k = 0; k < kGenericVariant; ++k)
+        for (int k = 0; k < kNumSpecialised; ++k)
             if (kVariants[k].dtype == t.param_dtype && kVariants[k].m1 == s1 && kVariants[k].m2 == s2) { v = k; break; }
         if (v == kGenericVariant) { generic.members.push_back(i); continue; }
         const bool f1 = t.m1.rounding == AW4_ROUND_FP32, f2 = t.m2.rounding == AW4_ROUND_FP32;
@@ -517,7 +536,7 @@ std::vector<LaunchGroup> plan_launches(const aw4_tensor* ts, int32_t count) {
             if (kVariants[c.variant].dtype == ts[i].param_dtype) { g = &c; break; }
         if (!g && !generic.members.empty()) g = &generic;
         if (!g) {
-            for (int k = 0; k < kGenericVariant && !g; ++k) {
+            for (int k = 0; k < kNumSpecialised && !g; ++k) {
                 if (kVariants[k].dtype != ts[i].param_dtype) continue;
                 groups.emplace_back();
                 g = &groups.back();
@@ -526,6 +545,7 @@ std::vector<LaunchGroup> plan_launches(const aw4_tensor* ts, int32_t count) {
         }
         (g ? g : &generic)->members.push_back(i);
     }
+    if (!sampled.members.empty()) groups.push_back(std::move(sampled));
     if (!generic.members.empty()) groups.push_back(std::move(generic));
     for (LaunchGroup& g : groups) std::sort(g.members.begin(), g.members.end());
     return groups;

@@ -98,7 +98,9 @@ ROUND_UPDATE_SR = 3  # preconditioner-space stochastic rounding (_compiled_quant
 
 # scheme -> (codebook id, rounding rule, floor code 0 to code 1)
 # Covers every scheme the reference's optimized path accepts (_optimized.py:36-41)
-# plus the non-optimized update-SR names that share a codebook.
+# plus the reference-step update-SR names that share a codebook and rule: the
+# fp32-read, sampled-read and store-side-EDEN variants differ only in what the
+# step reads back and stores (adamw.py:615-683).
 SCHEMES: Dict[str, Tuple[int, int, bool]] = {
     "nf4": (CB_NF4, ROUND_RTN, False),
     "nf4_sr": (CB_NF4, ROUND_STATE_SR, False),
@@ -114,7 +116,17 @@ SCHEMES: Dict[str, Tuple[int, int, bool]] = {
     "dyn4_upd_sr_fp32read": (CB_DYN4, ROUND_UPDATE_SR, False),
     "dyn4_lookahead_sr": (CB_DYN4, ROUND_UPDATE_SR, False),
     "dyn4_upd_sr_fp32read_nextbc": (CB_DYN4, ROUND_UPDATE_SR, False),
+    "lin4_upd_sr": (CB_LIN4, ROUND_UPDATE_SR, False),
+    "dyn4_upd_sr": (CB_DYN4, ROUND_UPDATE_SR, False),
+    "lin4_upd_sr_store_eden": (CB_LIN4, ROUND_UPDATE_SR, False),
+    "dyn4_upd_sr_store_eden": (CB_DYN4, ROUND_UPDATE_SR, False),
 }
+
+# m2 schemes whose update reads back the sampled value (adamw.py:636-656) and those that
+# also keep 1 / denominator as state "m2_read_preconditioner" and apply EDEN to the stored
+# scale only (adamw.py:615-635).
+SAMPLED_READ_SCHEMES = frozenset({"lin4_upd_sr", "dyn4_upd_sr"})
+STORE_EDEN_SCHEMES = frozenset({"lin4_upd_sr_store_eden", "dyn4_upd_sr_store_eden"})
 
 STOCHASTIC_ROUNDING = (ROUND_STATE_SR, ROUND_UPDATE_SR)
 

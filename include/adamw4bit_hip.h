@@ -61,6 +61,15 @@ extern "C" {
 #define AW4_MOMENT_GUARDS 0x4     /* exact-level SR guards of the optimized path (_compiled_quantization.py:48-57);
                                      clear for the reference step (quantization.py:279-377) */
 #define AW4_MOMENT_EXT_DRAWS 0x8  /* read uniforms from aw4_moment.draws instead of on-device Philox */
+/* m2 only: the parameter update's denominator reads the value just stored,
+ * cb[code] * scale, instead of the fp32 lerp (dyn4_upd_sr / lin4_upd_sr,
+ * adamw.py:636-656, quantization.py:748-776).  If `values` is set it receives
+ * 1 / denominator per element (m2_read_preconditioner, adamw.py:632). */
+#define AW4_MOMENT_SAMPLED_READ 0x10
+/* with AW4_MOMENT_SAMPLED_READ: read with the scale before the EDEN calibration
+ * that AW4_MOMENT_EDEN applies to the stored scale (*_upd_sr_store_eden,
+ * adamw.py:615-635, quantization.py:1007-1037) */
+#define AW4_MOMENT_READ_RAW_SCALE 0x20
 
 /* aw4_tensor.param_dtype / grad_dtype */
 #define AW4_F32 0
@@ -75,14 +84,15 @@ extern "C" {
 /*
  * One moment (m1 or m2) of one parameter.  For a quantized moment, `codes`
  * holds ceil(numel/2) bytes (element 2j in the low nibble of byte j) and
- * `scales` numel/128 fp32 block scales; `values` is 0.  For an fp32-state
- * moment only `values` (numel fp32) is set.  Layout as in optimizer.state
- * (_moment_buffer.py:89-142, adamw.py:326-362).
+ * `scales` numel/128 fp32 block scales; `values` is 0, or, for an m2 with
+ * AW4_MOMENT_SAMPLED_READ, the numel fp32 outputs of 1 / denominator.  For an
+ * fp32-state moment only `values` (numel fp32) is set.  Layout as in
+ * optimizer.state (_moment_buffer.py:89-142, adamw.py:326-362).
  */
 typedef struct aw4_moment {
     uint64_t codes;      /* device address, uint8[ceil(numel/2)] or 0 */
     uint64_t scales;     /* device address, float[numel/128] or 0 */
-    uint64_t values;     /* device address, float[numel] or 0 */
+    uint64_t values;     /* device address, float[numel] (fp32 state, or SAMPLED_READ output) or 0 */
     uint64_t draws;      /* device address, float[numel] uniforms (AW4_MOMENT_EXT_DRAWS) or 0 */
     uint64_t rng_seed;   /* Philox4x32-10 key: generator seed of this moment's stream */
     uint64_t rng_offset; /* stream position of this write's first draw; multiple of 128 */

@@ -18,7 +18,12 @@ order, the parts of ``adamw4bit`` that the fused HIP step replaces:
 * the default reference step (``adamw.py:472-805``) for the scheme set shared with
   the optimized path; it differs only in having no endpoint guards in stochastic
   rounding (``quantization.py:279-377``) and in drawing ``numel`` uniforms when a
-  stochastic moment is initialized (``adamw.py:524-545``).
+  stochastic moment is initialized (``adamw.py:524-545``);
+* the reference step's read-back m2 schemes (``dyn4_upd_sr``, ``lin4_upd_sr``,
+  ``*_upd_sr_store_eden``, ``adamw.py:615-656``), whose update uses the m2 just
+  encoded (``_update_sampled_read``).  A parameter whose schemes the optimized
+  backend does not accept takes the reference step, as the backend's preflight
+  sends it there (``_optimized.py:94-126``).
 
 Because the operations are ATen CPU kernels called in the reference's order, the
 element arithmetic (lerp as a fused multiply-add, true division, the 8-lane by
@@ -82,11 +87,18 @@ def codebook(mode: str) -> torch.Tensor:
 
 RTN_SCHEMES = {"nf4", "sdyn4", "lin4", "lin4_nz", "dyn4", "dyn4_nz"}
 STATE_SR_SCHEMES = {"nf4_sr", "sdyn4_sr", "lin4_sr", "dyn4_sr"}
-UPDATE_SR_SCHEMES = {"lin4_upd_sr_fp32read", "dyn4_upd_sr_fp32read", "dyn4_lookahead_sr",
+FP32_READ_SCHEMES = {"lin4_upd_sr_fp32read", "dyn4_upd_sr_fp32read", "dyn4_lookahead_sr",
                      "dyn4_upd_sr_fp32read_nextbc"}
+# Reference-step m2 schemes whose update reads the sampled value back (adamw.py:636-656), and
+# those that read it with the pre-EDEN scale, store the EDEN-calibrated scale and keep
+# 1 / denominator as "m2_read_preconditioner" (adamw.py:615-635).  Same update-SR rule
+# (quantization.py:318-377, 486-526).
+SAMPLED_READ_SCHEMES = {"lin4_upd_sr", "dyn4_upd_sr"}
+STORE_EDEN_SCHEMES = {"lin4_upd_sr_store_eden", "dyn4_upd_sr_store_eden"}
+UPDATE_SR_SCHEMES = FP32_READ_SCHEMES | SAMPLED_READ_SCHEMES | STORE_EDEN_SCHEMES
 NEXT_BIAS_SCHEMES = {"dyn4_lookahead_sr", "dyn4_upd_sr_fp32read_nextbc"}
 M1_SCHEMES = {"fp32", "nf4", "nf4_sr", "sdyn4", "sdyn4_sr"}            # _optimized.py:36
-M2_SCHEMES = {"fp32", "lin4", "lin4_sr", "lin4_nz", "dyn4", "dyn4_sr", "dyn4_nz"} | UPDATE_SR_SCHEMES
+M2_SCHEMES = {"fp32", "lin4", "lin4_sr", "lin4_nz", "dyn4", "dyn4_sr", "dyn4_nz"} | FP32_READ_SCHEMES
 
 
 def is_stochastic(mode: str) -> bool:
@@ -201,6 +213,7 @@ class ParamState:
     step: int = 0
     m1: Optional[MomentState] = None
     m2: Optional[MomentState] = None
+    read_preconditioner: Optional[torch.Tensor] = None  # store-EDEN schemes: 1 / denominator
 
 
 @dataclass
@@ -254,6 +267,7 @@ class Oracle:
         self.draw_fn = draw_fn
         self.draw_log: List[DrawLog] = []
         self.draw_counts = {"m1": 0, "m2": 0}
+        self._param_optimized = True  # the optimized backend accepts the parameter's schemes
 
     # -- random draws -------------------------------------------------------
     def _draw(self, moment: str, n: int, param: int, step: int, log: bool) -> torch.Tensor:
@@ -272,14 +286,15 @@ class Oracle:
         n = p.numel()
         if scheme == "fp32":
             return MomentState("fp32", values=torch.zeros(n, dtype=torch.float32))
-        if self.optimized:
+        optimized = self.optimized and self._param_optimized
+        if optimized:
             # _moment_buffer.py:106-126: encode one zero tile, broadcast its first byte/scale.
             tile = n if n <= self.chunk else math.lcm(BLOCK, 2)
         else:
             tile = n  # adamw.py:524-545 encodes the whole zero tensor
         draws = self._draw(moment, tile, index, 0, log=False) if is_stochastic(scheme) else None
         codes, scales = encode(torch.zeros(tile, dtype=torch.float32), scheme, eden=eden,
-                               draws=draws, guards=self.optimized)
+                               draws=draws, guards=optimized)
         byte = pack(codes)[:1]
         return MomentState(scheme, codes=byte.expand((n + 1) // 2).clone(),
                            scales=scales[:1].expand(n // BLOCK).clone())
@@ -295,6 +310,10 @@ class Oracle:
         s1 = effective_scheme(n, self.m1_schemes[index])
         s2 = effective_scheme(n, self.m2_schemes[index])
         eden = self.eden[index]
+        # The optimized backend's preflight sends other scheme pairs to the reference step
+        # (_optimized.py:94-126).
+        self._param_optimized = s1 in M1_SCHEMES and s2 in M2_SCHEMES
+        optimized = self.optimized and self._param_optimized
         if st.step == 0:
             st.m1 = self._init_moment(index, "m1", s1, False)
             st.m2 = self._init_moment(index, "m2", s2, eden)
@@ -307,7 +326,10 @@ class Oracle:
         storage_bc = 1 - b2 ** (st.step + 1) if s2 in NEXT_BIAS_SCHEMES else bc2
         flat_p = p.view(-1)
         flat_g = grad.reshape(-1)
-        chunk = self._chunk_size(s1, s2) if self.optimized else n
+        if s2 in SAMPLED_READ_SCHEMES or s2 in STORE_EDEN_SCHEMES:
+            self._update_sampled_read(index, st, flat_p, flat_g, s2, eden, bc1, bc2)
+            return
+        chunk = self._chunk_size(s1, s2) if optimized else n
         for start in range(0, n, chunk):
             stop = min(start + chunk, n)
             self._update_chunk(index, st, flat_p[start:stop], flat_g[start:stop], start, stop,
@@ -334,6 +356,40 @@ class Oracle:
         self._write(st.m1, m1, start, stop, eden=False, draws=draws, bias=1.0, eps=1e-8)
         draws = self._draw("m2", n, index, st.step, True) if is_stochastic(s2) else None
         self._write(st.m2, m2, start, stop, eden=eden, draws=draws, bias=storage_bc, eps=hp.eps)
+        if s2 not in STORE_EDEN_SCHEMES:
+            st.read_preconditioner = None
+
+    def _update_sampled_read(self, index, st, p, grad, s2, eden, bc1, bc2):
+        """The reference step for m2 schemes read back after their encode (adamw.py:615-656):
+        m2 is encoded first (update-SR towards the current bias correction) and the
+        denominator uses cb[code] * scale -- the stored scale, or for ``*_store_eden`` the scale
+        before EDEN, whose calibration goes only to the stored scale
+        (``quantize_with_dequantized``, ``apply_eden_correction_to_quant_state``,
+        quantization.py:748-776, 1007-1037)."""
+        hp = self.hyper
+        n = p.numel()
+        g = grad.to(dtype=torch.float32)
+        m1 = self._read(st.m1, 0, n)
+        m2 = self._read(st.m2, 0, n)
+        m1.lerp_(g, 1 - hp.betas[0])
+        m2.lerp_(g.square(), 1 - hp.betas[1])
+        draws = self._draw("m2", n, index, st.step, True)
+        store_eden = s2 in STORE_EDEN_SCHEMES
+        codes, read_scales = encode(m2, s2, eden=eden and not store_eden, draws=draws, bias=bc2, eps=hp.eps,
+                                    guards=False)
+        stored_scales = read_scales
+        if store_eden:
+            _, stored_scales = encode(m2, s2, eden=True, draws=draws, bias=bc2, eps=hp.eps, guards=False)
+        packed = pack(codes)
+        m2_read = decode(packed, read_scales, s2, n)
+        den = (m2_read.sqrt() / math.sqrt(bc2)).add_(hp.eps)
+        st.read_preconditioner = den.reciprocal() if store_eden else None
+        p.mul_(1 - hp.lr * hp.weight_decay)
+        p.addcdiv_(m1, den, value=-hp.lr / bc1)
+        draws = self._draw("m1", n, index, st.step, True) if is_stochastic(st.m1.scheme) else None
+        self._write(st.m1, m1, 0, n, eden=False, draws=draws, bias=1.0, eps=1e-8)
+        st.m2.codes[:] = packed
+        st.m2.scales[:] = stored_scales
 
     @staticmethod
     def _read(ms: MomentState, start: int, stop: int) -> torch.Tensor:
@@ -346,6 +402,6 @@ class Oracle:
         if ms.scheme == "fp32":
             return  # the read view was updated in place
         codes, scales = encode(value, ms.scheme, eden=eden, draws=draws, bias=bias, eps=eps,
-                               guards=self.optimized)
+                               guards=self.optimized and self._param_optimized)
         ms.codes[start // 2:(stop + 1) // 2] = pack(codes)
         ms.scales[start // BLOCK:stop // BLOCK] = scales

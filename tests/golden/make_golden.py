@@ -65,6 +65,8 @@ def snapshot(opt, params, prefix, out):
                 out[f"{prefix}p{i}_{m}_scale"] = to_np(qs.absmax)
             else:
                 out[f"{prefix}p{i}_{m}_fp32"] = to_np(st[m])
+        if "m2_read_preconditioner" in st:
+            out[f"{prefix}p{i}_m2_pre"] = to_np(st["m2_read_preconditioner"])
 
 
 def trajectory(name, build, shapes, dtype, steps, *, grad_seed, snap_steps, m1_override=None,
@@ -225,6 +227,14 @@ def main():
                "float32", 5, grad_seed=8, snap_steps={5}, m1_override=([0], "nf4_sr"))
     trajectory("refstep_zeeden_bf16", recipe(ZEEDENAdamW4Bit, optimized=False), [(4096,)],
                "bfloat16", 4, grad_seed=9, snap_steps={4})
+    trajectory("sampled_read_groups",
+               grouped([("nf4", "dyn4_upd_sr", False), ("nf4_sr", "lin4_upd_sr", True),
+                        ("fp32", "dyn4_upd_sr_store_eden", False), ("sdyn4", "lin4_upd_sr_store_eden", False),
+                        ("nf4", "dyn4_upd_sr", True)],
+                       seed=11),
+               [(4096,)] * 4 + [(64, 128)], "float32", 3, grad_seed=10, snap_steps={1, 3}, zero_block_frac=0.05)
+    trajectory("sampled_read_bf16", grouped([("nf4", "dyn4_upd_sr_store_eden", False)], seed=12), [(4096,)],
+               "bfloat16", 3, grad_seed=11, snap_steps={3})
     codec_cases()
     checkpoint_case()
 

@@ -89,8 +89,8 @@ def test_header_constants_match_python():
     assert val["AW4_ROUND_STATE_SR"] == q.ROUND_STATE_SR and val["AW4_ROUND_UPDATE_SR"] == q.ROUND_UPDATE_SR
     assert val["AW4_NUM_LUTS"] == _lib.NUM_LUTS and val["AW4_LUT_HALF"] == _lib.LUT_HALF
     assert val["AW4_LUT_EXP0"] == _lib.LUT_EXP0 and val["AW4_BLOCK"] == _lib.BLOCK
-    for name in ("MOMENT_ZERO_FLOOR", "MOMENT_EDEN", "MOMENT_GUARDS", "MOMENT_EXT_DRAWS",
-                 "TENSOR_LERP1_LARGE", "TENSOR_LERP2_LARGE", "TENSOR_VEC_ALIGNED", "F32", "BF16", "F16"):
+    for name in ("MOMENT_ZERO_FLOOR", "MOMENT_EDEN", "MOMENT_GUARDS", "MOMENT_EXT_DRAWS", "MOMENT_SAMPLED_READ",
+                 "MOMENT_READ_RAW_SCALE", "TENSOR_LERP1_LARGE", "TENSOR_LERP2_LARGE", "TENSOR_VEC_ALIGNED", "F32", "BF16", "F16"):
         assert val[f"AW4_{name}"] == getattr(_lib, name), name
 
 

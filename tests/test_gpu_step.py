@@ -187,6 +187,13 @@ def test_golden_trajectory(name):
                 else:
                     assert torch.equal(H.bits(st[f"{m}_fp32"].reshape(-1)),
                                        H.bits(torch.from_numpy(arrays[f"{pre}_{m}_fp32"]).reshape(-1))), (name, m)
+            # 1 / denominator of the store-EDEN schemes: within the square root's ulp
+            if f"{pre}_m2_pre" in arrays:
+                got = opt.state[p]["m2_read_preconditioner"].cpu().reshape(-1)
+                torch.testing.assert_close(got, torch.from_numpy(arrays[f"{pre}_m2_pre"]).reshape(-1),
+                                           rtol=1e-6, atol=0.0)
+            else:
+                assert "m2_read_preconditioner" not in opt.state[p]
             exact = H.assert_params_close(p, tensor(arrays[pre], cfg["dtype"]).reshape(p.shape),
                                           f"{name} step {k+1} p{i}", steps=k + 1)
             log(f"  p{i}: parameters bit-exact {exact:.6f}")
@@ -286,6 +293,34 @@ def test_zipsr_philox_matches_oracle():
     out = run_pair(lambda ps: aw.ZIPSRAdamW4Bit(ps, **args), [(512, 1024), (256, 128)], torch.float32, 6, seed=0,
                    m1_override=([1], "nf4_sr"))
     compare_pair(*out, "zipsr philox")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_sampled_read_schemes_match_oracle(dtype):
+    """m2 read back after its encode (reference step, adamw.py:615-656): dyn4_upd_sr / lin4_upd_sr
+    take the denominator from the stored sample, *_upd_sr_store_eden from the sample at the scale
+    before EDEN and keep 1 / denominator as state; on-device Philox replayed into the oracle."""
+    log(f"sampled-read schemes {dtype} x 4 steps")
+    spec = [("nf4", "dyn4_upd_sr", False), ("nf4_sr", "lin4_upd_sr", True), ("fp32", "dyn4_upd_sr_store_eden", False),
+            ("sdyn4", "lin4_upd_sr_store_eden", False), ("nf4", "dyn4_nz", True)]
+
+    def make(ps):
+        groups = [dict(params=[p], m1_quant_scheme=a, m2_quant_scheme=b, use_eden_m2=e) for p, (a, b, e) in zip(ps, spec)]
+        return aw.QuantizedAdamW(groups, lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True,
+                                 quant_rng_seed=3, m1_quant_scheme="nf4", m2_quant_scheme="dyn4_nz")
+    out = run_pair(make, [(512, 1024), (256, 512), (384, 128), (1024, 256), (128, 256)], dtype, 4, seed=3,
+                   zero_block_frac=0.02)
+    compare_pair(*out, f"sampled read {dtype}", steps=4)
+    opt, params, oracle, _, parted = out
+    for i, p in enumerate(params):
+        expect = oracle.states[i].read_preconditioner
+        if expect is None:
+            assert "m2_read_preconditioner" not in opt.state[p], i
+            continue
+        got = opt.state[p]["m2_read_preconditioner"].cpu().reshape(-1)
+        keep = ~parted[i]
+        torch.testing.assert_close(got[keep], expect.reshape(-1)[keep], rtol=1e-6, atol=0.0)
+        assert got.shape[0] == p.numel() and "m2" not in opt.state[p]
 
 
 def test_zipsr_4096x4096_matches_oracle():

@@ -1,0 +1,88 @@
+"""The optimizer's host API without a GPU: constructor validation with the reference's own
+messages (``adamw.py:127-239``), the scheme set this build steps, and the errors for the
+parts it does not (the reference's tests ``tests/quantization/test_upd_sr_store_eden.py``,
+``test_dyn4_la_upd_sr.py`` and ``test_upd_sr_full4bit.py`` exercise the same paths)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import adamw4bit_amd as aw
+from adamw4bit_amd import quantization as q
+
+
+def params():
+    return [torch.nn.Parameter(torch.zeros(4096))]
+
+
+def make(**kw):
+    base = dict(m1_quant_scheme="nf4", m2_quant_scheme="dyn4_nz")
+    base.update(kw)
+    return aw.QuantizedAdamW(params(), **base)
+
+
+@pytest.mark.parametrize("kw,message", [
+    (dict(lr=-1.0), "Invalid learning rate"),
+    (dict(eps=-1.0), "Invalid epsilon value"),
+    (dict(betas=(1.0, 0.95)), "Invalid beta parameter at index 0"),
+    (dict(betas=(0.9, -0.1)), "Invalid beta parameter at index 1"),
+    (dict(weight_decay=-0.1), "Invalid weight_decay value"),
+    (dict(quant_rng_seed=-3), "quant_rng_seed must be a non-negative integer"),
+    (dict(m2_quant_scheme="dyn5"), "m2_quant_scheme must be one of"),
+    (dict(m2_quant_scheme="dyn4_sr", use_eden_m2=True), "Vanilla stochastic-rounding m2 schemes"),
+])
+def test_constructor_rejects_bad_arguments(kw, message):
+    with pytest.raises(ValueError, match=message):
+        make(**kw)
+
+
+@pytest.mark.parametrize("mode", ["lin4_upd_sr_store_eden", "dyn4_upd_sr_store_eden"])
+def test_store_eden_rejects_use_eden_m2(mode):
+    # test_upd_sr_store_eden.py:69-82
+    with pytest.raises(ValueError, match="EDEN is built into the store path"):
+        make(m1_quant_scheme="fp32", m2_quant_scheme=mode, use_eden_m2=True)
+
+
+@pytest.mark.parametrize("scheme", ["dyn4_la_upd_sr", "dyn4_proxy_la_upd_sr", "dyn4_vproxy_la_upd_sr"])
+def test_lookahead_rejects_extra_corrections(scheme):
+    # test_dyn4_la_upd_sr.py:322-330: validated before anything else
+    with pytest.raises(ValueError, match="supports m1_quant_scheme"):
+        make(m1_quant_scheme="sdyn4", m2_quant_scheme=scheme)
+    with pytest.raises(ValueError, match="use_eden_m2"):
+        make(m1_quant_scheme="fp32", m2_quant_scheme=scheme, use_eden_m2=True)
+    with pytest.raises(ValueError, match="update clipping"):
+        make(m1_quant_scheme="fp32", m2_quant_scheme=scheme, update_norm_clip=1.0)
+
+
+@pytest.mark.parametrize("m2", ["dyn4_upd_sr", "lin4_upd_sr", "dyn4_upd_sr_store_eden", "lin4_upd_sr_store_eden",
+                                "dyn4_upd_sr_fp32read", "lin4_upd_sr_fp32read", "dyn4_lookahead_sr",
+                                "dyn4_upd_sr_fp32read_nextbc", "dyn4_nz", "lin4_nz", "dyn4", "lin4", "dyn4_sr",
+                                "lin4_sr", "fp32"])
+@pytest.mark.parametrize("m1", ["nf4", "nf4_sr", "sdyn4", "sdyn4_sr", "fp32"])
+def test_schemes_of_the_fused_step_construct(m1, m2):
+    opt = make(m1_quant_scheme=m1, m2_quant_scheme=m2)
+    group = opt.param_groups[0]
+    assert group["m1_quant_scheme"] == m1 and group["m2_quant_scheme"] == m2
+    for s in (m1, m2):
+        if s != "fp32":
+            assert q.default_block_size(s) == 128 and s in q.SCHEMES
+
+
+@pytest.mark.parametrize("kw", [
+    dict(m1_quant_scheme="linear"), dict(m2_quant_scheme="dynamic"),
+    dict(m1_quant_scheme="fp32", m2_quant_scheme="dyn4_la_upd_sr"),
+    dict(m1_quant_scheme="nf4", m2_quant_scheme="dyn4_proxy_la_upd_sr"),
+    dict(m1_quant_scheme="fp32", m2_quant_scheme="dyn4_vproxy_la_upd_sr"),
+    dict(update_sign_clip=0.5), dict(record_update_direction_every=2), dict(block_size=256),
+])
+def test_parts_outside_the_fused_step_raise(kw):
+    with pytest.raises(NotImplementedError):
+        make(**kw)
+
+
+def test_step_needs_a_hip_device():
+    opt = make()
+    opt.param_groups[0]["params"][0].grad = torch.ones(4096)
+    with pytest.raises(NotImplementedError, match="HIP devices"):
+        opt.step()
