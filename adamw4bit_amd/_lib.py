@@ -17,7 +17,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIBRARY = os.path.join(HERE, "libadamw4bit_hip.so")
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 BLOCK = 128
 
 # Error codes
@@ -25,9 +25,9 @@ OK, EINVAL, EHIP, EALIGN = 0, -1, -2, -3
 
 # Codebooks / rounding / flags (AW4_* in the header)
 CB_NF4, CB_SDYN4, CB_DYN4, CB_LIN4, CB_LIN4_NZ = 0, 1, 2, 3, 4
-ROUND_FP32, ROUND_RTN, ROUND_STATE_SR, ROUND_UPDATE_SR = 0, 1, 2, 3
+ROUND_FP32, ROUND_RTN, ROUND_STATE_SR, ROUND_UPDATE_SR, ROUND_LOOKAHEAD_SR = 0, 1, 2, 3, 4
 MOMENT_ZERO_FLOOR, MOMENT_EDEN, MOMENT_GUARDS, MOMENT_EXT_DRAWS = 0x1, 0x2, 0x4, 0x8
-MOMENT_SAMPLED_READ, MOMENT_READ_RAW_SCALE = 0x10, 0x20
+MOMENT_SAMPLED_READ, MOMENT_READ_RAW_SCALE, MOMENT_FRESH_PROXY, MOMENT_PENDING = 0x10, 0x20, 0x40, 0x80
 F32, BF16, F16 = 0, 1, 2
 TENSOR_LERP1_LARGE, TENSOR_LERP2_LARGE, TENSOR_VEC_ALIGNED = 0x1, 0x2, 0x4
 
@@ -39,6 +39,7 @@ MOMENT = np.dtype([
     ("rng_seed", "<u8"), ("rng_offset", "<u8"),
     ("codebook", "<i4"), ("rounding", "<i4"), ("flags", "<i4"),
     ("sr_bias", "<f4"), ("sr_bias_rcp", "<f4"), ("sr_eps", "<f4"),
+    ("la_beta2", "<f8"), ("la_fresh_weight", "<f8"), ("la_bias", "<f8"), ("la_eps", "<f8"),
 ])
 TENSOR = np.dtype([
     ("param", "<u8"), ("grad", "<u8"), ("numel", "<i8"),
@@ -47,7 +48,7 @@ TENSOR = np.dtype([
     ("bc2_sqrt", "<f4"), ("bc2_sqrt_rcp", "<f4"), ("eps", "<f4"),
     ("m1", MOMENT), ("m2", MOMENT),
 ])
-assert MOMENT.itemsize == 72 and TENSOR.itemsize == 208
+assert MOMENT.itemsize == 104 and TENSOR.itemsize == 272
 
 # Every function the header declares, with its ctypes signature.
 SIGNATURES = {

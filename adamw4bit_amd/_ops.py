@@ -4,7 +4,7 @@ It wraps the C ABI's ``aw4_fused_step`` (``include/adamw4bit_hip.h``) so that th
 opaque operator to PyTorch: it declares which tensors it writes (parameters and moment
 states, updated in place) and which it reads (gradients, caller-provided draws), and it runs
 on the current stream of the parameters' device.  ``table`` is the launch table, a CPU uint8
-tensor of ``aw4_tensor`` rows (208 bytes each) that hold the device addresses of the listed
+tensor of ``aw4_tensor`` rows (272 bytes each) that hold the device addresses of the listed
 tensors.  There is no implementation other than the HIP library.
 """
 

@@ -39,10 +39,15 @@ from torch.optim.optimizer import Optimizer
 from . import _lib, _ops
 from ._rng import PhiloxStream
 from .quantization import (
+    LOOKAHEAD_SCHEMES,
     NEXT_BIAS_SCHEMES,
+    PENDING_KEY,
+    PENDING_LOOKAHEAD_SCHEMES,
+    VPROXY_LOOKAHEAD_SCHEMES,
     SAMPLED_READ_SCHEMES,
     STORE_EDEN_SCHEMES,
     QuantState,
+    ROUND_LOOKAHEAD_SR,
     ROUND_STATE_SR,
     ROUND_UPDATE_SR,
     SCHEMES,
@@ -62,11 +67,8 @@ _OPT_M2_SCHEMES = {
     "lin4_upd_sr_fp32read", "dyn4_upd_sr_fp32read", "dyn4_lookahead_sr", "dyn4_upd_sr_fp32read_nextbc",
 }
 _DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
-_UNSUPPORTED_SCHEMES = {
-    "linear": "8-bit linear state", "dynamic": "8-bit dynamic state",
-    "dyn4_la_upd_sr": "oracle lookahead update-SR", "dyn4_proxy_la_upd_sr": "proxy lookahead update-SR",
-    "dyn4_vproxy_la_upd_sr": "v-proxy lookahead update-SR",
-}
+_UNSUPPORTED_SCHEMES = {"linear": "8-bit linear state", "dynamic": "8-bit dynamic state"}
+_SR_ROUNDINGS = (ROUND_STATE_SR, ROUND_UPDATE_SR, ROUND_LOOKAHEAD_SR)  # roundings that draw uniforms
 
 
 def _f32(x: float) -> float:
@@ -550,7 +552,7 @@ class QuantizedAdamW(Optimizer):
             if _overlaps(occupied[0], _byte_range(grad)):
                 grad = grad.clone()
             occupied.append(_byte_range(grad))
-            for key in ("m1", "m2", "m1_code", "m2_code"):
+            for key in ("m1", "m2", "m1_code", "m2_code", PENDING_KEY):
                 value = state.get(key)
                 if isinstance(value, torch.Tensor):
                     if any(_overlaps(_byte_range(value), r) for r in occupied):
@@ -590,7 +592,15 @@ class QuantizedAdamW(Optimizer):
         m1 = self._moment_row(p, state, "m1", schemes[0], False, optimized, 1.0, 1e-8, keep, written)
         m2 = self._moment_row(p, state, "m2", schemes[1], group["use_eden_m2"], optimized,
                               c.storage_bias, group["eps"], keep, written)
-        if schemes[1] in STORE_EDEN_SCHEMES:
+        if schemes[1] in LOOKAHEAD_SCHEMES:
+            # adamw.py:566-614: the pending form samples the fp32 state with bias_c2 before the
+            # update; the proxies encode the new m2 for the next step's bias correction.
+            beta2 = float(group["betas"][1])
+            bias = 1 - beta2 ** step if schemes[1] in PENDING_LOOKAHEAD_SCHEMES else 1 - beta2 ** (step + 1)
+            flags = m2[8] | (_lib.MOMENT_FRESH_PROXY if schemes[1] in VPROXY_LOOKAHEAD_SCHEMES else 0)
+            m2 = m2[:8] + (flags,) + m2[9:12] + (beta2, 1.0 - beta2, max(float(bias), 1e-12), float(group["eps"]))
+            state.pop("m2_read_preconditioner", None)
+        elif schemes[1] in STORE_EDEN_SCHEMES:
             # Reads with the scale before EDEN; stores the calibrated scale and 1/denominator.
             pre = state.get("m2_read_preconditioner")
             if not (isinstance(pre, torch.Tensor) and pre.shape == p.shape and pre.dtype == torch.float32
@@ -616,6 +626,9 @@ class QuantizedAdamW(Optimizer):
             state.pop(f"{moment}_code", None)
             state.pop(f"{moment}_quant_state", None)
             return
+        if scheme in PENDING_LOOKAHEAD_SCHEMES:  # adamw.py:534-535
+            state[PENDING_KEY] = torch.zeros(p.shape, device=p.device, dtype=torch.float32)
+            return
         code, scale = initial_code_and_scale(scheme, eden)
         state[f"{moment}_code"] = torch.full(((n + 1) // 2,), code | (code << 4), dtype=torch.uint8, device=p.device)
         absmax = torch.full((n // size,), scale, dtype=torch.float32, device=p.device)
@@ -630,15 +643,16 @@ class QuantizedAdamW(Optimizer):
     def _check_moment(self, p, state, moment, scheme) -> None:
         """Accept existing state in the layout the kernel writes (``_moment_buffer.py:54-87,127-141``)."""
         n = p.numel()
-        if scheme == "fp32":
-            value = state.get(moment)
+        if scheme == "fp32" or scheme in PENDING_LOOKAHEAD_SCHEMES:
+            key = moment if scheme == "fp32" else PENDING_KEY
+            value = state.get(key)
             if value is None and f"{moment}_code" in state:
-                raise NotImplementedError(f"{moment}: quantized state found where the scheme is fp32")
+                raise NotImplementedError(f"{moment}: quantized state found where the scheme keeps fp32 state")
             if not (isinstance(value, torch.Tensor) and value.device == p.device and value.dtype == torch.float32
                     and value.numel() == n):
-                raise ValueError(f"{moment}: fp32 state does not match the parameter")
+                raise ValueError(f"{key}: fp32 state does not match the parameter")
             if not value.is_contiguous():
-                state[moment] = value.contiguous()
+                state[key] = value.contiguous()
             return
         codes = state.get(f"{moment}_code")
         meta = state.get(f"{moment}_quant_state")
@@ -663,28 +677,35 @@ class QuantizedAdamW(Optimizer):
         n = p.numel()
         if scheme == "fp32":
             written.append(state[moment])
-            return (0, 0, state[moment].data_ptr(), 0, 0, 0, 0, _lib.ROUND_FP32, 0, 1.0, 1.0, _f32(1e-8))
+            return (0, 0, state[moment].data_ptr(), 0, 0, 0, 0, _lib.ROUND_FP32, 0, 1.0, 1.0, _f32(1e-8),
+                    0.0, 0.0, 0.0, 0.0)
         codebook, rounding, floor_zero = SCHEMES[scheme]
         flags = (_lib.MOMENT_ZERO_FLOOR if floor_zero else 0) | (_lib.MOMENT_EDEN if eden else 0)
         if optimized:
             flags |= _lib.MOMENT_GUARDS
         seed = offset = draws = 0
-        if rounding in (ROUND_STATE_SR, ROUND_UPDATE_SR):
+        if rounding in _SR_ROUNDINGS:
             stream = self._stream(moment, p.device)
             seed, offset = stream.seed, stream.take(n)
             if self._draw_provider is not None:
+                # lookahead update-SR draws float64 uniforms (quantization.py:873-878)
+                dtype = torch.float64 if rounding == ROUND_LOOKAHEAD_SR else torch.float32
                 u = self._draw_provider(p, moment, n, p.device)
-                if u.dtype != torch.float32 or u.numel() != n or u.device != p.device:
-                    raise ValueError("draw provider must return n float32 uniforms on the parameter's device")
+                if u.dtype != dtype or u.numel() != n or u.device != p.device:
+                    raise ValueError(f"draw provider must return n {dtype} uniforms on the parameter's device")
                 u = u.contiguous()
                 keep.append(u)
                 draws = u.data_ptr()
                 flags |= _lib.MOMENT_EXT_DRAWS
         sr_bias = _f32(max(float(bias), 1e-12))
+        if scheme in PENDING_LOOKAHEAD_SCHEMES:
+            written.append(state[PENDING_KEY])
+            return (0, 0, state[PENDING_KEY].data_ptr(), draws, seed, offset, codebook, rounding,
+                    flags | _lib.MOMENT_PENDING, sr_bias, _rcp32(sr_bias), _f32(eps), 0.0, 0.0, 0.0, 0.0)
         written.append(state[f"{moment}_code"])
         written.append(state[f"{moment}_quant_state"].absmax)
         return (state[f"{moment}_code"].data_ptr(), state[f"{moment}_quant_state"].absmax.data_ptr(), 0, draws,
-                seed, offset, codebook, rounding, flags, sr_bias, _rcp32(sr_bias), _f32(eps))
+                seed, offset, codebook, rounding, flags, sr_bias, _rcp32(sr_bias), _f32(eps), 0.0, 0.0, 0.0, 0.0)
 
 
 class _LaunchPlan:
@@ -699,7 +720,8 @@ class _LaunchPlan:
     """
 
     _STRUCTURE_KEYS = ("m1_quant_scheme", "m2_quant_scheme", "use_eden_m2", "block_size", _CHUNK_KEY)
-    _STATE_KEYS = ("m1", "m2", "m1_code", "m2_code", "m1_quant_state", "m2_quant_state", "m2_read_preconditioner")
+    _STATE_KEYS = ("m1", "m2", "m1_code", "m2_code", "m1_quant_state", "m2_quant_state", "m2_read_preconditioner",
+                   PENDING_KEY)
     _MAX_RANGES = 6  # a parameter and its writable moment tensors
 
     def __init__(self):
@@ -718,8 +740,8 @@ class _LaunchPlan:
 
     @classmethod
     def build(cls, opt: "QuantizedAdamW", per_device, tables, info) -> Optional["_LaunchPlan"]:
-        if opt._draw_provider is not None:
-            return None
+        if opt._draw_provider is not None or any(schemes[1] in LOOKAHEAD_SCHEMES for _, _, schemes in info):
+            return None  # lookahead rows carry per-step constants the plan does not refresh
         plan = cls()
         meta = {id(p): schemes for p, _, schemes in info}
         group_of = {}
@@ -751,7 +773,7 @@ class _LaunchPlan:
                     lo[i, k], hi[i, k] = a, b
                 sr = tuple((moment, opt._stream(moment, p.device))
                            for moment, scheme in (("m1", schemes[0]), ("m2", schemes[1]))
-                           if scheme != "fp32" and SCHEMES[scheme][1] in (ROUND_STATE_SR, ROUND_UPDATE_SR))
+                           if scheme != "fp32" and SCHEMES[scheme][1] in _SR_ROUNDINGS)
                 entries.append((p, state, cls._state_ids(state), group_of[id(p)], schemes[1], sr, p.numel()))
             table = tables[device]
             gbytes = np.array([p.numel() * p.element_size() for p in params], dtype=np.int64)

@@ -17,12 +17,23 @@ constexpr int kBlocksPerWave = 8;   // a wave tile: 8 blocks, 8 lanes per block
 
 // Rounding kinds (AW4_ROUND_*) and "any": the kind is read from the descriptor at run time.
 enum : int { K_FP32 = AW4_ROUND_FP32, K_RTN = AW4_ROUND_RTN, K_SSR = AW4_ROUND_STATE_SR,
-             K_USR = AW4_ROUND_UPDATE_SR, K_ANY = 7 };
+             K_USR = AW4_ROUND_UPDATE_SR, K_LA = AW4_ROUND_LOOKAHEAD_SR, K_ANY = 7 };
+
+// Whether a moment keeps codes and scales in memory (a pending lookahead m2 keeps fp32
+// values but is still processed block by block).
+__host__ __device__ inline bool has_codes(int rounding, int flags) {
+    return rounding != K_FP32 && !(rounding == K_LA && (flags & AW4_MOMENT_PENDING));
+}
 
 // A moment's compile-time specification: its rounding kind and the AW4_MOMENT_* flags a
 // specialised kernel is built for (zero floor, EDEN, guards; external draws stay a run-time
-// choice).  kFlagsAtRunTime makes the encoder read the flags from the descriptor instead.
-constexpr int kFlagsAtRunTime = 0x80;
+// choice).  kFlagsAtRunTime, a bit above every AW4_MOMENT_* flag, makes the encoder read the
+// flags from the descriptor instead.
+constexpr int kFlagsAtRunTime = 0x1000;
+static_assert(kFlagsAtRunTime > (AW4_MOMENT_ZERO_FLOOR | AW4_MOMENT_EDEN | AW4_MOMENT_GUARDS | AW4_MOMENT_EXT_DRAWS |
+                                 AW4_MOMENT_SAMPLED_READ | AW4_MOMENT_READ_RAW_SCALE | AW4_MOMENT_FRESH_PROXY |
+                                 AW4_MOMENT_PENDING),
+              "run-time flag marker collides with a moment flag");
 constexpr int mspec(int kind, int flags = 0) { return kind | (flags << 4); }
 constexpr int kind_of(int spec) { return spec & 15; }
 constexpr int flags_of(int spec) { return spec >> 4; }
@@ -370,6 +381,119 @@ __device__ __forceinline__ BlockScales encode_block(const aw4_moment& M, const M
     }
     if (active && j == 0) __builtin_nontemporal_store(scale, gaddr<float>(M.scales) + blk0 + grp);
     return BlockScales{s, scale};
+}
+
+// ---------------------------------------------------------------------------
+// Lookahead update-SR (quantize_dyn4_la_upd_sr, quantization.py:779-895), in float64 as
+// the reference computes it: for levels a <= x <= b of the block-scaled value
+// x = clamp(z / s, 0, 1), with q = s * level and the next step's second moment
+// n(q) = max(beta2 * q + fresh, 0),
+//   P(lo) = (f(n(z)) - f(n(q_hi))) / max(f(n(q_lo)) - f(n(q_hi)), 1e-300),
+//   f(n) = 1 / (sqrt(n / bias) + eps),
+// replaced by 1 - clamp((z - q_lo) / max(q_hi - q_lo, 1e-300), 0, 1) where the interval is
+// flat (|f(n(q_lo)) - f(n(q_hi))| <= 1e-12 max(|f(n(q_lo))|, |f(n(q_hi))|, 1)), 1 where it is
+// degenerate (q_hi <= q_lo), clamped to [0, 1].  No guards: z at a level gives 0 or 1
+// through the formula itself.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ double clamp_min0_nan(double v) { return v < 0.0 ? 0.0 : v; }
+__device__ __forceinline__ double clamp01_nan_d(double v) { return v < 0.0 ? 0.0 : (v > 1.0 ? 1.0 : v); }
+__device__ __forceinline__ double max_nan(double a, double b) { return (a != a || b != b) ? a + b : (a > b ? a : b); }
+
+__device__ __forceinline__ double la_prob_lo(const aw4_moment& M, float z, float a, float b, float s, double fresh) {
+    const double s64 = (double)s, z64 = (double)z;
+    const double q_lo = s64 * (double)a, q_hi = s64 * (double)b;  // exact: products of two floats
+    const double beta2 = M.la_beta2;
+    const double n_lo = clamp_min0_nan(beta2 * q_lo + fresh);
+    const double n_ref = clamp_min0_nan(beta2 * z64 + fresh);
+    const double n_hi = clamp_min0_nan(beta2 * q_hi + fresh);
+    const double p_lo = 1.0 / (sqrt(n_lo / M.la_bias) + M.la_eps);
+    const double p_ref = 1.0 / (sqrt(n_ref / M.la_bias) + M.la_eps);
+    const double p_hi = 1.0 / (sqrt(n_hi / M.la_bias) + M.la_eps);
+    const double denom = p_lo - p_hi, width = q_hi - q_lo;
+    const double raw = (p_ref - p_hi) / (denom < 1e-300 ? 1e-300 : denom);
+    const double fallback = 1.0 - clamp01_nan_d((z64 - q_lo) / (width < 1e-300 ? 1e-300 : width));
+    const bool degenerate = width <= 0.0;
+    double flat_scale = max_nan(fabs(p_lo), fabs(p_hi));
+    flat_scale = flat_scale < 1.0 ? 1.0 : flat_scale;
+    const bool flat = !degenerate && fabs(denom) <= 1e-12 * flat_scale;
+    double p = flat ? fallback : raw;
+    if (degenerate) p = 1.0;
+    return clamp01_nan_d(p);
+}
+
+// Float64 uniforms of this lane's 4 values of quarter q (see draws_quarter): the
+// generator's 24-bit fields times 2^-24, or a caller's doubles (AW4_MOMENT_EXT_DRAWS).
+__device__ __forceinline__ void la_draws_quarter(const aw4_moment& M, int64_t blk0, int grp, int j, int q, bool active,
+                                                 uint32_t (&rw)[12], double (&u)[4]) {
+    if (M.flags & AW4_MOMENT_EXT_DRAWS) {
+        const gptr<const double> d = gaddr<const double>(M.draws) + (blk0 + grp) * kBlock + 32 * q + 4 * j;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) u[t] = active ? d[t] : 0.0;
+    } else {
+        if (q < 3) philox_lane_call(M.rng_seed, (M.rng_offset >> 7) + (uint64_t)(blk0 + grp), j, q, &rw[4 * q]);
+        float f[4];
+        lane_fields4(&rw[3 * q], f);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) u[t] = (double)f[t] * 0x1p-24;
+    }
+}
+
+// Lookahead update-SR of this lane's 16 values z of block blk0 + grp (clamped at 0 first).
+// fresh: (1-beta2) * g^2 in float64 from the gradients g, or with AW4_MOMENT_FRESH_PROXY
+// fp32(w2f * z) (the v-proxy's (1 - beta2) * m2, fp32(1-beta2) = w2f).  Stores the codes
+// and scale (store), and/or returns each value's sample fp32(s * level) (sampled).
+__device__ __forceinline__ BlockScales encode_block_la(const aw4_moment& M, const MomentTables& L, int64_t blk0,
+                                                       int grp, int j, bool active, const float (&z_in)[16],
+                                                       const float (&g)[16], float w2f, bool store, float* sampled,
+                                                       BlockScratch sc) {
+    float z[16];
+    float amf = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        z[i] = clamp_min_nan(z_in[i], 0.0f);
+        amf = abs_max_acc(amf, z[i]);
+    }
+    const uint32_t amax = block_max_u32(f2u(amf));
+    const float s = u2f(max(amax, 0x2B8CBCCCu));  // max(absmax, fp32(1e-12))
+    const bool wave_fast = __builtin_amdgcn_ballot_w64(!(s < 0x1p125f)) == 0;
+    const float y = div_cr(1.0f, s);
+    const bool proxy = (M.flags & AW4_MOMENT_FRESH_PROXY) != 0;
+    uint32_t rw[12];
+    wave_lds_sync();  // the stage's previous contents have been read
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        double u[4];
+        la_draws_quarter(M, blk0, grp, j, q, active, rw, u);
+        uint32_t code[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int i = 4 * q + t;
+            const float xq = __builtin_expect(wave_fast, 1) ? div_by_rcp(z[i], s, y) : z[i] / s;
+            const float x = clamp01_nan(xq);
+            const LutEntry le = L.lut[lut_bucket_unsigned(x)];
+            const bool up = x >= le.thr;
+            const int idx = (int)le.base + (up ? 1 : 0);
+            const float b = up ? le.lv_hi : le.lv_lo;   // cb[min(idx, 15)]
+            const float a = L.cb[idx > 0 ? idx - 1 : 0];
+            const double fresh = proxy ? (double)clamp_min_nan(w2f * z_in[i], 0.0f)
+                                       : M.la_fresh_weight * ((double)g[i] * (double)g[i]);
+            const bool lower = u[t] < la_prob_lo(M, z[i], a, b, s, fresh);
+            code[t] = (uint32_t)min(max(idx - (lower ? 1 : 0), 0), 15);
+            if (sampled) sampled[i] = s * (lower ? a : b);
+        }
+        if (store) sc.stage[8 * q + j] = (uint16_t)(code[0] | (code[1] << 4) | (code[2] << 8) | (code[3] << 12));
+    }
+    if (store) {
+        wave_lds_sync();
+        if (active) {
+            const u32x2 w = *(const u32x2*)(sc.stage + 4 * j);
+            const gptr<uint8_t> codes = gaddr<uint8_t>(M.codes) + blk0 * (kBlock / 2);
+            __builtin_nontemporal_store(w, (gptr<u32x2>)(codes + (uint32_t)(grp * (kBlock / 2) + 8 * j)));
+        }
+        if (active && j == 0) __builtin_nontemporal_store(s, gaddr<float>(M.scales) + blk0 + grp);
+    }
+    return BlockScales{s, s};
 }
 
 // Runtime dispatch over the rounding kind (generic kernels).

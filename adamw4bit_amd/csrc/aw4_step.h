@@ -163,7 +163,9 @@ struct TileInputs {
     float v1[kV1 ? 16 : 1], v2[kV2 ? 16 : 1];
 };
 
-__device__ __forceinline__ bool is_quantized(const aw4_moment& m) { return m.rounding != K_FP32; }
+// Whether the moment's state is codes and scales (else fp32 values: an fp32-state moment, or
+// a pending lookahead m2).
+__device__ __forceinline__ bool is_quantized(const aw4_moment& m) { return has_codes(m.rounding, m.flags); }
 
 template <int MK>
 __device__ __forceinline__ bool moment_quantized(const aw4_moment& m) {
@@ -284,10 +286,13 @@ struct M2Staged {
 // Decode, update and store one quarter (4 values) of this lane; the new moments go to m1/m2.
 // kDefer: the parameter update waits for the stored m2 (AW4_MOMENT_SAMPLED_READ); p1 receives
 // the decayed parameters and nothing is stored.
+// la_prior (pending lookahead m2): the samples of the pending state; the new m2 is then
+// fp32(beta2) * sample + fp32(1-beta2) * g * g in ATen's addcmul form
+// fma(fp32(1-beta2) * g, g, fp32(beta2) * sample) (adamw.py:576).
 template <int M1K, int M2K, int D, int DP, bool kGenericLerp, bool kDefer, class M2Sink>
 __device__ __forceinline__ void update_quarter(const aw4_tensor& T, int q, const TileInputs<M1K, M2K, D>& in,
                                                const MomentTables& L1, const MomentTables& L2, const TileLane& tl,
-                                               float (&m1)[16], M2Sink& m2, float* p1) {
+                                               float (&m1)[16], M2Sink& m2, float* p1, const float* la_prior) {
     using In = TileInputs<M1K, M2K, D>;
     constexpr int DC = D == D_ANY ? D_F32 : D;  // generic loads are already fp32 words
     float g[4], p[4], a[4], b[4];
@@ -319,6 +324,8 @@ __device__ __forceinline__ void update_quarter(const aw4_tensor& T, int q, const
         } else {
             moments_update<false, false>(T, g[t], a[t], b[t]);
         }
+        if (la_prior)
+            b[t] = __builtin_fmaf((float)T.m2.la_fresh_weight * g[t], g[t], la_prior[4 * q + t] * (float)T.m2.la_beta2);
         if constexpr (kDefer) p1[4 * q + t] = round_to_storage<DP>(p[t] * T.decay);
         else p[t] = param_update<DP>(T, p[t], a[t], b[t]);
         m1[4 * q + t] = a[t];
@@ -341,13 +348,15 @@ __device__ __forceinline__ void update_quarter(const aw4_tensor& T, int q, const
 template <int M1K, int M2K, int D, int DP, bool kDefer, class M2Sink>
 __device__ __forceinline__ void update_tile(const aw4_tensor& T, const TileInputs<M1K, M2K, D>& in,
                                             const MomentTables& L1, const MomentTables& L2, const TileLane& tl,
-                                            float (&m1)[16], M2Sink& m2, float* p1) {
+                                            float (&m1)[16], M2Sink& m2, float* p1, const float* la_prior) {
     if (__builtin_expect((T.flags & (AW4_TENSOR_LERP1_LARGE | AW4_TENSOR_LERP2_LARGE)) == 0, 1)) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) update_quarter<M1K, M2K, D, DP, false, kDefer>(T, q, in, L1, L2, tl, m1, m2, p1);
+        for (int q = 0; q < 4; ++q)
+            update_quarter<M1K, M2K, D, DP, false, kDefer>(T, q, in, L1, L2, tl, m1, m2, p1, la_prior);
     } else {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) update_quarter<M1K, M2K, D, DP, true, kDefer>(T, q, in, L1, L2, tl, m1, m2, p1);
+        for (int q = 0; q < 4; ++q)
+            update_quarter<M1K, M2K, D, DP, true, kDefer>(T, q, in, L1, L2, tl, m1, m2, p1, la_prior);
     }
 }
 
@@ -356,13 +365,28 @@ template <int M1K, int M2K, int D, bool kDefer = false, class M2Sink>
 __device__ __forceinline__ void update_tile_any(const aw4_tensor& T, const TileLane& tl,
                                                 const TileInputs<M1K, M2K, D>& in, const MomentTables& L1,
                                                 const MomentTables& L2, float (&m1)[16], M2Sink& m2,
-                                                float* p1 = nullptr) {
+                                                float* p1 = nullptr, const float* la_prior = nullptr) {
     if constexpr (D == D_ANY) {
-        if (T.param_dtype == D_F32) update_tile<M1K, M2K, D, D_F32, kDefer>(T, in, L1, L2, tl, m1, m2, p1);
-        else if (T.param_dtype == D_BF16) update_tile<M1K, M2K, D, D_BF16, kDefer>(T, in, L1, L2, tl, m1, m2, p1);
-        else update_tile<M1K, M2K, D, D_F16, kDefer>(T, in, L1, L2, tl, m1, m2, p1);
+        if (T.param_dtype == D_F32) update_tile<M1K, M2K, D, D_F32, kDefer>(T, in, L1, L2, tl, m1, m2, p1, la_prior);
+        else if (T.param_dtype == D_BF16)
+            update_tile<M1K, M2K, D, D_BF16, kDefer>(T, in, L1, L2, tl, m1, m2, p1, la_prior);
+        else update_tile<M1K, M2K, D, D_F16, kDefer>(T, in, L1, L2, tl, m1, m2, p1, la_prior);
     } else {
-        update_tile<M1K, M2K, D, D, kDefer>(T, in, L1, L2, tl, m1, m2, p1);
+        update_tile<M1K, M2K, D, D, kDefer>(T, in, L1, L2, tl, m1, m2, p1, la_prior);
+    }
+}
+
+// The gradients of this lane's 16 values as fp32.
+template <int M1K, int M2K, int D>
+__device__ __forceinline__ void tile_grads(const TileInputs<M1K, M2K, D>& in, float (&g)[16]) {
+    using In = TileInputs<M1K, M2K, D>;
+    constexpr int DC = D == D_ANY ? D_F32 : D;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        float v[4];
+        words_to_f32<DC>(&in.g[In::kW * q], v);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) g[4 * q + t] = v[t];
     }
 }
 
@@ -481,8 +505,12 @@ __device__ void step_tile_values(const aw4_tensor& T, int64_t e_tile, int lane) 
 // one counter covers both, in issue order).
 // ---------------------------------------------------------------------------
 
+// Tiles of tensors without block structure: both moments fp32 state, or numel not a
+// multiple of 128.  (Written through has_codes: the equivalent comparisons with K_FP32
+// lead hipcc to copy the prefetched tile registers instead of coalescing them, 40 more
+// VGPRs in the specialised kernels; the resource test pins the counts.)
 __device__ __forceinline__ bool values_only(const aw4_tensor& T) {
-    return (!is_quantized(T.m1) && !is_quantized(T.m2)) || (T.numel & (kBlock - 1)) != 0;
+    return (!has_codes(T.m1.rounding, 0) && !has_codes(T.m2.rounding, 0)) || (T.numel & (kBlock - 1)) != 0;
 }
 
 // Tile order: grid order (wave w takes tiles w, w + W, ...) or consecutive tiles per wave
@@ -497,9 +525,10 @@ constexpr bool prefetch_next_tile(int m1k, int m2k, int d) {
 constexpr bool tile_order_grid(int m1k, int m2k, int d) {
     return prefetch_next_tile(m1k, m2k, d) && kind_of(m2k) != K_USR;
 }
-// The generic kernel instance for tensors whose m2 is read back after its encode
-// (AW4_MOMENT_SAMPLED_READ in the m2 spec's flags).
-constexpr bool sampled_read_kernel(int m2k) { return (flags_of(m2k) & AW4_MOMENT_SAMPLED_READ) != 0; }
+// The generic kernel instance for the reference step's research m2 variants (marked by
+// AW4_MOMENT_SAMPLED_READ in the m2 spec's flags): m2 read back after its encode
+// (AW4_MOMENT_SAMPLED_READ) and lookahead update-SR (AW4_ROUND_LOOKAHEAD_SR).
+constexpr bool research_kernel(int m2k) { return (flags_of(m2k) & AW4_MOMENT_SAMPLED_READ) != 0; }
 // Update-SR kernels stage the new second moments in LDS (M2Staged) so that the prefetched
 // inputs fit in the registers of four waves per SIMD.
 constexpr bool stage_m2(int m1k, int m2k, int d) { return prefetch_next_tile(m1k, m2k, d) && kind_of(m2k) == K_USR; }
@@ -571,17 +600,42 @@ __device__ __forceinline__ void run_tiles(const StepHeader* hdr, const LdsT& lds
                 }
             };
             float m1[16];
-            if constexpr (sampled_read_kernel(M2K)) {
-                // every block tile of this kernel reads its m2 back (the host groups them)
-                float m2v[16], p1[16];
+            if constexpr (research_kernel(M2K)) {
+                // every block tile of this kernel has a research m2 (the host groups them)
+                float m2v[16];
                 M2Regs m2{m2v};
-                update_tile_any<M1K, M2K, D, true>(T, tl, in, L1, L2, m1, m2, p1);
-                finish_moment<M1K, false>(T.m1, L1, tl, RegValues{m1}, ws);
-                prefetch();
-                const BlockScales bs = finish_moment<M2K, true>(T.m2, L2, tl, m2.values(), ws);
-                if (T.param_dtype == D_F32) sampled_read_update<D_F32>(T, tl, L2, ws.block(tl.grp), bs, m1, p1);
-                else if (T.param_dtype == D_BF16) sampled_read_update<D_BF16>(T, tl, L2, ws.block(tl.grp), bs, m1, p1);
-                else sampled_read_update<D_F16>(T, tl, L2, ws.block(tl.grp), bs, m1, p1);
+                if (T.m2.flags & AW4_MOMENT_SAMPLED_READ) {
+                    float p1[16];
+                    update_tile_any<M1K, M2K, D, true>(T, tl, in, L1, L2, m1, m2, p1);
+                    finish_moment<M1K, false>(T.m1, L1, tl, RegValues{m1}, ws);
+                    prefetch();
+                    const BlockScales bs = finish_moment<M2K, true>(T.m2, L2, tl, m2.values(), ws);
+                    if (T.param_dtype == D_F32) sampled_read_update<D_F32>(T, tl, L2, ws.block(tl.grp), bs, m1, p1);
+                    else if (T.param_dtype == D_BF16)
+                        sampled_read_update<D_BF16>(T, tl, L2, ws.block(tl.grp), bs, m1, p1);
+                    else sampled_read_update<D_F16>(T, tl, L2, ws.block(tl.grp), bs, m1, p1);
+                } else {
+                    // lookahead update-SR: sample the pending state before the update, or encode
+                    // the new m2 after it
+                    float g[16];
+                    tile_grads(in, g);
+                    const bool pending = (T.m2.flags & AW4_MOMENT_PENDING) != 0;
+                    const float w2f = (float)T.m2.la_fresh_weight;
+                    float prior[16];
+                    if (pending) {
+                        float z[16];
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) z[i] = in.v2[i];
+                        encode_block_la(T.m2, L2, tl.blk0, tl.grp, tl.j, tl.active, z, g, w2f, false, prior,
+                                        ws.block(tl.grp));
+                    }
+                    update_tile_any<M1K, M2K, D, false>(T, tl, in, L1, L2, m1, m2, nullptr, pending ? prior : nullptr);
+                    finish_moment<M1K, false>(T.m1, L1, tl, RegValues{m1}, ws);
+                    prefetch();
+                    if (pending) finish_moment<M2K, true>(T.m2, L2, tl, m2.values(), ws);
+                    else encode_block_la(T.m2, L2, tl.blk0, tl.grp, tl.j, tl.active, m2v, g, w2f, true, nullptr,
+                                         ws.block(tl.grp));
+                }
             } else if constexpr (stage_m2(M1K, M2K, D)) {
                 M2Staged m2{m2_stage + lane, 0.0f};
                 update_tile_any(T, tl, in, L1, L2, m1, m2);

@@ -48,8 +48,8 @@ namespace {
 
 using namespace aw4;
 
-static_assert(sizeof(aw4_moment) == 72, "aw4_moment layout");
-static_assert(sizeof(aw4_tensor) == 208, "aw4_tensor layout");
+static_assert(sizeof(aw4_moment) == 104, "aw4_moment layout");
+static_assert(sizeof(aw4_tensor) == 272, "aw4_tensor layout");
 
 // Codebooks as fp32 bit patterns (ascending; code = index).  Values of the reference's
 // closed forms: NF4 table (quantization.py:401-422), signed and unsigned dynamic maps
@@ -151,7 +151,7 @@ constexpr int kSsrGuarded = mspec(K_SSR, AW4_MOMENT_GUARDS);
 constexpr int kUsrGuarded = mspec(K_USR, AW4_MOMENT_GUARDS);
 constexpr int kUsrGuardedEden = mspec(K_USR, AW4_MOMENT_GUARDS | AW4_MOMENT_EDEN);
 // Any m2 kind, read back after its encode (dyn4_upd_sr / lin4_upd_sr / *_upd_sr_store_eden).
-constexpr int kAnySampledRead = mspec(K_ANY, AW4_MOMENT_SAMPLED_READ);
+constexpr int kAnyResearch = mspec(K_ANY, AW4_MOMENT_SAMPLED_READ);  // read-back and lookahead m2
 struct KernelVariant {
     int m1, m2, dtype;
     const void* fn;
@@ -163,14 +163,14 @@ const KernelVariant kVariants[] = {
     AW4_VARIANT(kSsrGuarded, kUsrGuarded, D_F32), AW4_VARIANT(kSsrGuarded, kUsrGuarded, D_BF16),
     AW4_VARIANT(kRtn, kFp32, D_F32),              AW4_VARIANT(kRtn, kFp32, D_BF16),
     AW4_VARIANT(kRtn, kUsrGuardedEden, D_F32),    AW4_VARIANT(kRtn, kUsrGuardedEden, D_BF16),
-    AW4_VARIANT(K_ANY, kAnySampledRead, D_ANY),
+    AW4_VARIANT(K_ANY, kAnyResearch, D_ANY),
     AW4_VARIANT(K_ANY, K_ANY, D_ANY),
 };
 #undef AW4_VARIANT
 constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 constexpr int kGenericVariant = kNumVariants - 1;
-constexpr int kSampledReadVariant = kNumVariants - 2;  // generic, for m2 read back after its encode
-constexpr int kNumSpecialised = kSampledReadVariant;
+constexpr int kResearchVariant = kNumVariants - 2;  // generic, for read-back and lookahead m2
+constexpr int kNumSpecialised = kResearchVariant;
 
 // Stand-alone codec kernels (one wave tile per wave, grid-stride).
 __global__ void __launch_bounds__(kThreads) quantize_kernel(const float* __restrict__ values, int64_t numel,
@@ -429,21 +429,41 @@ int device_state(DeviceState** out) {
 bool aligned(uint64_t addr, uint64_t a) { return (addr % a) == 0; }
 
 int check_moment(const aw4_moment& m, int64_t numel, int index, const char* name) {
+    const bool la = m.rounding == AW4_ROUND_LOOKAHEAD_SR;
+    if ((m.flags & (AW4_MOMENT_FRESH_PROXY | AW4_MOMENT_PENDING)) && !la)
+        return set_error(AW4_EINVAL, "tensor %d: %s lookahead flags without lookahead rounding", index, name);
     if (m.rounding == AW4_ROUND_FP32) {
         if (!m.values) return set_error(AW4_EINVAL, "tensor %d: %s fp32 state without values", index, name);
         if (!aligned(m.values, 16)) return set_error(AW4_EALIGN, "tensor %d: %s values not 16-byte aligned", index, name);
         return AW4_OK;
     }
-    if (m.rounding < AW4_ROUND_RTN || m.rounding > AW4_ROUND_UPDATE_SR)
+    if (m.rounding < AW4_ROUND_RTN || m.rounding > AW4_ROUND_LOOKAHEAD_SR)
         return set_error(AW4_EINVAL, "tensor %d: %s has rounding %d", index, name, m.rounding);
     if (m.codebook < 0 || m.codebook >= AW4_NUM_CODEBOOKS)
         return set_error(AW4_EINVAL, "tensor %d: %s has codebook %d", index, name, m.codebook);
     if (numel % kBlock != 0)
         return set_error(AW4_EINVAL, "tensor %d: %s quantized but numel %lld is not a multiple of %d", index, name,
                          (long long)numel, kBlock);
-    if (!m.codes || !m.scales) return set_error(AW4_EINVAL, "tensor %d: %s quantized without codes/scales", index, name);
-    if (!aligned(m.codes, 2) || !aligned(m.scales, 4))
-        return set_error(AW4_EALIGN, "tensor %d: %s codes/scales misaligned", index, name);
+    if (la) {
+        // lookahead update-SR (quantize_dyn4_la_upd_sr): m2 on the dyn4 codebook only
+        if (strcmp(name, "m2") != 0 || m.codebook != AW4_CB_DYN4)
+            return set_error(AW4_EINVAL, "tensor %d: lookahead update-SR is for a dyn4 m2 only", index);
+        if ((m.flags & AW4_MOMENT_FRESH_PROXY) && (m.flags & AW4_MOMENT_PENDING))
+            return set_error(AW4_EINVAL, "tensor %d: m2 FRESH_PROXY and PENDING together", index);
+        if (m.flags & (AW4_MOMENT_SAMPLED_READ | AW4_MOMENT_READ_RAW_SCALE | AW4_MOMENT_EDEN))
+            return set_error(AW4_EINVAL, "tensor %d: lookahead m2 with read-back or EDEN flags", index);
+        if (!(m.la_bias > 0.0) || !(m.la_beta2 >= 0.0 && m.la_beta2 < 1.0) || !(m.la_eps >= 0.0))
+            return set_error(AW4_EINVAL, "tensor %d: lookahead m2 needs bias > 0, beta2 in [0, 1), eps >= 0", index);
+    }
+    if (la && (m.flags & AW4_MOMENT_PENDING)) {
+        if (!m.values || !aligned(m.values, 16))
+            return set_error(AW4_EINVAL, "tensor %d: pending lookahead m2 without 16-byte aligned values", index);
+    } else {
+        if (!m.codes || !m.scales)
+            return set_error(AW4_EINVAL, "tensor %d: %s quantized without codes/scales", index, name);
+        if (!aligned(m.codes, 2) || !aligned(m.scales, 4))
+            return set_error(AW4_EALIGN, "tensor %d: %s codes/scales misaligned", index, name);
+    }
     if (m.rounding != AW4_ROUND_RTN) {
         if (m.flags & AW4_MOMENT_EXT_DRAWS) {
             if (!m.draws || !aligned(m.draws, 16))
@@ -485,6 +505,11 @@ bool host_values_only(const aw4_tensor& t) {
     return (t.m1.rounding == AW4_ROUND_FP32 && t.m2.rounding == AW4_ROUND_FP32) || t.numel % kBlock != 0;
 }
 
+// m2 of the reference step's research variants, stepped by the research kernel instance.
+bool research_m2(const aw4_moment& m) {
+    return (m.flags & AW4_MOMENT_SAMPLED_READ) || m.rounding == AW4_ROUND_LOOKAHEAD_SR;
+}
+
 // One launch of a step: a kernel variant, the tables its LDS slots load, and its tensors.
 struct LaunchGroup {
     int variant = kGenericVariant;
@@ -498,9 +523,9 @@ struct LaunchGroup {
 // the generic kernel.  A recipe's table is one launch.
 std::vector<LaunchGroup> plan_launches(const aw4_tensor* ts, int32_t count) {
     std::vector<LaunchGroup> groups;
-    LaunchGroup generic, sampled;
+    LaunchGroup generic, research;
     generic.variant = kGenericVariant;
-    sampled.variant = kSampledReadVariant;
+    research.variant = kResearchVariant;
     std::vector<int> values;
     for (int i = 0; i < count; ++i) {
         const aw4_tensor& t = ts[i];
@@ -508,7 +533,7 @@ std::vector<LaunchGroup> plan_launches(const aw4_tensor* ts, int32_t count) {
             if (t.param_dtype != t.grad_dtype) generic.members.push_back(i); else values.push_back(i);
             continue;
         }
-        if (t.m2.flags & AW4_MOMENT_SAMPLED_READ) { sampled.members.push_back(i); continue; }
+        if (research_m2(t.m2)) { research.members.push_back(i); continue; }
         if (t.param_dtype != t.grad_dtype) { generic.members.push_back(i); continue; }
         const int s1 = mspec(t.m1.rounding, t.m1.flags & spec_flags_mask(t.m1.rounding));
         const int s2 = mspec(t.m2.rounding, t.m2.flags & spec_flags_mask(t.m2.rounding));
@@ -545,7 +570,7 @@ std::vector<LaunchGroup> plan_launches(const aw4_tensor* ts, int32_t count) {
         }
         (g ? g : &generic)->members.push_back(i);
     }
-    if (!sampled.members.empty()) groups.push_back(std::move(sampled));
+    if (!research.members.empty()) groups.push_back(std::move(research));
     if (!generic.members.empty()) groups.push_back(std::move(generic));
     for (LaunchGroup& g : groups) std::sort(g.members.begin(), g.members.end());
     return groups;
@@ -662,6 +687,8 @@ int aw4_quantize(const float* values, int64_t numel, const aw4_moment* m, void* 
         return set_error(AW4_EINVAL, "aw4_quantize: bad arguments (numel %lld)", (long long)numel);
     if (((uint64_t)values) % 16 != 0) return set_error(AW4_EALIGN, "aw4_quantize: values not 16-byte aligned");
     if (m->rounding == AW4_ROUND_FP32) return set_error(AW4_EINVAL, "aw4_quantize: fp32 moment");
+    if (m->rounding == AW4_ROUND_LOOKAHEAD_SR)
+        return set_error(AW4_EINVAL, "aw4_quantize: lookahead update-SR reads gradients (fused step only)");
     int rc = check_moment(*m, numel, 0, "moment");
     if (rc) return rc;
     std::lock_guard<std::mutex> lock(g_mutex);

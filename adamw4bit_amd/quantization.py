@@ -95,6 +95,7 @@ ROUND_NONE = 0      # fp32 state, no codec
 ROUND_RTN = 1       # nearest level, ties to the upper level (_compiled_quantization.py:41-45)
 ROUND_STATE_SR = 2  # value-unbiased stochastic rounding (_compiled_quantization.py:60-71)
 ROUND_UPDATE_SR = 3  # preconditioner-space stochastic rounding (_compiled_quantization.py:74-109)
+ROUND_LOOKAHEAD_SR = 4  # next-step preconditioner stochastic rounding (quantization.py:779-895)
 
 # scheme -> (codebook id, rounding rule, floor code 0 to code 1)
 # Covers every scheme the reference's optimized path accepts (_optimized.py:36-41)
@@ -120,6 +121,9 @@ SCHEMES: Dict[str, Tuple[int, int, bool]] = {
     "dyn4_upd_sr": (CB_DYN4, ROUND_UPDATE_SR, False),
     "lin4_upd_sr_store_eden": (CB_LIN4, ROUND_UPDATE_SR, False),
     "dyn4_upd_sr_store_eden": (CB_DYN4, ROUND_UPDATE_SR, False),
+    "dyn4_la_upd_sr": (CB_DYN4, ROUND_LOOKAHEAD_SR, False),
+    "dyn4_proxy_la_upd_sr": (CB_DYN4, ROUND_LOOKAHEAD_SR, False),
+    "dyn4_vproxy_la_upd_sr": (CB_DYN4, ROUND_LOOKAHEAD_SR, False),
 }
 
 # m2 schemes whose update reads back the sampled value (adamw.py:636-656) and those that
@@ -127,6 +131,16 @@ SCHEMES: Dict[str, Tuple[int, int, bool]] = {
 # scale only (adamw.py:615-635).
 SAMPLED_READ_SCHEMES = frozenset({"lin4_upd_sr", "dyn4_upd_sr"})
 STORE_EDEN_SCHEMES = frozenset({"lin4_upd_sr_store_eden", "dyn4_upd_sr_store_eden"})
+
+# Lookahead update-SR m2 schemes (adamw.py:118-120, 566-614): the pending form keeps the new
+# m2 in fp32 as state "lookahead_pending_exp_avg_sq" and updates from a lookahead sample of
+# it; the proxy forms store codes sampled for the next step's update, with the fresh term
+# (1 - beta2) g^2 of the current gradient (proxy) or (1 - beta2) m2 (v-proxy).
+PENDING_LOOKAHEAD_SCHEMES = frozenset({"dyn4_la_upd_sr"})
+PROXY_LOOKAHEAD_SCHEMES = frozenset({"dyn4_proxy_la_upd_sr"})
+VPROXY_LOOKAHEAD_SCHEMES = frozenset({"dyn4_vproxy_la_upd_sr"})
+LOOKAHEAD_SCHEMES = PENDING_LOOKAHEAD_SCHEMES | PROXY_LOOKAHEAD_SCHEMES | VPROXY_LOOKAHEAD_SCHEMES
+PENDING_KEY = "lookahead_pending_exp_avg_sq"
 
 STOCHASTIC_ROUNDING = (ROUND_STATE_SR, ROUND_UPDATE_SR)
 
@@ -213,7 +227,8 @@ def initial_code_and_scale(mode: str, eden: bool) -> Tuple[int, float]:
     count = sum(1 for v in levels if v < x)          # searchsorted, side="left"
     lower, upper = max(count - 1, 0), min(count, 15)
     a, b = levels[lower], levels[upper]
-    if rounding == ROUND_RTN:
+    if rounding in (ROUND_RTN, ROUND_LOOKAHEAD_SR):
+        # the proxy lookahead schemes store their zero state with plain dyn4 (quantization.py:583-584)
         code = lower if abs(x - a) < abs(b - x) else upper
     elif rounding == ROUND_STATE_SR:
         # P(upper) is 1 at x >= b and 0 at x <= a; otherwise x is strictly inside.

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define AW4_ABI_VERSION 2
+#define AW4_ABI_VERSION 3
 #define AW4_BLOCK 128 /* values per block scale (quantization.py:694-703, 4-bit default) */
 
 /* Error codes. */
@@ -54,6 +54,14 @@ extern "C" {
 #define AW4_ROUND_RTN 1       /* nearest level, ties up (_compiled_quantization.py:41-45) */
 #define AW4_ROUND_STATE_SR 2  /* value-unbiased SR (_compiled_quantization.py:60-71) */
 #define AW4_ROUND_UPDATE_SR 3 /* preconditioner-space SR (_compiled_quantization.py:74-109) */
+/* m2 only, dyn4 codebook: lookahead update-SR (quantize_dyn4_la_upd_sr,
+ * quantization.py:779-895).  The probability is computed in float64 on the next
+ * step's preconditioner beta2 * q + fresh, fresh = (1-beta2) * g^2, from the
+ * aw4_moment la_* constants; the uniforms are float64.  Stores codes and scales
+ * (dyn4_proxy_la_upd_sr, dyn4_vproxy_la_upd_sr, adamw.py:579-614), or, with
+ * AW4_MOMENT_PENDING, samples the fp32 pending state before the update instead
+ * (dyn4_la_upd_sr, adamw.py:566-578). */
+#define AW4_ROUND_LOOKAHEAD_SR 4
 
 /* aw4_moment.flags */
 #define AW4_MOMENT_ZERO_FLOOR 0x1 /* code 0 -> code 1 after rounding (dyn4_nz, quantization.py:529-552) */
@@ -70,6 +78,13 @@ extern "C" {
  * that AW4_MOMENT_EDEN applies to the stored scale (*_upd_sr_store_eden,
  * adamw.py:615-635, quantization.py:1007-1037) */
 #define AW4_MOMENT_READ_RAW_SCALE 0x20
+/* AW4_ROUND_LOOKAHEAD_SR: fresh = fp32(fp32(1-beta2) * m2) instead of (1-beta2) * g^2
+ * (the v-proxy, dyn4_vproxy_la_upd_sr, adamw.py:597-614) */
+#define AW4_MOMENT_FRESH_PROXY 0x40
+/* AW4_ROUND_LOOKAHEAD_SR: `values` is the fp32 pending second moment z.  The step
+ * samples z (codes are not kept) and sets m2 = fp32(beta2) * sample + (1-beta2) * g * g
+ * (addcmul), then stores m2 back to `values` (dyn4_la_upd_sr, adamw.py:566-578, 771-776). */
+#define AW4_MOMENT_PENDING 0x80
 
 /* aw4_tensor.param_dtype / grad_dtype */
 #define AW4_F32 0
@@ -93,7 +108,8 @@ typedef struct aw4_moment {
     uint64_t codes;      /* device address, uint8[ceil(numel/2)] or 0 */
     uint64_t scales;     /* device address, float[numel/128] or 0 */
     uint64_t values;     /* device address, float[numel] (fp32 state, or SAMPLED_READ output) or 0 */
-    uint64_t draws;      /* device address, float[numel] uniforms (AW4_MOMENT_EXT_DRAWS) or 0 */
+    uint64_t draws;      /* device address of numel uniforms (AW4_MOMENT_EXT_DRAWS): float, double for
+                            AW4_ROUND_LOOKAHEAD_SR; or 0 */
     uint64_t rng_seed;   /* Philox4x32-10 key: generator seed of this moment's stream */
     uint64_t rng_offset; /* stream position of this write's first draw; multiple of 128 */
     int32_t codebook;    /* AW4_CB_* (ignored for AW4_ROUND_FP32) */
@@ -102,7 +118,13 @@ typedef struct aw4_moment {
     float sr_bias;       /* update-SR storage bias correction, fp32(max(c,1e-12)) (_optimized_quantization.py:66-67) */
     float sr_bias_rcp;   /* correctly rounded 1/sr_bias */
     float sr_eps;        /* update-SR epsilon, fp32(eps) */
-} aw4_moment; /* 72 bytes */
+    /* AW4_ROUND_LOOKAHEAD_SR, as the float64 values the reference computes with:
+     * beta2, 1.0 - beta2, max(bias_correction, 1e-12), eps */
+    double la_beta2;
+    double la_fresh_weight;
+    double la_bias;
+    double la_eps;
+} aw4_moment; /* 104 bytes */
 
 /*
  * One parameter of a step.  All scalars are the fp32 values the reference's
@@ -121,7 +143,7 @@ typedef struct aw4_tensor {
     float w1, w2, decay, step_coef, bc2_sqrt, bc2_sqrt_rcp, eps;
     aw4_moment m1;
     aw4_moment m2;
-} aw4_tensor; /* 208 bytes */
+} aw4_tensor; /* 272 bytes */
 
 /* Library ABI version (AW4_ABI_VERSION of the build). */
 int aw4_abi_version(void);

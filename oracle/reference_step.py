@@ -21,7 +21,10 @@ order, the parts of ``adamw4bit`` that the fused HIP step replaces:
   stochastic moment is initialized (``adamw.py:524-545``);
 * the reference step's read-back m2 schemes (``dyn4_upd_sr``, ``lin4_upd_sr``,
   ``*_upd_sr_store_eden``, ``adamw.py:615-656``), whose update uses the m2 just
-  encoded (``_update_sampled_read``).  A parameter whose schemes the optimized
+  encoded (``_update_sampled_read``), and its lookahead update-SR schemes
+  (``dyn4_la_upd_sr``, ``dyn4_proxy_la_upd_sr``, ``dyn4_vproxy_la_upd_sr``,
+  ``adamw.py:566-614``) with their float64 quantizer (``encode_lookahead``,
+  ``quantization.py:779-895``).  A parameter whose schemes the optimized
   backend does not accept takes the reference step, as the backend's preflight
   sends it there (``_optimized.py:94-126``).
 
@@ -96,13 +99,18 @@ FP32_READ_SCHEMES = {"lin4_upd_sr_fp32read", "dyn4_upd_sr_fp32read", "dyn4_looka
 SAMPLED_READ_SCHEMES = {"lin4_upd_sr", "dyn4_upd_sr"}
 STORE_EDEN_SCHEMES = {"lin4_upd_sr_store_eden", "dyn4_upd_sr_store_eden"}
 UPDATE_SR_SCHEMES = FP32_READ_SCHEMES | SAMPLED_READ_SCHEMES | STORE_EDEN_SCHEMES
+# Lookahead update-SR (adamw.py:118-120): the pending form keeps m2 in fp32 and samples it
+# before each update; the proxies store m2 sampled for the next step's update.
+PENDING_LOOKAHEAD_SCHEMES = {"dyn4_la_upd_sr"}
+VPROXY_LOOKAHEAD_SCHEMES = {"dyn4_vproxy_la_upd_sr"}
+LOOKAHEAD_SCHEMES = PENDING_LOOKAHEAD_SCHEMES | VPROXY_LOOKAHEAD_SCHEMES | {"dyn4_proxy_la_upd_sr"}
 NEXT_BIAS_SCHEMES = {"dyn4_lookahead_sr", "dyn4_upd_sr_fp32read_nextbc"}
 M1_SCHEMES = {"fp32", "nf4", "nf4_sr", "sdyn4", "sdyn4_sr"}            # _optimized.py:36
 M2_SCHEMES = {"fp32", "lin4", "lin4_sr", "lin4_nz", "dyn4", "dyn4_sr", "dyn4_nz"} | FP32_READ_SCHEMES
 
 
 def is_stochastic(mode: str) -> bool:
-    return mode in STATE_SR_SCHEMES or mode in UPDATE_SR_SCHEMES
+    return mode in STATE_SR_SCHEMES or mode in UPDATE_SR_SCHEMES or mode in LOOKAHEAD_SCHEMES
 
 
 # ---------------------------------------------------------------------------
@@ -180,6 +188,50 @@ def encode(values: torch.Tensor, mode: str, *, eden: bool = False,
         den = (x * levels).sum(dim=1)
         scales = scales * (num / den.clamp_min(1e-12))
     return codes.reshape(-1), scales
+
+
+def encode_lookahead(z_prev: torch.Tensor, grad: torch.Tensor, *, beta2: float, bias: float, eps: float,
+                     draws: torch.Tensor, fresh_proxy: Optional[torch.Tensor] = None):
+    """Lookahead update-SR of a second moment (``quantize_dyn4_la_upd_sr``, quantization.py:779-895).
+
+    The dyn4 neighbours lo <= x <= hi of x = clamp(z / s, 0, 1) (s the block absmax floored at
+    1e-12, in fp32) are chosen so that the NEXT step's preconditioner is unbiased: with
+    q = s * level and n(q) = max(beta2 q + fresh, 0) in float64,
+        P(lo) = (f(n(z)) - f(n(q_hi))) / max(f(n(q_lo)) - f(n(q_hi)), 1e-300),
+        f(n) = 1 / (sqrt(n / bias) + eps),
+    or 1 - clamp((z - q_lo) / (q_hi - q_lo), 0, 1) where f is flat over the interval and 1 where
+    the interval is empty; fresh is (1 - beta2) g^2 in float64 or a caller's proxy.  Returns
+    (unpacked codes, fp32 scales, fp32 samples s * level).  ``draws``: float64 uniforms.
+    """
+    z = z_prev.reshape(-1, BLOCK).clamp_min(0)
+    s = z.abs().max(dim=1).values.clamp_min(1e-12)
+    x = (z / s.unsqueeze(1)).clamp(0.0, 1.0)
+    cb = codebook("dyn4")
+    lower, upper, _, _ = _endpoints(x, cb)
+    cb64 = cb.to(torch.float64)
+    s64 = s.to(torch.float64).unsqueeze(1)
+    if fresh_proxy is None:
+        fresh = (1.0 - float(beta2)) * grad.reshape(-1, BLOCK).to(torch.float64).square()
+    else:
+        fresh = fresh_proxy.reshape(-1, BLOCK).clamp_min(0).to(torch.float64)
+    bias = max(float(bias), 1e-12)
+
+    def f(q: torch.Tensor) -> torch.Tensor:
+        n = (float(beta2) * q + fresh).clamp_min(0.0)
+        return 1.0 / (n.div(bias).sqrt() + float(eps))
+
+    q_lo, q_hi = s64 * cb64[lower.long()], s64 * cb64[upper.long()]
+    f_lo, f_z, f_hi = f(q_lo), f(z.to(torch.float64)), f(q_hi)
+    den, width = f_lo - f_hi, q_hi - q_lo
+    raw = (f_z - f_hi) / den.clamp_min(1e-300)
+    fallback = 1.0 - ((z.to(torch.float64) - q_lo) / width.clamp_min(1e-300)).clamp(0.0, 1.0)
+    empty = width <= 0.0
+    flat = ~empty & (den.abs() <= 1e-12 * torch.maximum(f_lo.abs(), f_hi.abs()).clamp_min(1.0))
+    p_lo = torch.where(empty, 1.0, torch.where(flat, fallback, raw)).clamp(0.0, 1.0)
+    take_lo = draws.reshape(p_lo.shape) < p_lo
+    codes = torch.where(take_lo, lower, upper).to(torch.uint8)
+    samples = torch.where(take_lo, q_lo, q_hi).to(torch.float32)
+    return codes.reshape(-1), s, samples.reshape(-1)
 
 
 def pack(codes: torch.Tensor) -> torch.Tensor:
@@ -270,11 +322,12 @@ class Oracle:
         self._param_optimized = True  # the optimized backend accepts the parameter's schemes
 
     # -- random draws -------------------------------------------------------
-    def _draw(self, moment: str, n: int, param: int, step: int, log: bool) -> torch.Tensor:
+    def _draw(self, moment: str, n: int, param: int, step: int, log: bool,
+              dtype: torch.dtype = torch.float32) -> torch.Tensor:
         if self.draw_fn is not None:
-            u = self.draw_fn(moment, n).reshape(n // BLOCK, BLOCK).to(torch.float32)
+            u = self.draw_fn(moment, n).reshape(n // BLOCK, BLOCK).to(dtype)
         else:
-            u = torch.rand((n // BLOCK, BLOCK), dtype=torch.float32, generator=self.generators[moment])
+            u = torch.rand((n // BLOCK, BLOCK), dtype=dtype, generator=self.generators[moment])
         self.draw_counts[moment] += n
         if self.record_draws and log:
             self.draw_log.append(DrawLog(param, moment, step, u.reshape(-1).clone()))
@@ -286,6 +339,11 @@ class Oracle:
         n = p.numel()
         if scheme == "fp32":
             return MomentState("fp32", values=torch.zeros(n, dtype=torch.float32))
+        if scheme in PENDING_LOOKAHEAD_SCHEMES:  # adamw.py:534-535
+            return MomentState(scheme, values=torch.zeros(n, dtype=torch.float32))
+        if scheme in LOOKAHEAD_SCHEMES:  # the proxies store zeros with plain dyn4 (quantization.py:583-584)
+            codes, scales = encode(torch.zeros(n, dtype=torch.float32), "dyn4")
+            return MomentState(scheme, codes=pack(codes), scales=scales)
         optimized = self.optimized and self._param_optimized
         if optimized:
             # _moment_buffer.py:106-126: encode one zero tile, broadcast its first byte/scale.
@@ -328,6 +386,9 @@ class Oracle:
         flat_g = grad.reshape(-1)
         if s2 in SAMPLED_READ_SCHEMES or s2 in STORE_EDEN_SCHEMES:
             self._update_sampled_read(index, st, flat_p, flat_g, s2, eden, bc1, bc2)
+            return
+        if s2 in LOOKAHEAD_SCHEMES:
+            self._update_lookahead(index, st, flat_p, flat_g, s2, bc1, bc2)
             return
         chunk = self._chunk_size(s1, s2) if optimized else n
         for start in range(0, n, chunk):
@@ -390,6 +451,42 @@ class Oracle:
         self._write(st.m1, m1, 0, n, eden=False, draws=draws, bias=1.0, eps=1e-8)
         st.m2.codes[:] = packed
         st.m2.scales[:] = stored_scales
+
+    def _update_lookahead(self, index, st, p, grad, s2, bc1, bc2):
+        """The reference step for lookahead update-SR m2 (adamw.py:566-614, 771-790).
+
+        Pending form: a lookahead sample A of the pending fp32 state (bias_c2), then
+        m2 = A * beta2 + (1 - beta2) g^2 (``mul`` then ``addcmul``), kept in fp32 as the next
+        pending state.  Proxies: m2 = lerp(decoded m2, g^2, 1 - beta2) for the update, stored
+        as codes sampled for the next step's bias correction with fresh term (1 - beta2) g^2
+        (proxy) or (1 - beta2) m2 (v-proxy).  Every write draws numel float64 uniforms."""
+        hp = self.hyper
+        b1, b2 = hp.betas
+        n = p.numel()
+        g = grad.to(dtype=torch.float32)
+        m1 = self._read(st.m1, 0, n)
+        m1.lerp_(g, 1 - b1)
+        draws = self._draw("m2", n, index, st.step, True, dtype=torch.float64)
+        if s2 in PENDING_LOOKAHEAD_SCHEMES:
+            _, _, sample = encode_lookahead(st.m2.values, g, beta2=b2, bias=bc2, eps=hp.eps, draws=draws)
+            m2 = sample.mul(b2).addcmul(g, g, value=1 - b2)
+        else:
+            m2 = self._read(st.m2, 0, n)
+            m2.lerp_(g.square(), 1 - b2)
+        den = (m2.sqrt() / math.sqrt(bc2)).add_(hp.eps)
+        if s2 not in PENDING_LOOKAHEAD_SCHEMES:
+            proxy = (1 - b2) * m2 if s2 in VPROXY_LOOKAHEAD_SCHEMES else None
+            codes, scales, _ = encode_lookahead(m2, g, beta2=b2, bias=1 - b2 ** (st.step + 1), eps=hp.eps,
+                                                draws=draws, fresh_proxy=proxy)
+        p.mul_(1 - hp.lr * hp.weight_decay)
+        p.addcdiv_(m1, den, value=-hp.lr / bc1)
+        self._write(st.m1, m1, 0, n, eden=False, draws=None, bias=1.0, eps=1e-8)  # fp32 or nf4
+        if s2 in PENDING_LOOKAHEAD_SCHEMES:
+            st.m2.values = m2
+        else:
+            st.m2.codes[:] = pack(codes)
+            st.m2.scales[:] = scales
+        st.read_preconditioner = None
 
     @staticmethod
     def _read(ms: MomentState, start: int, stop: int) -> torch.Tensor:

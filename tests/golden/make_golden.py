@@ -58,7 +58,10 @@ def snapshot(opt, params, prefix, out):
         st = opt.state[p]
         out[f"{prefix}p{i}_step"] = np.array(st["step"], dtype=np.int64)
         for m in ("m1", "m2"):
-            if f"{m}_code" in st:
+            if m == "m2" and "lookahead_pending_exp_avg_sq" in st:
+                assert "m2" not in st and "m2_code" not in st
+                out[f"{prefix}p{i}_m2_pending"] = to_np(st["lookahead_pending_exp_avg_sq"])
+            elif f"{m}_code" in st:
                 out[f"{prefix}p{i}_{m}_code"] = to_np(st[f"{m}_code"])
                 qs = st[f"{m}_quant_state"]
                 assert isinstance(qs, QuantState) and qs.packed
@@ -70,7 +73,7 @@ def snapshot(opt, params, prefix, out):
 
 
 def trajectory(name, build, shapes, dtype, steps, *, grad_seed, snap_steps, m1_override=None,
-               zero_block_frac=0.0, note=""):
+               zero_block_frac=0.0, note="", grad_mu=-7.0):
     gen = torch.Generator().manual_seed(grad_seed)
     dt = DTYPES[dtype]
     params = [torch.nn.Parameter((torch.randn(s, generator=gen) * 0.02).to(dt)) for s in shapes]
@@ -82,7 +85,7 @@ def trajectory(name, build, shapes, dtype, steps, *, grad_seed, snap_steps, m1_o
         opt.set_m1_quant_scheme_for_parameters([params[j] for j in m1_override[0]], m1_override[1])
     for k in range(steps):
         for i, p in enumerate(params):
-            g = heavy_tailed(tuple(p.shape), gen)
+            g = heavy_tailed(tuple(p.shape), gen, row_mu=grad_mu)
             if zero_block_frac:
                 flat = g.view(-1)
                 nb = flat.numel() // 128
@@ -94,7 +97,7 @@ def trajectory(name, build, shapes, dtype, steps, *, grad_seed, snap_steps, m1_o
         if (k + 1) in snap_steps:
             snapshot(opt, params, f"after{k + 1}_", out)
     cfg.update(dict(name=name, shapes=[list(s) for s in shapes], dtype=dtype, steps=steps,
-                    snap_steps=sorted(snap_steps), m1_override=m1_override, note=note))
+                    snap_steps=sorted(snap_steps), m1_override=m1_override, note=note, grad_mu=grad_mu))
     out["config"] = np.array(json.dumps(cfg))
     np.savez_compressed(os.path.join(HERE, f"traj_{name}.npz"), **out)
     print("wrote", name, sum(v.nbytes for v in out.values()), "bytes raw")
@@ -235,6 +238,20 @@ def main():
                [(4096,)] * 4 + [(64, 128)], "float32", 3, grad_seed=10, snap_steps={1, 3}, zero_block_frac=0.05)
     trajectory("sampled_read_bf16", grouped([("nf4", "dyn4_upd_sr_store_eden", False)], seed=12), [(4096,)],
                "bfloat16", 3, grad_seed=11, snap_steps={3})
+    trajectory("lookahead_groups",
+               grouped([("nf4", "dyn4_la_upd_sr", False), ("fp32", "dyn4_proxy_la_upd_sr", False),
+                        ("nf4", "dyn4_vproxy_la_upd_sr", False), ("fp32", "dyn4_la_upd_sr", False),
+                        ("nf4", "dyn4_proxy_la_upd_sr", False)],
+                       seed=13),
+               [(4096,)] * 4 + [(64, 128)], "float32", 3, grad_seed=12, snap_steps={1, 3}, zero_block_frac=0.05)
+    trajectory("lookahead_bf16",
+               grouped([("nf4", "dyn4_vproxy_la_upd_sr", False), ("nf4", "dyn4_la_upd_sr", False)], seed=14),
+               [(4096,), (4096,)], "bfloat16", 3, grad_seed=13, snap_steps={3})
+    # gradients near 1e-8: sqrt(m2 / bias) comparable to eps, so the bias corrections matter
+    trajectory("lookahead_small_grad",
+               grouped([("fp32", "dyn4_la_upd_sr", False), ("fp32", "dyn4_proxy_la_upd_sr", False),
+                        ("fp32", "dyn4_vproxy_la_upd_sr", False)], seed=15),
+               [(4096,)] * 3, "float32", 4, grad_seed=14, snap_steps={4}, grad_mu=-18.0)
     codec_cases()
     checkpoint_case()
 

@@ -88,7 +88,9 @@ def state_of(opt, p):
     st = opt.state[p]
     out = {"step": st["step"]}
     for m in ("m1", "m2"):
-        if f"{m}_code" in st:
+        if m == "m2" and "lookahead_pending_exp_avg_sq" in st:
+            out["m2_pending"] = st["lookahead_pending_exp_avg_sq"].cpu()
+        elif f"{m}_code" in st:
             out[f"{m}_code"] = st[f"{m}_code"].cpu()
             out[f"{m}_scale"] = st[f"{m}_quant_state"].absmax.cpu()
         else:
@@ -101,6 +103,8 @@ def oracle_state(ms_pair):
     for name, ms in zip(("m1", "m2"), ms_pair):
         if ms.scheme == "fp32":
             st[f"{name}_fp32"] = ms.values.clone()
+        elif ms.scheme in ref.PENDING_LOOKAHEAD_SCHEMES:
+            st[f"{name}_pending"] = ms.values.clone()
         else:
             st[f"{name}_code"] = ms.codes.clone()
             st[f"{name}_scale"] = ms.scales.clone()

@@ -1,0 +1,70 @@
+"""Register budgets of the specialised step kernels, read from the gfx950 assembly of the
+library's own source (compiled here with the library's flags; no GPU needed).
+
+Waves per SIMD follow from the VGPR count (512 per lane per SIMD, allocated in steps of
+8): 128 or fewer VGPRs run 4 waves.  The memory-bound kernels are latency bound at their
+occupancy, and small source changes can make hipcc copy the prefetched tile registers
+instead of coalescing them (about 40 VGPRs), so each kernel's occupancy is pinned here.
+"""
+
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+
+from adamw4bit_amd import build
+
+# (m1 spec, m2 spec, dtype) template arguments -> minimum waves per SIMD
+# m1: 1 = NF4 round-to-nearest, 66 = value-space SR with guards;
+# m2: 33 = round-to-nearest + EDEN, 67 = update-SR with guards, 99 = update-SR + EDEN, 0 = fp32;
+# dtype: 0 = fp32, 1 = bf16.
+MIN_WAVES = {
+    (1, 33, 0): 3, (1, 67, 0): 4, (1, 33, 1): 4, (1, 67, 1): 4, (66, 67, 0): 3, (66, 67, 1): 4,
+    (1, 0, 0): 4, (1, 0, 1): 4, (1, 99, 0): 3, (1, 99, 1): 4,
+}
+
+
+def waves_per_simd(vgprs: int) -> int:
+    granule = (vgprs + 7) // 8 * 8
+    return min(8, 512 // granule)
+
+
+@pytest.fixture(scope="module")
+def kernel_vgprs():
+    hipcc = build.hipcc()
+    if not os.path.exists(hipcc):
+        pytest.skip("hipcc not available")
+    with tempfile.TemporaryDirectory() as tmp:
+        out = os.path.join(tmp, "fused_step.s")
+        cmd = [a for a in build.command(out) if a not in ("-shared", "-fPIC")] + ["--cuda-device-only", "-S"]
+        proc = subprocess.run(cmd, capture_output=True, text=True)
+        assert proc.returncode == 0, proc.stderr[-2000:]
+        text = open(out).read()
+    meta = text[text.index("amdhsa.kernels"):]
+    found = {}
+    for block in re.split(r"\n  - \.", meta):
+        name = re.search(r"\.name:\s+(\S+)", block)
+        if not name or "step_kernel" not in name.group(1):
+            continue
+        args = re.search(r"step_kernelILi(\d+)ELi(\d+)ELi(\d+)E", name.group(1))
+        vgpr = re.search(r"\.vgpr_count:\s+(\d+)", block)
+        spill = re.search(r"\.vgpr_spill_count:\s+(\d+)", block)
+        found[tuple(int(x) for x in args.groups())] = (int(vgpr.group(1)), int(spill.group(1)))
+    return found
+
+
+def test_specialised_kernels_keep_their_occupancy(kernel_vgprs):
+    for key, waves in MIN_WAVES.items():
+        assert key in kernel_vgprs, f"kernel {key} not instantiated"
+        vgprs, spills = kernel_vgprs[key]
+        assert spills == 0, f"kernel {key} spills {spills} VGPRs"
+        assert waves_per_simd(vgprs) >= waves, f"kernel {key}: {vgprs} VGPRs -> {waves_per_simd(vgprs)} waves < {waves}"
+
+
+def test_generic_kernels_do_not_spill(kernel_vgprs):
+    generic = [k for k in kernel_vgprs if k not in MIN_WAVES]
+    assert generic, "generic kernels not found"
+    for key in generic:
+        assert kernel_vgprs[key][1] == 0, f"kernel {key} spills"

@@ -185,8 +185,9 @@ def test_golden_trajectory(name):
                         assert torch.equal(H.bits(st[f"{m}_scale"]),
                                            H.bits(torch.from_numpy(arrays[f"{pre}_{m}_scale"]))), (name, pre, m)
                 else:
-                    assert torch.equal(H.bits(st[f"{m}_fp32"].reshape(-1)),
-                                       H.bits(torch.from_numpy(arrays[f"{pre}_{m}_fp32"]).reshape(-1))), (name, m)
+                    kind = "pending" if f"{pre}_{m}_pending" in arrays else "fp32"
+                    assert torch.equal(H.bits(st[f"{m}_{kind}"].reshape(-1)),
+                                       H.bits(torch.from_numpy(arrays[f"{pre}_{m}_{kind}"]).reshape(-1))), (name, m)
             # 1 / denominator of the store-EDEN schemes: within the square root's ulp
             if f"{pre}_m2_pre" in arrays:
                 got = opt.state[p]["m2_read_preconditioner"].cpu().reshape(-1)
@@ -242,7 +243,7 @@ def run_pair(make_opt, shapes, dtype, steps, *, seed=0, grad_seed=1, m1_override
         for i, p in enumerate(params):
             st = H.state_of(opt, p)
             for m, ms in (("m1", oracle.states[i].m1), ("m2", oracle.states[i].m2)):
-                if ref.is_stochastic(ms.scheme):
+                if ref.is_stochastic(ms.scheme) and f"{m}_code" in st:
                     parted[i] |= H.code_diff_mask(st[f"{m}_code"], ms.codes, p.numel())
     torch.cuda.synchronize()
     return opt, params, oracle, cpu_params, parted
@@ -270,7 +271,8 @@ def compare_pair(opt, params, oracle, cpu_params, parted, what, steps=1):
                     assert flips == 0, f"{what} p{i} {m} ({ms.scheme}): {flips} flips"
                     assert torch.equal(H.bits(st[f"{m}_scale"]), H.bits(ost[f"{m}_scale"])), (what, i, m)
             else:
-                assert torch.equal(H.bits(st[f"{m}_fp32"].reshape(-1)), H.bits(ost[f"{m}_fp32"])), (what, i, m)
+                kind = "pending" if f"{m}_pending" in ost else "fp32"
+                assert torch.equal(H.bits(st[f"{m}_{kind}"].reshape(-1)), H.bits(ost[f"{m}_{kind}"])), (what, i, m)
         n_parted = int(parted[i].sum())
         total_parted += n_parted
         exact = H.assert_params_close(p, cp, f"{what} p{i}", steps=steps, exclude=parted[i])
@@ -321,6 +323,31 @@ def test_sampled_read_schemes_match_oracle(dtype):
         keep = ~parted[i]
         torch.testing.assert_close(got[keep], expect.reshape(-1)[keep], rtol=1e-6, atol=0.0)
         assert got.shape[0] == p.numel() and "m2" not in opt.state[p]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_lookahead_schemes_match_oracle(dtype):
+    """Lookahead update-SR m2 (reference step, adamw.py:566-614): the pending form samples its fp32
+    state before the update, the proxies store codes sampled for the next step; float64
+    probabilities, on-device Philox replayed into the oracle.  Codes, scales and the pending
+    state bit-exact (no parted values)."""
+    log(f"lookahead schemes {dtype} x 4 steps")
+    spec = [("nf4", "dyn4_la_upd_sr"), ("fp32", "dyn4_proxy_la_upd_sr"), ("nf4", "dyn4_vproxy_la_upd_sr"),
+            ("fp32", "dyn4_la_upd_sr"), ("nf4", "dyn4_nz")]
+
+    def make(ps):
+        groups = [dict(params=[p], m1_quant_scheme=a, m2_quant_scheme=b) for p, (a, b) in zip(ps, spec)]
+        return aw.QuantizedAdamW(groups, lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True,
+                                 quant_rng_seed=5, m1_quant_scheme="nf4", m2_quant_scheme="dyn4_nz")
+    out = run_pair(make, [(512, 1024), (256, 512), (384, 128), (1024, 256), (128, 256)], dtype, 4, seed=5,
+                   zero_block_frac=0.02)
+    parted = compare_pair(*out, f"lookahead {dtype}", steps=4)
+    assert parted == 0
+    opt, params, _, _, _ = out
+    for p, (_, m2) in zip(params, spec):
+        st = opt.state[p]
+        assert ("lookahead_pending_exp_avg_sq" in st) == (m2 == "dyn4_la_upd_sr")
+        assert "m2_read_preconditioner" not in st
 
 
 def test_zipsr_4096x4096_matches_oracle():

@@ -1,6 +1,6 @@
 """The optimizer's host API without a GPU: constructor validation with the reference's own
-messages (``adamw.py:127-239``), the scheme set this build steps, and the errors for the
-parts it does not (the reference's tests ``tests/quantization/test_upd_sr_store_eden.py``,
+messages (``adamw.py:127-239``), the scheme set the fused step covers, and the errors for
+the parts it does not (the reference's tests ``tests/quantization/test_upd_sr_store_eden.py``,
 ``test_dyn4_la_upd_sr.py`` and ``test_upd_sr_full4bit.py`` exercise the same paths)."""
 
 from __future__ import annotations
@@ -58,9 +58,12 @@ def test_lookahead_rejects_extra_corrections(scheme):
 @pytest.mark.parametrize("m2", ["dyn4_upd_sr", "lin4_upd_sr", "dyn4_upd_sr_store_eden", "lin4_upd_sr_store_eden",
                                 "dyn4_upd_sr_fp32read", "lin4_upd_sr_fp32read", "dyn4_lookahead_sr",
                                 "dyn4_upd_sr_fp32read_nextbc", "dyn4_nz", "lin4_nz", "dyn4", "lin4", "dyn4_sr",
-                                "lin4_sr", "fp32"])
+                                "lin4_sr", "fp32", "dyn4_la_upd_sr", "dyn4_proxy_la_upd_sr",
+                                "dyn4_vproxy_la_upd_sr"])
 @pytest.mark.parametrize("m1", ["nf4", "nf4_sr", "sdyn4", "sdyn4_sr", "fp32"])
 def test_schemes_of_the_fused_step_construct(m1, m2):
+    if "_la_" in m2 and m1 not in ("fp32", "nf4"):
+        pytest.skip("lookahead update-SR takes an fp32 or nf4 m1 (adamw.py:198-208)")
     opt = make(m1_quant_scheme=m1, m2_quant_scheme=m2)
     group = opt.param_groups[0]
     assert group["m1_quant_scheme"] == m1 and group["m2_quant_scheme"] == m2
@@ -71,9 +74,6 @@ def test_schemes_of_the_fused_step_construct(m1, m2):
 
 @pytest.mark.parametrize("kw", [
     dict(m1_quant_scheme="linear"), dict(m2_quant_scheme="dynamic"),
-    dict(m1_quant_scheme="fp32", m2_quant_scheme="dyn4_la_upd_sr"),
-    dict(m1_quant_scheme="nf4", m2_quant_scheme="dyn4_proxy_la_upd_sr"),
-    dict(m1_quant_scheme="fp32", m2_quant_scheme="dyn4_vproxy_la_upd_sr"),
     dict(update_sign_clip=0.5), dict(record_update_direction_every=2), dict(block_size=256),
 ])
 def test_parts_outside_the_fused_step_raise(kw):
@@ -86,3 +86,14 @@ def test_step_needs_a_hip_device():
     opt.param_groups[0]["params"][0].grad = torch.ones(4096)
     with pytest.raises(NotImplementedError, match="HIP devices"):
         opt.step()
+
+
+@pytest.mark.parametrize("scheme", ["dyn4_la_upd_sr", "dyn4_proxy_la_upd_sr", "dyn4_vproxy_la_upd_sr"])
+def test_lookahead_state_layout(scheme):
+    # test_dyn4_la_upd_sr.py:106-114, 300-307: the pending form keeps fp32 state under
+    # "lookahead_pending_exp_avg_sq" and no codes; the proxies keep codes.  Initial state only
+    # (the step itself needs a HIP device).
+    from adamw4bit_amd.quantization import PENDING_LOOKAHEAD_SCHEMES, SCHEMES, initial_code_and_scale
+    assert SCHEMES[scheme][0] == q.CB_DYN4 and SCHEMES[scheme][1] == q.ROUND_LOOKAHEAD_SR
+    if scheme not in PENDING_LOOKAHEAD_SCHEMES:
+        assert initial_code_and_scale(scheme, False) == initial_code_and_scale("dyn4", False)

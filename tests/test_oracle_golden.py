@@ -44,6 +44,8 @@ def _copy_state(st):
         ms = getattr(st, name)
         if ms.scheme == "fp32":
             out[f"{name}_fp32"] = ms.values.clone()
+        elif ms.scheme in ref.PENDING_LOOKAHEAD_SCHEMES:
+            out[f"{name}_pending"] = ms.values.clone()
         else:
             out[f"{name}_code"] = ms.codes.clone()
             out[f"{name}_scale"] = ms.scales.clone()
@@ -62,7 +64,7 @@ def test_oracle_matches_reference_trajectory(name):
             expect_p = tensor(arrays[prefix], cfg["dtype"]).reshape(p.shape)
             assert torch.equal(bits(p), bits(expect_p)), f"{name} step {step} param {i}"
             assert st["step"] == int(arrays[f"{prefix}_step"])
-            for key in ("m1_code", "m2_code", "m1_scale", "m2_scale", "m1_fp32", "m2_fp32", "m2_pre"):
+            for key in ("m1_code", "m2_code", "m1_scale", "m2_scale", "m1_fp32", "m2_fp32", "m2_pre", "m2_pending"):
                 if f"{prefix}_{key}" in arrays:
                     expect = torch.from_numpy(arrays[f"{prefix}_{key}"])
                     assert key in st, f"{name}: oracle state lacks {key} for param {i}"

@@ -277,3 +277,130 @@ def test_planted_mistakes_are_caught(monkeypatch):
     step = max(snaps)
     _, st = snaps[step][0]
     assert not torch.equal(st["m2_code"], torch.from_numpy(arrays[f"after{step}_p0_m2_code"]))
+
+
+# ---------------------------------------------------------------------------
+# Lookahead update-SR (quantization.py:779-895, adamw.py:566-614)
+# ---------------------------------------------------------------------------
+
+def _next_preconditioner(prev, grad, beta2, bias, eps):
+    # The target of test_dyn4_la_upd_sr.py:14-23, written out in float64.
+    return 1.0 / (((beta2 * prev + (1.0 - beta2) * grad.square()) / bias).sqrt() + eps)
+
+
+def test_lookahead_block_scale_is_dyn4s():
+    # test_dyn4_la_upd_sr.py:26-41
+    z = torch.linspace(1e-4, 0.5, steps=128, dtype=torch.float32)
+    g = torch.linspace(-0.2, 0.2, steps=128, dtype=torch.float32)
+    _, la_scale, _ = ref.encode_lookahead(z, g, beta2=0.95, bias=0.25, eps=1e-8,
+                                          draws=torch.rand(128, dtype=torch.float64))
+    _, dyn4_scale = ref.encode(z, "dyn4")
+    assert torch.equal(la_scale, dyn4_scale)
+
+
+def _grid_draws(grid, n):
+    return ((torch.arange(grid, dtype=torch.float64) + 0.5) / grid).view(-1, 1).expand(grid, n).contiguous()
+
+
+@pytest.mark.parametrize("scale", [1.0, 1e-16])
+def test_lookahead_is_next_preconditioner_unbiased(scale):
+    # test_dyn4_la_upd_sr.py:44-79 by Monte Carlo; here on a uniform grid of draws, whose mean
+    # is the expectation up to (f(lo) - f(hi)) / grid.  Negative and zero state clamps to 0.
+    # scale 1e-16: sqrt(n / bias) is comparable to eps, where the bias does not cancel.
+    gen = torch.Generator().manual_seed(5)
+    z = torch.rand(128, generator=gen) ** 4 * 0.5 * scale
+    z[:4] = torch.tensor([0.0, -1e-3, 0.5, 0.03125]) * scale
+    g = (torch.rand(128, generator=gen) - 0.5) * 0.3 * math.sqrt(scale)
+    beta2, bias, eps = 0.95, 0.4, 1e-8
+    grid = 4096
+    _, s, samples = ref.encode_lookahead(z.repeat(grid), g.repeat(grid), beta2=beta2, bias=bias, eps=eps,
+                                         draws=_grid_draws(grid, 128))
+    f = _next_preconditioner(samples.double().view(grid, 128), g.double(), beta2, bias, eps)
+    expectation = f.mean(0)
+    target = _next_preconditioner(z.clamp_min(0).double(), g.double(), beta2, bias, eps)
+    cb = ref.codebook("dyn4").double()
+    lo_hi = [_next_preconditioner(s[0].double() * cb[k], g.double(), beta2, bias, eps) for k in (0, 15)]
+    slack = (lo_hi[0] - lo_hi[1]).abs() / grid + 1e-9 * target
+    assert ((expectation - target).abs() <= slack).all()
+    # values at a level (and the clamped zeros) are stored exactly; at scale 1e-16 the block
+    # maximum sits below the 1e-12 scale floor and is no level
+    for i in (0, 1, 2) if scale == 1.0 else (0, 1):
+        assert torch.all(samples.view(grid, 128)[:, i] == z[i].clamp_min(0))
+
+
+def test_lookahead_flat_interval_is_value_unbiased():
+    # A fresh term that swamps beta2 * q makes f flat over the interval: the rule falls back to
+    # value-unbiased rounding, E[sample] = z.
+    # (levels 1e-9 apart against n ~ 5e4: relative differences of f near 1e-14 < 1e-12)
+    gen = torch.Generator().manual_seed(6)
+    z = torch.rand(128, generator=gen) * 1e-9
+    g = torch.full((128,), 1e3)
+    grid = 4096
+    _, s, samples = ref.encode_lookahead(z.repeat(grid), g.repeat(grid), beta2=0.95, bias=1.0, eps=1e-8,
+                                         draws=_grid_draws(grid, 128))
+    mean = samples.double().view(grid, 128).mean(0)
+    cb = ref.codebook("dyn4").double()
+    width = s[0].double() * (cb[1:] - cb[:-1]).max()
+    assert ((mean - z.double()).abs() <= width / grid + 1e-6 * z.double()).all()
+    # both neighbours drawn (the fallback, not a guard) except at the block maximum, a level
+    assert samples.view(grid, 128).std(0)[z != z.max()].min() > 0
+
+
+@pytest.mark.parametrize("scheme", ["dyn4_la_upd_sr", "dyn4_proxy_la_upd_sr", "dyn4_vproxy_la_upd_sr"])
+def test_lookahead_first_step_equals_torch_adamw(scheme):
+    # test_dyn4_la_upd_sr.py:82-114 (pending state = (1 - beta2) g^2) and :276-316 (proxies).
+    values = torch.linspace(-1.0, 1.0, steps=4096)
+    grad = torch.linspace(-0.5, 0.5, steps=4096)
+    p = values.clone()
+    r = torch.nn.Parameter(values.clone())
+    oracle = ref.Oracle([p], ref.Hyper(1e-3, (0.9, 0.95), 1e-8, 0.0), ["fp32"], [scheme], [False], seed=0,
+                        optimized=False)
+    adamw = torch.optim.AdamW([r], lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.0)
+    oracle.step([grad.clone()])
+    r.grad = grad.clone()
+    adamw.step()
+    torch.testing.assert_close(p, r.detach(), rtol=1e-6, atol=1e-6)
+    m2 = oracle.states[0].m2
+    if scheme == "dyn4_la_upd_sr":
+        torch.testing.assert_close(m2.values, (1.0 - 0.95) * grad.square())
+        assert m2.codes is None
+    else:
+        assert m2.codes.numel() == 2048 and torch.isfinite(ref.decode(m2.codes, m2.scales, "dyn4", 4096)).all()
+
+
+def _all_params_match(name):
+    cfg, arrays = load(name)
+    _, snaps = run_oracle(cfg, arrays)
+    step = max(snaps)
+    from tests._fixtures import tensor
+    ok = True
+    for i, (p, st) in enumerate(snaps[step]):
+        ok &= torch.equal(bits(p), bits(tensor(arrays[f"after{step}_p{i}"], cfg["dtype"]).reshape(p.shape)))
+        for key in ("m2_code", "m2_scale", "m2_pending"):
+            if f"after{step}_p{i}_{key}" in arrays:
+                ok &= torch.equal(bits(st[key]), bits(torch.from_numpy(arrays[f"after{step}_p{i}_{key}"])))
+    return ok
+
+
+def test_lookahead_planted_mistakes_are_caught(monkeypatch):
+    name = "traj_lookahead_groups.npz"
+    assert _all_params_match(name)
+    original = ref.encode_lookahead
+
+    # 1. v-proxy with the gradient's fresh term instead of (1 - beta2) m2.
+    monkeypatch.setattr(ref, "encode_lookahead", lambda *a, fresh_proxy=None, **kw: original(*a, **kw))
+    assert not _all_params_match(name)
+    # 2. Probabilities without the next step's beta2 decay of the candidate levels.
+    monkeypatch.setattr(ref, "encode_lookahead", lambda *a, beta2, **kw: original(*a, beta2=1.0 - 1e-12, **kw))
+    assert not _all_params_match(name)
+    # 3. Bias corrections one step behind (1 - beta2^(k-1) for 1 - beta2^k).  The bias cancels
+    # from P(lo) wherever sqrt(m2 / bias) >> eps, so this needs the small-gradient trajectory.
+    small = "traj_lookahead_small_grad.npz"
+    monkeypatch.setattr(ref, "encode_lookahead", original)
+    assert _all_params_match(small)
+
+    def step_behind(*a, bias, **kw):
+        k = round(math.log(1.0 - bias) / math.log(0.95))
+        return original(*a, bias=1.0 - 0.95 ** (k - 1) if k > 1 else bias, **kw)
+    monkeypatch.setattr(ref, "encode_lookahead", step_behind)
+    assert not _all_params_match(small)
