@@ -17,7 +17,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIBRARY = os.path.join(HERE, "libadamw4bit_hip.so")
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 BLOCK = 128
 
 # Error codes
@@ -29,7 +29,7 @@ ROUND_FP32, ROUND_RTN, ROUND_STATE_SR, ROUND_UPDATE_SR, ROUND_LOOKAHEAD_SR = 0, 
 MOMENT_ZERO_FLOOR, MOMENT_EDEN, MOMENT_GUARDS, MOMENT_EXT_DRAWS = 0x1, 0x2, 0x4, 0x8
 MOMENT_SAMPLED_READ, MOMENT_READ_RAW_SCALE, MOMENT_FRESH_PROXY, MOMENT_PENDING = 0x10, 0x20, 0x40, 0x80
 F32, BF16, F16 = 0, 1, 2
-TENSOR_LERP1_LARGE, TENSOR_LERP2_LARGE, TENSOR_VEC_ALIGNED = 0x1, 0x2, 0x4
+TENSOR_LERP1_LARGE, TENSOR_LERP2_LARGE, TENSOR_VEC_ALIGNED, TENSOR_GRAD_SCALE = 0x1, 0x2, 0x4, 0x8
 
 NUM_LUTS, LUT_HALF, LUT_EXP0 = 11, 89, 936
 LUT_ENTRIES = 2 * LUT_HALF
@@ -42,13 +42,13 @@ MOMENT = np.dtype([
     ("la_beta2", "<f8"), ("la_fresh_weight", "<f8"), ("la_bias", "<f8"), ("la_eps", "<f8"),
 ])
 TENSOR = np.dtype([
-    ("param", "<u8"), ("grad", "<u8"), ("numel", "<i8"),
+    ("param", "<u8"), ("grad", "<u8"), ("grad_scale", "<u8"), ("numel", "<i8"),
     ("param_dtype", "<i4"), ("grad_dtype", "<i4"), ("flags", "<i4"),
     ("w1", "<f4"), ("w2", "<f4"), ("decay", "<f4"), ("step_coef", "<f4"),
     ("bc2_sqrt", "<f4"), ("bc2_sqrt_rcp", "<f4"), ("eps", "<f4"),
     ("m1", MOMENT), ("m2", MOMENT),
 ])
-assert MOMENT.itemsize == 104 and TENSOR.itemsize == 272
+assert MOMENT.itemsize == 104 and TENSOR.itemsize == 280
 
 # Every function the header declares, with its ctypes signature.
 SIGNATURES = {
@@ -60,6 +60,8 @@ SIGNATURES = {
     "aw4_uniforms": (ctypes.c_int, [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int64, ctypes.c_void_p,
                                     ctypes.c_void_p]),
     "aw4_encode_tables": (ctypes.c_int64, [ctypes.c_void_p, ctypes.c_int64]),
+    "aw4_clip_coefficient": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_float, ctypes.c_void_p,
+                                            ctypes.c_void_p, ctypes.c_void_p]),
 }
 
 
@@ -112,6 +114,14 @@ def quantize(values_ptr: int, numel: int, moment: np.ndarray, stream: int) -> No
 def dequantize(moment: np.ndarray, numel: int, out_ptr: int, stream: int) -> None:
     assert moment.dtype == MOMENT and moment.shape == ()
     check(library().aw4_dequantize(moment.ctypes.data, numel, out_ptr, stream), "aw4_dequantize")
+
+
+def clip_coefficient(table: np.ndarray, max_norm: float, norm_ptr: int, coef_ptr: int, stream: int) -> None:
+    """Global gradient norm of the rows of ``table`` and the clipping coefficient, written to
+    the device floats at ``norm_ptr`` and ``coef_ptr``."""
+    assert table.dtype == TENSOR and table.flags.c_contiguous
+    check(library().aw4_clip_coefficient(table.ctypes.data, len(table), max_norm, norm_ptr, coef_ptr, stream),
+          "aw4_clip_coefficient")
 
 
 def uniforms(seed: int, offset: int, n: int, out_ptr: int, stream: int) -> None:

@@ -278,6 +278,9 @@ class QuantizedAdamW(Optimizer):
         # on-device Philox draws of a stochastic write (bit-exact comparisons with fed draws).
         self._draw_provider = None
         self._launch_plan: Optional[_LaunchPlan] = None
+        # Gradient clipping computed by clip_grad_norm_ and applied by the next step:
+        # (device, fp32 coefficient on that device) or None.
+        self._grad_clip: Optional[Tuple[torch.device, torch.Tensor]] = None
         if optimized:
             for group in self.param_groups:
                 group.setdefault(_CHUNK_KEY, _CHUNK_NUMEL)
@@ -473,6 +476,68 @@ class QuantizedAdamW(Optimizer):
     # The step
     # ------------------------------------------------------------------
     @torch.no_grad()
+    # ------------------------------------------------------------------
+    # Gradient clipping fused into the step
+    # ------------------------------------------------------------------
+    @torch.no_grad()
+    def clip_grad_norm_(self, max_norm: float, norm_type: float = 2.0, error_if_nonfinite: bool = False,
+                        foreach: Optional[bool] = None) -> torch.Tensor:
+        """``torch.nn.utils.clip_grad_norm_`` over this optimizer's parameters, fused into the next
+        ``step()``.
+
+        The reference's training examples clip before every step (an HF Trainer with
+        ``max_grad_norm=1.0``, ``examples/train_gpt_small.py:214``).  Here one pass over the
+        gradients computes the total norm and the coefficient ``min(max_norm / (norm + 1e-6), 1)``
+        on the device with torch's dtype rounding points (``aw4_clip_coefficient``), and the next
+        ``step()`` reads every gradient value as ``grad_dtype(g * coef)`` -- what torch's in-place
+        ``_foreach_mul_`` would have stored -- instead of scaling the gradients in memory.  The
+        gradients themselves are left unscaled.  Returns the total norm (a 0-dim tensor on the
+        parameters' device, in the promoted gradient dtype), like torch.  Only the 2-norm of
+        parameters on one HIP device; one pending clip per step.
+        """
+        if float(norm_type) != 2.0:
+            raise NotImplementedError("the fused clip computes the 2-norm only")
+        if self._grad_clip is not None:
+            raise RuntimeError("a gradient clip is already pending: call step() before clipping again")
+        params = [p for group in self.param_groups for p in group["params"] if p.grad is not None]
+        if not params:
+            return torch.tensor(0.0)
+        devices = {p.device for p in params}
+        device = params[0].device
+        if len(devices) != 1 or device.type != "cuda":
+            raise NotImplementedError("the fused clip runs over gradients on one HIP device")
+        grads = []
+        for p in params:
+            g = p.grad
+            if g.layout != torch.strided or g.dtype not in _DTYPES:
+                raise NotImplementedError("gradients must be dense float32/bfloat16/float16 tensors")
+            grads.append(g if g.is_contiguous() else g.contiguous())
+        table = np.zeros(len(grads), dtype=_lib.TENSOR)
+        table["grad"] = [g.data_ptr() for g in grads]
+        table["numel"] = [g.numel() for g in grads]
+        table["grad_dtype"] = [_DTYPES[g.dtype] for g in grads]
+        table["flags"] = [_lib.TENSOR_VEC_ALIGNED if g.data_ptr() % (4 * g.element_size()) == 0 else 0 for g in grads]
+        out = torch.empty(2, dtype=torch.float32, device=device)  # [total norm, coefficient]
+        _ops.clip_coefficient_(grads, out, torch.from_numpy(table.view(np.uint8)), float(max_norm))
+        result_dtype = grads[0].dtype
+        for g in grads[1:]:
+            if g.dtype != result_dtype:
+                result_dtype = torch.float32  # torch.stack promotes the per-tensor norms
+        total = out[0].to(result_dtype)
+        if error_if_nonfinite and bool(torch.logical_or(total.isnan(), total.isinf())):
+            raise RuntimeError(
+                f"The total norm of order {float(norm_type)} for gradients from `parameters` is non-finite, so it "
+                "cannot be clipped. To disable this error and scale the gradients by the non-finite norm anyway, "
+                "set `error_if_nonfinite=False`")
+        self._grad_clip = (device, out[1:])
+        return total
+
+    def _take_grad_clip(self, device: torch.device) -> Optional[torch.Tensor]:
+        clip = self._grad_clip
+        if clip is None or clip[0] != device:
+            return None
+        return clip[1]
+
     def step(self, closure=None):  # type: ignore[override]
         loss = None
         if closure is not None:
@@ -480,6 +545,7 @@ class QuantizedAdamW(Optimizer):
                 loss = closure()
         plan = self._launch_plan
         if plan is not None and plan.step(self):
+            self._grad_clip = None
             return loss
         # per device: launch rows, parameters, written states, read inputs (gradients, draws)
         per_device: Dict[torch.device, Tuple[List[Tuple], List[torch.Tensor], List[torch.Tensor],
@@ -494,8 +560,14 @@ class QuantizedAdamW(Optimizer):
                 params.append(p)
         tables = {}
         for device, (rows, params, written, read) in per_device.items():
-            tables[device] = np.array(rows, dtype=_lib.TENSOR)
-            _ops.fused_step_(params, written, read, torch.from_numpy(tables[device].view(np.uint8)))
+            table = tables[device] = np.array(rows, dtype=_lib.TENSOR)
+            coef = self._take_grad_clip(device)
+            if coef is not None:
+                table["grad_scale"] = coef.data_ptr()
+                table["flags"] |= _lib.TENSOR_GRAD_SCALE
+                read = read + [coef]
+            _ops.fused_step_(params, written, read, torch.from_numpy(table.view(np.uint8)))
+        self._grad_clip = None
         self._launch_plan = _LaunchPlan.build(self, per_device, tables, info)
         return loss
 
@@ -597,8 +669,8 @@ class QuantizedAdamW(Optimizer):
             # update; the proxies encode the new m2 for the next step's bias correction.
             beta2 = float(group["betas"][1])
             bias = 1 - beta2 ** step if schemes[1] in PENDING_LOOKAHEAD_SCHEMES else 1 - beta2 ** (step + 1)
-            flags = m2[8] | (_lib.MOMENT_FRESH_PROXY if schemes[1] in VPROXY_LOOKAHEAD_SCHEMES else 0)
-            m2 = m2[:8] + (flags,) + m2[9:12] + (beta2, 1.0 - beta2, max(float(bias), 1e-12), float(group["eps"]))
+            m2_flags = m2[8] | (_lib.MOMENT_FRESH_PROXY if schemes[1] in VPROXY_LOOKAHEAD_SCHEMES else 0)
+            m2 = m2[:8] + (m2_flags,) + m2[9:12] + (beta2, 1.0 - beta2, max(float(bias), 1e-12), float(group["eps"]))
             state.pop("m2_read_preconditioner", None)
         elif schemes[1] in STORE_EDEN_SCHEMES:
             # Reads with the scale before EDEN; stores the calibrated scale and 1/denominator.
@@ -615,7 +687,7 @@ class QuantizedAdamW(Optimizer):
                 m2 = m2[:8] + (m2[8] | _lib.MOMENT_SAMPLED_READ,) + m2[9:]
         if info is not None:
             info.append((p, optimized, schemes))
-        return (p.data_ptr(), grad.data_ptr(), n, _DTYPES[p.dtype], _DTYPES[grad.dtype], flags,
+        return (p.data_ptr(), grad.data_ptr(), 0, n, _DTYPES[p.dtype], _DTYPES[grad.dtype], flags,
                 c.w1, c.w2, c.decay, c.step_coef, c.bc2_sqrt, c.bc2_sqrt_rcp, c.eps, m1, m2)
 
     def _init_moment(self, p, state, moment, scheme, size, eden, chunk) -> None:
@@ -854,6 +926,11 @@ class _LaunchPlan:
             m1["rng_offset"] = offsets["m1"]
             m2["rng_offset"] = offsets["m2"]
             read = [p.grad for p in params]
+            coef = opt._take_grad_clip(params[0].device)
+            table["grad_scale"] = 0 if coef is None else coef.data_ptr()
+            if coef is not None:
+                table["flags"] |= _lib.TENSOR_GRAD_SCALE
+                read.append(coef)
             _ops.fused_step_(params, written, read, torch.from_numpy(table.view(np.uint8)))
         return True
 

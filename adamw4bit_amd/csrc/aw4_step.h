@@ -99,6 +99,21 @@ __device__ __forceinline__ float round_to_storage(float v) {
     else return v;
 }
 
+// Gradient clipping (AW4_TENSOR_GRAD_SCALE): g -> grad_dtype(fp32(g * c)), the value the
+// in-place _foreach_mul_ of torch.nn.utils.clip_grad_norm_ leaves in a gradient of that dtype
+// (the fp32 product of two 16-bit values is exact, so one rounding to the dtype).  G is the
+// gradient's storage dtype, D_ANY for a run-time one.  The branch is uniform per tensor.
+template <int G>
+__device__ __forceinline__ void clip_grads(const aw4_tensor& T, float* g, int n) {
+    if (__builtin_expect((T.flags & AW4_TENSOR_GRAD_SCALE) == 0, 1)) return;
+    const float c = *gaddr<const float>(T.grad_scale);
+    const int dt = G == D_ANY ? T.grad_dtype : G;
+    for (int t = 0; t < n; ++t) {
+        const float v = g[t] * c;
+        g[t] = dt == D_BF16 ? round_to_storage<D_BF16>(v) : dt == D_F16 ? round_to_storage<D_F16>(v) : v;
+    }
+}
+
 // Run-time dtype dispatch for the generic kernel (D_ANY): loads convert to fp32 words.
 __device__ __forceinline__ void load_words_any(int dtype, uint64_t base, int64_t e, bool vec, uint32_t* w) {
     uint32_t r[4];
@@ -297,6 +312,7 @@ __device__ __forceinline__ void update_quarter(const aw4_tensor& T, int q, const
     constexpr int DC = D == D_ANY ? D_F32 : D;  // generic loads are already fp32 words
     float g[4], p[4], a[4], b[4];
     words_to_f32<DC>(&in.g[In::kW * q], g);
+    clip_grads<D>(T, g, 4);
     words_to_f32<DC>(&in.p[In::kW * q], p);
     if (moment_quantized<M1K>(T.m1)) {
         if constexpr (In::kQ1) decode4(L1.dec, in.c1[q >> 1] >> (16 * (q & 1)), in.s1, a);
@@ -378,13 +394,14 @@ __device__ __forceinline__ void update_tile_any(const aw4_tensor& T, const TileL
 
 // The gradients of this lane's 16 values as fp32.
 template <int M1K, int M2K, int D>
-__device__ __forceinline__ void tile_grads(const TileInputs<M1K, M2K, D>& in, float (&g)[16]) {
+__device__ __forceinline__ void tile_grads(const aw4_tensor& T, const TileInputs<M1K, M2K, D>& in, float (&g)[16]) {
     using In = TileInputs<M1K, M2K, D>;
     constexpr int DC = D == D_ANY ? D_F32 : D;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         float v[4];
         words_to_f32<DC>(&in.g[In::kW * q], v);
+        clip_grads<D>(T, v, 4);
 #pragma unroll
         for (int t = 0; t < 4; ++t) g[4 * q + t] = v[t];
     }
@@ -457,7 +474,8 @@ template <int D>
 __device__ __forceinline__ void step_values_one(const aw4_tensor& T, int64_t k) {
     const gptr<float> v1 = gaddr<float>(T.m1.values);
     const gptr<float> v2 = gaddr<float>(T.m2.values);
-    const float g = load_value<D>(T, T.grad, T.grad_dtype, k);
+    float g = load_value<D>(T, T.grad, T.grad_dtype, k);
+    clip_grads<D>(T, &g, 1);
     float p = load_value<D>(T, T.param, T.param_dtype, k);
     float a = v1[k], b = v2[k];
     const int lf = T.flags & (AW4_TENSOR_LERP1_LARGE | AW4_TENSOR_LERP2_LARGE);
@@ -618,7 +636,7 @@ __device__ __forceinline__ void run_tiles(const StepHeader* hdr, const LdsT& lds
                     // lookahead update-SR: sample the pending state before the update, or encode
                     // the new m2 after it
                     float g[16];
-                    tile_grads(in, g);
+                    tile_grads(T, in, g);
                     const bool pending = (T.m2.flags & AW4_MOMENT_PENDING) != 0;
                     const float w2f = (float)T.m2.la_fresh_weight;
                     float prior[16];

@@ -42,6 +42,7 @@
 #include <vector>
 
 #include "adamw4bit_hip.h"
+#include "aw4_prologue.h"
 #include "aw4_step.h"
 
 namespace {
@@ -49,7 +50,7 @@ namespace {
 using namespace aw4;
 
 static_assert(sizeof(aw4_moment) == 104, "aw4_moment layout");
-static_assert(sizeof(aw4_tensor) == 272, "aw4_tensor layout");
+static_assert(sizeof(aw4_tensor) == 280, "aw4_tensor layout");
 
 // Codebooks as fp32 bit patterns (ascending; code = index).  Values of the reference's
 // closed forms: NF4 table (quantization.py:401-422), signed and unsigned dynamic maps
@@ -496,6 +497,8 @@ int check_tensor(const aw4_tensor& t, int index) {
         if (!aligned(t.param, pa) || !aligned(t.grad, ga))
             return set_error(AW4_EALIGN, "tensor %d: VEC_ALIGNED but param/grad misaligned", index);
     }
+    if ((t.flags & AW4_TENSOR_GRAD_SCALE) && (!t.grad_scale || !aligned(t.grad_scale, 4)))
+        return set_error(AW4_EINVAL, "tensor %d: GRAD_SCALE without a 4-byte aligned grad_scale", index);
     int rc = check_moment(t.m1, t.numel, index, "m1");
     if (rc) return rc;
     return check_moment(t.m2, t.numel, index, "m2");
@@ -576,6 +579,31 @@ std::vector<LaunchGroup> plan_launches(const aw4_tensor* ts, int32_t count) {
     return groups;
 }
 
+// The next staging slot with at least `bytes` of pinned host and device memory, once the
+// launch that last used it has completed.
+int acquire_slot(DeviceState* ds, size_t bytes, StagingSlot** out) {
+    StagingSlot& slot = ds->slots[ds->next];
+    ds->next = (ds->next + 1) % kSlots;
+    if (slot.pending) {
+        AW4_HIP_CHECK(hipEventSynchronize(slot.done));
+        slot.pending = false;
+    }
+    if (slot.cap < bytes) {
+        if (slot.host) AW4_HIP_CHECK(hipHostFree(slot.host));
+        if (slot.dev) AW4_HIP_CHECK(hipFree(slot.dev));
+        slot.host = slot.dev = nullptr;
+        slot.cap = 0;
+        size_t cap = 4096;
+        while (cap < bytes) cap *= 2;
+        AW4_HIP_CHECK(hipHostMalloc(&slot.host, cap, hipHostMallocDefault));
+        AW4_HIP_CHECK(hipMalloc(&slot.dev, cap));
+        slot.cap = cap;
+    }
+    if (!slot.done) AW4_HIP_CHECK(hipEventCreateWithFlags(&slot.done, hipEventDisableTiming));
+    *out = &slot;
+    return AW4_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -616,24 +644,10 @@ int aw4_fused_step(const aw4_tensor* tensors, int32_t count, void* stream) {
     DeviceState* ds = nullptr;
     int rc = device_state(&ds);
     if (rc) return rc;
-    StagingSlot& slot = ds->slots[ds->next];
-    ds->next = (ds->next + 1) % kSlots;
-    if (slot.pending) {
-        AW4_HIP_CHECK(hipEventSynchronize(slot.done));
-        slot.pending = false;
-    }
-    if (slot.cap < bytes) {
-        if (slot.host) AW4_HIP_CHECK(hipHostFree(slot.host));
-        if (slot.dev) AW4_HIP_CHECK(hipFree(slot.dev));
-        slot.host = slot.dev = nullptr;
-        slot.cap = 0;
-        size_t cap = 4096;
-        while (cap < bytes) cap *= 2;
-        AW4_HIP_CHECK(hipHostMalloc(&slot.host, cap, hipHostMallocDefault));
-        AW4_HIP_CHECK(hipMalloc(&slot.dev, cap));
-        slot.cap = cap;
-    }
-    if (!slot.done) AW4_HIP_CHECK(hipEventCreateWithFlags(&slot.done, hipEventDisableTiming));
+    StagingSlot* sp = nullptr;
+    rc = acquire_slot(ds, bytes, &sp);
+    if (rc) return rc;
+    StagingSlot& slot = *sp;
 
     // A few tiles per wave and a grid covering all of them: the hardware dispatcher hands
     // each free slot the next workgroup, so the tiles in flight stay a narrow, moving window
@@ -723,6 +737,73 @@ int aw4_dequantize(const aw4_moment* m, int64_t numel, float* out, void* stream)
     hipLaunchKernelGGL(dequantize_kernel, dim3((unsigned)groups), dim3(kThreads), 0, (hipStream_t)stream, *m, numel,
                        out, (const Tables*)ds->tables);
     AW4_HIP_CHECK(hipGetLastError());
+    return AW4_OK;
+}
+
+int aw4_clip_coefficient(const aw4_tensor* tensors, int32_t count, float max_norm, float* norm_out,
+                         float* coef_out, void* stream) {
+    g_error.clear();
+    if (count <= 0 || !tensors || !norm_out || !coef_out)
+        return set_error(AW4_EINVAL, "aw4_clip_coefficient: bad arguments");
+    if (!aligned((uint64_t)norm_out, 4) || !aligned((uint64_t)coef_out, 4))
+        return set_error(AW4_EALIGN, "aw4_clip_coefficient: outputs not 4-byte aligned");
+    int result_dtype = tensors[0].grad_dtype;
+    int64_t segments = 0;
+    for (int i = 0; i < count; ++i) {
+        const aw4_tensor& t = tensors[i];
+        if (!t.grad || t.numel <= 0) return set_error(AW4_EINVAL, "tensor %d: null grad or numel %lld", i,
+                                                      (long long)t.numel);
+        if (t.grad_dtype != AW4_F32 && t.grad_dtype != AW4_BF16 && t.grad_dtype != AW4_F16)
+            return set_error(AW4_EINVAL, "tensor %d: grad dtype %d", i, t.grad_dtype);
+        if ((t.flags & AW4_TENSOR_VEC_ALIGNED) && !aligned(t.grad, t.grad_dtype == AW4_F32 ? 16 : 8))
+            return set_error(AW4_EALIGN, "tensor %d: VEC_ALIGNED but grad misaligned", i);
+        if (t.grad_dtype != result_dtype) result_dtype = AW4_F32;  // torch.stack promotes mixed dtypes
+        segments += (t.numel + kNormSegment - 1) / kNormSegment;
+    }
+    if (segments > 0x7fffffff) return set_error(AW4_EINVAL, "aw4_clip_coefficient: too many segments");
+    // staging: header, rows, segment starts (copied), then the partial sums and the per-gradient
+    // squared norms (device only)
+    const size_t table = (sizeof(NormHeader) + sizeof(aw4_tensor) * count + sizeof(int64_t) * (count + 1) + 255) &
+                         ~(size_t)255;
+    const size_t bytes = table + sizeof(double) * ((size_t)segments + (size_t)count);
+
+    std::lock_guard<std::mutex> lock(g_mutex);
+    DeviceState* ds = nullptr;
+    int rc = device_state(&ds);
+    if (rc) return rc;
+    StagingSlot* slot = nullptr;
+    rc = acquire_slot(ds, bytes, &slot);
+    if (rc) return rc;
+    NormHeader* h = (NormHeader*)slot->host;
+    memset(h, 0, sizeof(*h));
+    aw4_tensor* rows = (aw4_tensor*)(h + 1);
+    int64_t* starts = (int64_t*)(rows + count);
+    int64_t acc = 0;
+    for (int i = 0; i < count; ++i) {
+        rows[i] = tensors[i];
+        starts[i] = acc;
+        acc += (tensors[i].numel + kNormSegment - 1) / kNormSegment;
+    }
+    starts[count] = acc;
+    h->count = count;
+    h->result_dtype = result_dtype;
+    h->max_norm = max_norm;
+    h->total_segments = segments;
+    h->partials = (uint64_t)slot->dev + table;
+    h->norm_sq = h->partials + sizeof(double) * (uint64_t)segments;
+    h->norm_out = (uint64_t)norm_out;
+    h->coef_out = (uint64_t)coef_out;
+    hipStream_t s = (hipStream_t)stream;
+    AW4_HIP_CHECK(hipMemcpyAsync(slot->dev, slot->host, table, hipMemcpyHostToDevice, s));
+    const NormHeader* dh = (const NormHeader*)slot->dev;
+    hipLaunchKernelGGL(norm_partials_kernel, dim3((unsigned)segments), dim3(kNormThreads), 0, s, dh);
+    AW4_HIP_CHECK(hipGetLastError());
+    hipLaunchKernelGGL(norm_tensor_kernel, dim3((unsigned)count), dim3(64), 0, s, dh);
+    AW4_HIP_CHECK(hipGetLastError());
+    hipLaunchKernelGGL(norm_finish_kernel, dim3(1), dim3(kNormThreads), 0, s, dh);
+    AW4_HIP_CHECK(hipGetLastError());
+    AW4_HIP_CHECK(hipEventRecord(slot->done, s));
+    slot->pending = true;
     return AW4_OK;
 }
 

@@ -161,6 +161,9 @@ def main():
     ap.add_argument("--recipes", default="zeeden,zipsr")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--clip-grad-norm", type=float, default=None, metavar="MAX_NORM",
+                    help="clip the gradients to this global 2-norm before every step, fused into the step "
+                         "(QuantizedAdamW.clip_grad_norm_), and also time torch.nn.utils.clip_grad_norm_ + step")
     ap.add_argument("--copy-probe-gb", type=float, default=0.0,
                     help="also run plain device copies of this many GB (calibrates HBM byte counters)")
     args = ap.parse_args()
@@ -228,6 +231,9 @@ def main():
             else:
                 raise SystemExit(f"unknown recipe {r}")
     algo_bytes = {name: a for name, _, a in recipes}
+    grad_bytes = sum(p.grad.numel() * p.grad.element_size() for p in params)
+    if args.clip_grad_norm is not None:  # the fused clip adds one read of every gradient
+        algo_bytes = {name: a + grad_bytes for name, a in algo_bytes.items()}
     print(f"[bench] {args.config}: {len(shapes)} tensors, {total:,} values, "
           f"{ {k: round(v / 1e9, 2) for k, v in algo_bytes.items()} } GB algorithmic per launch",
           file=sys.stderr, flush=True)
@@ -236,23 +242,59 @@ def main():
           file=sys.stderr, flush=True)
 
     stream = torch.cuda.current_stream(device)
+    clip = args.clip_grad_norm
     for _ in range(args.warmup):
         for _, opt, _ in recipes:
+            if clip is not None:
+                opt.clip_grad_norm_(clip)
             opt.step()
     torch.cuda.synchronize()
 
     events = {name: [] for name, _, _ in recipes}
+    norm_events = []
     t0 = time.perf_counter()
     for _ in range(args.steps):
         for name, opt, _ in recipes:
-            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start, mid, stop = (torch.cuda.Event(enable_timing=True) for _ in range(3))
             start.record(stream)
+            if clip is not None:
+                opt.clip_grad_norm_(clip)
+            mid.record(stream)
             opt.step()
             stop.record(stream)
             events[name].append((start, stop))
+            norm_events.append((start, mid))
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     launch_ms = {name: [a.elapsed_time(b) for a, b in ev] for name, ev in events.items()}
+    prologue = None
+    if clip is not None:
+        # The unfused path a trainer runs: torch's clip (norm pass + in-place multiply) then step.
+        norm_ms = statistics.mean(a.elapsed_time(b) for a, b in norm_events)
+        unfused = {}
+        for name, opt, _ in recipes:
+            for _ in range(args.warmup):
+                torch.nn.utils.clip_grad_norm_(params, clip)
+                opt.step()
+            ev = []
+            for _ in range(args.steps):
+                start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                start.record(stream)
+                torch.nn.utils.clip_grad_norm_(params, clip)
+                opt.step()
+                stop.record(stream)
+                ev.append((start, stop))
+            torch.cuda.synchronize()
+            unfused[name] = statistics.mean(a.elapsed_time(b) for a, b in ev)
+        prologue = {
+            "max_grad_norm": clip,
+            "fused_clip_and_step_ms": {k: round(statistics.mean(v), 4) for k, v in launch_ms.items()},
+            "torch_clip_then_step_ms": {k: round(v, 4) for k, v in unfused.items()},
+            "norm_pass_ms": round(norm_ms, 4),
+            "norm_pass_gb": round(grad_bytes / 1e9, 3),
+            "norm_pass_gb_s": round(grad_bytes / (norm_ms * 1e-3) / 1e9, 1),
+        }
+        print(f"[bench] clip prologue: {prologue}", file=sys.stderr, flush=True)
     per_recipe = {name: statistics.mean(v) for name, v in launch_ms.items()}
     # The dominant kernel is the recipe with the longest launches; its roofline is reported.
     dominant = max(per_recipe, key=per_recipe.get)
@@ -288,13 +330,15 @@ def main():
                          "tenth tensor an fp32-m2 / EDEN-m2 ablation, one optimizer step per timed step"
                          if mixed else
                          f"{args.config} fp32 parameter set, one {' + one '.join(n for n, _, _ in recipes)} step "
-                         f"per timed step ({len(recipes)} fused launches)"),
+                         f"per timed step ({len(recipes)} fused launches)")
+                        + (f", each after a fused gradient clip to norm {clip}" if clip is not None else ""),
             "tensors": len(shapes), "values": total, "recipes": [n for n, _, _ in recipes],
             "launch_ms": {k: round(v, 4) for k, v in per_recipe.items()},
             "gelem_s_per_recipe": {k: round(total / (v * 1e-3) / 1e9, 2) for k, v in per_recipe.items()},
             "hbm_frac_per_recipe": {k: round(algo_bytes[k] / (v * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
                                     for k, v in per_recipe.items()},
             "algorithmic_gb_per_launch": {k: round(v / 1e9, 4) for k, v in algo_bytes.items()},
+            **({"prologue": prologue} if prologue else {}),
         },
         "roofline": {
             "bound": "hbm",

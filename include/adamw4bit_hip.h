@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define AW4_ABI_VERSION 3
+#define AW4_ABI_VERSION 4
 #define AW4_BLOCK 128 /* values per block scale (quantization.py:694-703, 4-bit default) */
 
 /* Error codes. */
@@ -95,6 +95,10 @@ extern "C" {
 #define AW4_TENSOR_LERP1_LARGE 0x1 /* lerp weight 1-beta1 >= 0.5: m1 = fma(w-1, g-m1, g) */
 #define AW4_TENSOR_LERP2_LARGE 0x2 /* same for m2 with g*g */
 #define AW4_TENSOR_VEC_ALIGNED 0x4 /* param and grad allow 4-element vector access */
+/* Every gradient value g is read as grad_dtype(fp32(g * c)), c = the fp32 at device address
+ * `grad_scale` (the gradient clipping of torch.nn.utils.clip_grad_norm_, whose
+ * _foreach_mul_ rounds each product to the gradient's dtype; see aw4_clip_coefficient) */
+#define AW4_TENSOR_GRAD_SCALE 0x8
 
 /*
  * One moment (m1 or m2) of one parameter.  For a quantized moment, `codes`
@@ -136,6 +140,7 @@ typedef struct aw4_moment {
 typedef struct aw4_tensor {
     uint64_t param;      /* device address, contiguous, param_dtype[numel]; updated in place */
     uint64_t grad;       /* device address, contiguous, grad_dtype[numel] */
+    uint64_t grad_scale; /* device address of one float (AW4_TENSOR_GRAD_SCALE) or 0 */
     int64_t numel;
     int32_t param_dtype; /* AW4_F32 / AW4_BF16 / AW4_F16 */
     int32_t grad_dtype;
@@ -143,7 +148,7 @@ typedef struct aw4_tensor {
     float w1, w2, decay, step_coef, bc2_sqrt, bc2_sqrt_rcp, eps;
     aw4_moment m1;
     aw4_moment m2;
-} aw4_tensor; /* 272 bytes */
+} aw4_tensor; /* 280 bytes */
 
 /* Library ABI version (AW4_ABI_VERSION of the build). */
 int aw4_abi_version(void);
@@ -188,6 +193,26 @@ int aw4_dequantize(const aw4_moment* m, int64_t numel, float* out, void* stream)
  * reproduce.
  */
 int aw4_uniforms(uint64_t seed, uint64_t offset, int64_t n, float* out, void* stream);
+
+/*
+ * The global gradient clipping that precedes step() in the reference's training
+ * examples (an HF Trainer with max_grad_norm=1.0, examples/train_gpt_small.py:214),
+ * i.e. torch.nn.utils.clip_grad_norm_(params, max_norm) (norm type 2), computed on
+ * device in one pass over the gradients of `count` rows (grad, grad_dtype, numel and
+ * AW4_TENSOR_VEC_ALIGNED are read; every other field is ignored):
+ *   norm_t = ||grad_t||_2 rounded to grad_t's dtype (torch._foreach_norm),
+ *   total  = sqrt(sum_t norm_t^2) rounded to R, the promotion of all gradient dtypes,
+ *   coef   = min(RN(RN(1 / RN(total + 1e-6)) * max_norm), 1), each op rounded to R
+ *            (clip_grad.py: max_norm / (total_norm + 1e-6) is reciprocal then multiply).
+ * Sums of squares are taken in float64 in a fixed order (the result does not depend on
+ * the launch shape).  Writes the fp32 values of total to norm_out[0] and of coef to
+ * coef_out[0] (device addresses) without a host synchronisation.  Pass coef_out as the
+ * rows' grad_scale (AW4_TENSOR_GRAD_SCALE) of the next aw4_fused_step: the step then
+ * reads the clipped gradients the in-place _foreach_mul_ would have written, and the
+ * gradients themselves stay unscaled in memory (no extra pass over them).
+ */
+int aw4_clip_coefficient(const aw4_tensor* tensors, int32_t count, float max_norm, float* norm_out,
+                         float* coef_out, void* stream);
 
 /*
  * Host-only: copy the encode lookup tables the kernels use into `out`

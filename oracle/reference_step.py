@@ -234,6 +234,47 @@ def encode_lookahead(z_prev: torch.Tensor, grad: torch.Tensor, *, beta2: float, 
     return codes.reshape(-1), s, samples.reshape(-1)
 
 
+def clip_grad_norm(grads: List[torch.Tensor], max_norm: float) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The gradient clipping the reference's trainer runs before each step (an HF Trainer with
+    ``max_grad_norm``, examples/train_gpt_small.py:214): ``torch.nn.utils.clip_grad_norm_``
+    (norm type 2) on CPU copies.  Returns (total norm, clip coefficient), both in the promoted
+    gradient dtype, as torch computes them (clip_grad.py: per-tensor ``_foreach_norm``, the norm
+    of the stacked norms, ``max_norm / (total + 1e-6)`` clamped at 1)."""
+    params = []
+    for g in grads:
+        p = torch.nn.Parameter(torch.empty(g.shape, dtype=g.dtype))
+        p.grad = g.detach().clone()
+        params.append(p)
+    total = torch.nn.utils.clip_grad_norm_(params, max_norm)
+    return total, torch.clamp(max_norm / (total + 1e-6), max=1.0)
+
+
+def clip_grad_norm_f64(grads: List[torch.Tensor], max_norm: float) -> Tuple[torch.Tensor, torch.Tensor]:
+    """``clip_grad_norm`` with float64 sums of squares in place of torch's fp32 accumulation and
+    torch's rounding points otherwise: norm_t = grad_dtype(fp32(sqrt(sum g^2))), total =
+    R(fp32(sqrt(sum norm_t^2))) with R the promoted dtype, and the coefficient computed by torch's
+    own operations on that total."""
+    dtype = grads[0].dtype
+    for g in grads[1:]:
+        if g.dtype != dtype:
+            dtype = torch.float32
+    sq = 0.0
+    for g in grads:
+        n = math.sqrt(float(g.detach().to(torch.float64).square().sum()))
+        n = float(torch.tensor(n, dtype=torch.float64).to(torch.float32).to(g.dtype))
+        sq += n * n
+    total = torch.tensor(math.sqrt(sq), dtype=torch.float64).to(torch.float32).to(dtype)
+    return total, torch.clamp(max_norm / (total + 1e-6), max=1.0)
+
+
+def scale_grads(grads: List[torch.Tensor], coef: torch.Tensor) -> List[torch.Tensor]:
+    """The in-place ``_foreach_mul_`` of the clipping, on copies: each gradient becomes
+    grad_dtype(fp32(g * coef))."""
+    out = [g.detach().clone() for g in grads]
+    torch._foreach_mul_(out, coef)
+    return out
+
+
 def pack(codes: torch.Tensor) -> torch.Tensor:
     out = codes[0::2].clone()
     out[: codes.numel() // 2] |= codes[1::2] << 4

@@ -44,6 +44,8 @@ def test_error_path_reports_message():
     table = np.zeros(1, dtype=_lib.TENSOR)  # null pointers
     with pytest.raises(_lib.HipLibraryError, match="null param"):
         _lib.fused_step(table, 0)
+    with pytest.raises(_lib.HipLibraryError, match="null grad"):
+        _lib.clip_coefficient(table, 1.0, 64, 64, 0)
 
 
 def test_struct_layout_matches_header():
@@ -58,7 +60,7 @@ int main(void) {
   P(aw4_moment, rng_seed) P(aw4_moment, rng_offset) P(aw4_moment, codebook) P(aw4_moment, rounding)
   P(aw4_moment, flags) P(aw4_moment, sr_bias) P(aw4_moment, sr_bias_rcp) P(aw4_moment, sr_eps)
   P(aw4_moment, la_beta2) P(aw4_moment, la_fresh_weight) P(aw4_moment, la_bias) P(aw4_moment, la_eps)
-  P(aw4_tensor, param) P(aw4_tensor, grad) P(aw4_tensor, numel) P(aw4_tensor, param_dtype)
+  P(aw4_tensor, param) P(aw4_tensor, grad) P(aw4_tensor, grad_scale) P(aw4_tensor, numel) P(aw4_tensor, param_dtype)
   P(aw4_tensor, grad_dtype) P(aw4_tensor, flags) P(aw4_tensor, w1) P(aw4_tensor, w2) P(aw4_tensor, decay)
   P(aw4_tensor, step_coef) P(aw4_tensor, bc2_sqrt) P(aw4_tensor, bc2_sqrt_rcp) P(aw4_tensor, eps)
   P(aw4_tensor, m1) P(aw4_tensor, m2)
@@ -92,7 +94,8 @@ def test_header_constants_match_python():
     assert val["AW4_LUT_EXP0"] == _lib.LUT_EXP0 and val["AW4_BLOCK"] == _lib.BLOCK
     for name in ("MOMENT_ZERO_FLOOR", "MOMENT_EDEN", "MOMENT_GUARDS", "MOMENT_EXT_DRAWS", "MOMENT_SAMPLED_READ",
                  "MOMENT_READ_RAW_SCALE", "MOMENT_FRESH_PROXY", "MOMENT_PENDING", "ROUND_LOOKAHEAD_SR",
-                 "TENSOR_LERP1_LARGE", "TENSOR_LERP2_LARGE", "TENSOR_VEC_ALIGNED", "F32", "BF16", "F16"):
+                 "TENSOR_LERP1_LARGE", "TENSOR_LERP2_LARGE", "TENSOR_VEC_ALIGNED", "TENSOR_GRAD_SCALE", "F32", "BF16",
+                 "F16"):
         assert val[f"AW4_{name}"] == getattr(_lib, name), name
 
 
@@ -239,7 +242,13 @@ def test_torch_custom_op_schema_and_argument_checks():
     assert schema.startswith("adamw4bit_hip::fused_step_(Tensor(a0!)[] params, Tensor(a1!)[] states, "
                              "Tensor[] inputs, Tensor table)")
     op([], [], [], torch.zeros(0, dtype=torch.uint8))  # nothing to launch
+    row = _lib.TENSOR.itemsize
     with pytest.raises(ValueError, match="CPU uint8 tensor"):
-        op([torch.zeros(4)], [], [], torch.zeros(272, dtype=torch.float32))
+        op([torch.zeros(4)], [], [], torch.zeros(row, dtype=torch.float32))
     with pytest.raises(ValueError, match="HIP devices only"):
-        op([torch.zeros(4)], [], [], torch.zeros(272, dtype=torch.uint8))
+        op([torch.zeros(4)], [], [], torch.zeros(row, dtype=torch.uint8))
+    clip = torch.ops.adamw4bit_hip.clip_coefficient_
+    assert str(clip.default._schema).startswith(
+        "adamw4bit_hip::clip_coefficient_(Tensor[] grads, Tensor(a1!) out, Tensor table, float max_norm)")
+    with pytest.raises(ValueError, match="HIP device"):
+        clip([torch.zeros(4)], torch.zeros(2), torch.zeros(row, dtype=torch.uint8), 1.0)

@@ -325,19 +325,21 @@ def test_sampled_read_schemes_match_oracle(dtype):
         assert got.shape[0] == p.numel() and "m2" not in opt.state[p]
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_lookahead_schemes_match_oracle(dtype):
+@pytest.mark.parametrize("dtype,betas", [(torch.float32, (0.9, 0.95)), (torch.bfloat16, (0.9, 0.95)),
+                                         (torch.float32, (0.3, 0.45))])
+def test_lookahead_schemes_match_oracle(dtype, betas):
     """Lookahead update-SR m2 (reference step, adamw.py:566-614): the pending form samples its fp32
     state before the update, the proxies store codes sampled for the next step; float64
     probabilities, on-device Philox replayed into the oracle.  Codes, scales and the pending
-    state bit-exact (no parted values)."""
-    log(f"lookahead schemes {dtype} x 4 steps")
+    state bit-exact (no parted values).  Betas at most 0.5 take ATen's other lerp form (the
+    row's LERP flags)."""
+    log(f"lookahead schemes {dtype} betas {betas} x 4 steps")
     spec = [("nf4", "dyn4_la_upd_sr"), ("fp32", "dyn4_proxy_la_upd_sr"), ("nf4", "dyn4_vproxy_la_upd_sr"),
             ("fp32", "dyn4_la_upd_sr"), ("nf4", "dyn4_nz")]
 
     def make(ps):
         groups = [dict(params=[p], m1_quant_scheme=a, m2_quant_scheme=b) for p, (a, b) in zip(ps, spec)]
-        return aw.QuantizedAdamW(groups, lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True,
+        return aw.QuantizedAdamW(groups, lr=1e-3, betas=betas, eps=1e-8, weight_decay=0.1, optimized=True,
                                  quant_rng_seed=5, m1_quant_scheme="nf4", m2_quant_scheme="dyn4_nz")
     out = run_pair(make, [(512, 1024), (256, 512), (384, 128), (1024, 256), (128, 256)], dtype, 4, seed=5,
                    zero_block_frac=0.02)
@@ -348,6 +350,63 @@ def test_lookahead_schemes_match_oracle(dtype):
         st = opt.state[p]
         assert ("lookahead_pending_exp_avg_sq" in st) == (m2 == "dyn4_la_upd_sr")
         assert "m2_read_preconditioner" not in st
+
+
+@pytest.mark.parametrize("kind", ["f32", "bf16", "mixed"])
+def test_fused_clip_matches_torch_clip(kind):
+    """clip_grad_norm_ fused into the step (examples/train_gpt_small.py:214's max_grad_norm): the
+    total norm agrees with torch.nn.utils.clip_grad_norm_ on the CPU (float64 sums here, torch's own
+    order there), the coefficient is torch's arithmetic on that norm bit for bit, and the step
+    reads the gradients torch's in-place multiply would leave (oracle fed the same scaled
+    gradients; bit-exact states, parameters within the usual tolerance).  Three steps: the first
+    runs the full path, the next ones the cached launch plan; max_norm alternates between clipping
+    and not (coefficient 1)."""
+    log(f"fused clip {kind} x 3 steps")
+    shapes = [(256, 512), (1000,), (4097,), (384, 128), (3, 5)]
+    dtypes = {"f32": [torch.float32] * 5, "bf16": [torch.bfloat16] * 5,
+              "mixed": [torch.bfloat16, torch.float32, torch.bfloat16, torch.bfloat16, torch.float32]}[kind]
+    gen = torch.Generator().manual_seed(21)
+    init = [(torch.randn(s, generator=gen) * 0.02).to(dt) for s, dt in zip(shapes, dtypes)]
+    params = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
+    opt = aw.ZIPSRAdamW4Bit(params, lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True,
+                            quant_rng_seed=4)
+    cpu_params = [t.clone() for t in init]
+    oracle = ref.Oracle(cpu_params, ref.Hyper(1e-3, (0.9, 0.95), 1e-8, 0.1), ["nf4"] * 5,
+                        ["dyn4_upd_sr_fp32read"] * 5, [False] * 5, seed=4, draw_fn=H.PhiloxMirror(opt, H.DEVICE))
+    parted = [torch.zeros(p.numel(), dtype=torch.bool) for p in params]
+    for step, max_norm in enumerate((1e-3, 1e3, 2e-3)):
+        grads = [H.heavy_tailed(s, gen).to(dt) for s, dt in zip(shapes, dtypes)]
+        for p, g in zip(params, grads):
+            p.grad = g.to(H.DEVICE)
+        total = opt.clip_grad_norm_(max_norm)
+        coef = opt._grad_clip[1].cpu().reshape(())
+        with pytest.raises(RuntimeError, match="already pending"):
+            opt.clip_grad_norm_(max_norm)
+        expect_total, _ = ref.clip_grad_norm_f64(grads, max_norm)
+        torch_total, _ = ref.clip_grad_norm(grads, max_norm)
+        assert total.dtype == expect_total.dtype == torch_total.dtype and total.shape == ()
+        # the float64 restatement: equal up to one ulp of the result dtype (the order of the
+        # float64 sums differs); torch's own CPU clip: within its fp32 accumulation error
+        ulp = H.ULP16.get(total.dtype, 2.0 ** -23)
+        got, want, tt = float(total), float(expect_total), float(torch_total)
+        assert abs(got - want) <= ulp * abs(want), (got, want)
+        assert abs(got - tt) <= max(2e-5, 2 * ulp) * abs(tt), (got, tt)
+        # torch's coefficient arithmetic on this norm, in its dtype
+        t_cpu = total.cpu()
+        assert torch.equal(coef.to(t_cpu.dtype), torch.clamp(max_norm / (t_cpu + 1e-6), max=1.0)), (float(coef), step)
+        assert (float(coef) < 1.0) == (step != 1)
+        opt.step()
+        assert opt._grad_clip is None
+        for g, pg in zip(grads, (p.grad.cpu() for p in params)):
+            assert torch.equal(H.bits(g), H.bits(pg))  # the gradients stay unscaled in memory
+        oracle.step(ref.scale_grads(grads, coef.to(t_cpu.dtype)))
+        for i, p in enumerate(params):
+            st = H.state_of(opt, p)
+            ms = oracle.states[i].m2
+            if ref.is_stochastic(ms.scheme) and "m2_code" in st:
+                parted[i] |= H.code_diff_mask(st["m2_code"], ms.codes, p.numel())
+    torch.cuda.synchronize()
+    compare_pair(opt, params, oracle, cpu_params, parted, f"clip {kind}", steps=3)
 
 
 def test_zipsr_4096x4096_matches_oracle():

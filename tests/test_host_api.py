@@ -97,3 +97,15 @@ def test_lookahead_state_layout(scheme):
     assert SCHEMES[scheme][0] == q.CB_DYN4 and SCHEMES[scheme][1] == q.ROUND_LOOKAHEAD_SR
     if scheme not in PENDING_LOOKAHEAD_SCHEMES:
         assert initial_code_and_scale(scheme, False) == initial_code_and_scale("dyn4", False)
+
+
+def test_clip_grad_norm_host_checks():
+    # the fused clip covers the 2-norm of gradients on one HIP device (torch's other norms and CPU
+    # tensors raise); no gradients gives torch's tensor(0.)
+    opt = make()
+    assert float(opt.clip_grad_norm_(1.0)) == 0.0 and opt._grad_clip is None
+    opt.param_groups[0]["params"][0].grad = torch.ones(4096)
+    with pytest.raises(NotImplementedError, match="2-norm"):
+        opt.clip_grad_norm_(1.0, norm_type=float("inf"))
+    with pytest.raises(NotImplementedError, match="one HIP device"):
+        opt.clip_grad_norm_(1.0)

@@ -404,3 +404,38 @@ def test_lookahead_planted_mistakes_are_caught(monkeypatch):
         return original(*a, bias=1.0 - 0.95 ** (k - 1) if k > 1 else bias, **kw)
     monkeypatch.setattr(ref, "encode_lookahead", step_behind)
     assert not _all_params_match(small)
+
+
+# ---------------------------------------------------------------------------
+# Gradient clipping before the step (examples/train_gpt_small.py:214)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtypes", [[torch.float32] * 3, [torch.bfloat16] * 3, [torch.float16] * 3,
+                                    [torch.bfloat16, torch.float32, torch.float16]])
+def test_clip_restatement_matches_torch(dtypes):
+    # The float64 restatement the device follows against torch.nn.utils.clip_grad_norm_ itself:
+    # within torch's fp32 accumulation error (one storage ulp for 16-bit norms), and the same
+    # coefficient arithmetic bit for bit given the total.
+    gen = torch.Generator().manual_seed(8)
+    shapes = [(300, 700), (4097,), (5,)]
+    for scale in (1e-3, 1.0):
+        grads = [(torch.randn(s, generator=gen) * scale).to(dt) for s, dt in zip(shapes, dtypes)]
+        for max_norm in (1e-4, 1e4):
+            t64, c64 = ref.clip_grad_norm_f64(grads, max_norm)
+            tt, ct = ref.clip_grad_norm(grads, max_norm)
+            assert t64.dtype == tt.dtype
+            ulp = {torch.bfloat16: 2.0 ** -7, torch.float16: 2.0 ** -10}.get(tt.dtype, 0.0)
+            assert abs(float(t64) - float(tt)) <= max(2e-5, 2 * ulp) * float(tt)
+            assert torch.equal(c64, torch.clamp(max_norm / (t64 + 1e-6), max=1.0))
+            assert (float(c64) == 1.0) == (max_norm == 1e4)
+
+
+def test_clip_scaling_is_one_rounding_to_the_gradient_dtype():
+    # _foreach_mul_ by the coefficient: an fp32 product rounded once to the gradient's dtype
+    # (exact for two 16-bit operands), which the step reproduces in-register.
+    g = [torch.randn(1000).to(torch.bfloat16), torch.randn(1000)]
+    for coef in (torch.tensor(0.3, dtype=torch.bfloat16), torch.tensor(0.3)):
+        out = ref.scale_grads(g, coef)
+        for a, b in zip(out, g):
+            expect = (b.float() * coef.float()).to(b.dtype)
+            assert torch.equal(bits(a), bits(expect))
