@@ -352,7 +352,7 @@ def test_lookahead_schemes_match_oracle(dtype, betas):
         assert "m2_read_preconditioner" not in st
 
 
-@pytest.mark.parametrize("kind", ["f32", "bf16", "mixed"])
+@pytest.mark.parametrize("kind", ["f32", "bf16", "mixed", "research_f16"])
 def test_fused_clip_matches_torch_clip(kind):
     """clip_grad_norm_ fused into the step (examples/train_gpt_small.py:214's max_grad_norm): the
     total norm agrees with torch.nn.utils.clip_grad_norm_ on the CPU (float64 sums here, torch's own
@@ -363,16 +363,24 @@ def test_fused_clip_matches_torch_clip(kind):
     and not (coefficient 1)."""
     log(f"fused clip {kind} x 3 steps")
     shapes = [(256, 512), (1000,), (4097,), (384, 128), (3, 5)]
-    dtypes = {"f32": [torch.float32] * 5, "bf16": [torch.bfloat16] * 5,
+    dtypes = {"f32": [torch.float32] * 5, "bf16": [torch.bfloat16] * 5, "research_f16": [torch.float16] * 5,
               "mixed": [torch.bfloat16, torch.float32, torch.bfloat16, torch.bfloat16, torch.float32]}[kind]
+    # fp16 and the research m2 schemes run the generic kernels (lookahead: the gradients of
+    # tile_grads; read-back: the deferred update), the rest the specialised ZIP-SR kernels
+    schemes = ([("nf4", "dyn4_la_upd_sr"), ("fp32", "dyn4_proxy_la_upd_sr"), ("nf4", "dyn4_upd_sr"),
+                ("nf4", "dyn4_vproxy_la_upd_sr"), ("nf4", "dyn4_nz")] if kind == "research_f16"
+               else [("nf4", "dyn4_upd_sr_fp32read")] * 5)
+    if kind == "research_f16":
+        shapes = [(256, 512), (64, 128), (4097,), (384, 128), (3, 5)]
     gen = torch.Generator().manual_seed(21)
     init = [(torch.randn(s, generator=gen) * 0.02).to(dt) for s, dt in zip(shapes, dtypes)]
     params = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
-    opt = aw.ZIPSRAdamW4Bit(params, lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True,
-                            quant_rng_seed=4)
+    groups = [dict(params=[p], m1_quant_scheme=a, m2_quant_scheme=b) for p, (a, b) in zip(params, schemes)]
+    opt = aw.QuantizedAdamW(groups, lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True,
+                            quant_rng_seed=4, m1_quant_scheme="nf4", m2_quant_scheme="dyn4_nz")
     cpu_params = [t.clone() for t in init]
-    oracle = ref.Oracle(cpu_params, ref.Hyper(1e-3, (0.9, 0.95), 1e-8, 0.1), ["nf4"] * 5,
-                        ["dyn4_upd_sr_fp32read"] * 5, [False] * 5, seed=4, draw_fn=H.PhiloxMirror(opt, H.DEVICE))
+    oracle = ref.Oracle(cpu_params, ref.Hyper(1e-3, (0.9, 0.95), 1e-8, 0.1), [a for a, _ in schemes],
+                        [b for _, b in schemes], [False] * 5, seed=4, draw_fn=H.PhiloxMirror(opt, H.DEVICE))
     parted = [torch.zeros(p.numel(), dtype=torch.bool) for p in params]
     for step, max_norm in enumerate((1e-3, 1e3, 2e-3)):
         grads = [H.heavy_tailed(s, gen).to(dt) for s, dt in zip(shapes, dtypes)]
@@ -407,6 +415,41 @@ def test_fused_clip_matches_torch_clip(kind):
                 parted[i] |= H.code_diff_mask(st["m2_code"], ms.codes, p.numel())
     torch.cuda.synchronize()
     compare_pair(opt, params, oracle, cpu_params, parted, f"clip {kind}", steps=3)
+
+
+def test_tensor_beyond_2_31_values():
+    """One fp32 parameter of 2^31 + 4096 values (64-bit element, code and scale offsets): the 4096
+    values straddling element 2^31 are stepped exactly as a separate 4096-value parameter holding
+    them, fed the uniforms at the same Philox positions of the big tensor's streams (ZIP-SR, two
+    steps; bit-exact parameters, codes and scales).  Needs about 28 GB of device memory."""
+    n = (1 << 31) + 4096
+    lo, hi = (1 << 31) - 2048, (1 << 31) + 2048
+    log(f"ZIP-SR, one tensor of {n} values, window [{lo}, {hi})")
+    dev = torch.device(H.DEVICE)
+    gen = torch.Generator(device=dev).manual_seed(31)
+    big = torch.nn.Parameter(torch.randn(n, generator=gen, device=dev) * 0.02)
+    probe = torch.nn.Parameter(big.detach()[lo:hi].clone())
+    args = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True, quant_rng_seed=0)
+    opt_big, opt_probe = aw.ZIPSRAdamW4Bit([big], **args), aw.ZIPSRAdamW4Bit([probe], **args)
+    for step in range(2):
+        g = torch.randn(n, generator=gen, device=dev) * 1e-3
+        big.grad, probe.grad = g, g[lo:hi].clone()
+        opt_big.step()
+        # the m2 write is the step's last draw from the big tensor's m2 stream: n positions,
+        # rounded up to 128, ending at the stream's position now
+        stream = opt_big._stream("m2", big.device)  # streams are keyed by the parameter's device
+        seed, offset = stream.seed, stream.offset - (n + 127) // 128 * 128
+        opt_probe._draw_provider = lambda p, moment, k, d: H.uniforms_gpu(seed, offset + lo, k)
+        opt_probe.step()
+        torch.cuda.synchronize()
+        assert torch.equal(H.bits(big.detach()[lo:hi]), H.bits(probe.detach())), step
+        sb, sp = opt_big.state[big], opt_probe.state[probe]
+        for m in ("m1", "m2"):
+            assert torch.equal(sb[f"{m}_code"][lo // 2:hi // 2].cpu(), sp[f"{m}_code"].cpu()), (step, m)
+            assert torch.equal(H.bits(sb[f"{m}_quant_state"].absmax[lo // 128:hi // 128]),
+                               H.bits(sp[f"{m}_quant_state"].absmax)), (step, m)
+        del g
+    log("  window bit-exact over 2 steps")
 
 
 def test_zipsr_4096x4096_matches_oracle():
