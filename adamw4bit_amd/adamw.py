@@ -493,7 +493,8 @@ class QuantizedAdamW(Optimizer):
         ``_foreach_mul_`` would have stored -- instead of scaling the gradients in memory.  The
         gradients themselves are left unscaled.  Returns the total norm (a 0-dim tensor on the
         parameters' device, in the promoted gradient dtype), like torch.  Only the 2-norm of
-        parameters on one HIP device; one pending clip per step.
+        parameters on one HIP device; one pending clip per step (``zero_grad()`` drops a pending
+        clip whose step was skipped).
         """
         if float(norm_type) != 2.0:
             raise NotImplementedError("the fused clip computes the 2-norm only")
@@ -531,6 +532,12 @@ class QuantizedAdamW(Optimizer):
                 "set `error_if_nonfinite=False`")
         self._grad_clip = (device, out[1:])
         return total
+
+    def zero_grad(self, set_to_none: bool = True) -> None:
+        """``Optimizer.zero_grad``; also drops a pending gradient clip, whose gradients are gone
+        (a step skipped after the clip, as a GradScaler skips one on overflow, leaves it)."""
+        self._grad_clip = None
+        super().zero_grad(set_to_none=set_to_none)
 
     def _take_grad_clip(self, device: torch.device) -> Optional[torch.Tensor]:
         clip = self._grad_clip
