@@ -39,7 +39,15 @@ Pinning (see ``tests/test_oracle_*.py``): golden trajectories written by
 ``tests/golden/make_golden.py`` from the reference itself, the reference's
 known-answer tests (codebooks, nibble order, tie rule, scale floor, zero floor,
 first step equal to ``torch.optim.AdamW``), the EDEN invariant and brute force over
-all 16 levels on small blocks.
+all 16 levels on small blocks.  ``encode_lookahead`` and the lookahead flows: the
+reference's lookahead trajectories (one with gradients near 1e-8, where the bias
+correction matters), the next-step preconditioner's unbiasedness over a grid of draws
+against an independently written preconditioner, the flat-interval fallback's value
+unbiasedness and planted mistakes.  The gradient clipping that precedes a step:
+``clip_grad_norm`` is torch's own ``clip_grad_norm_`` on CPU copies;
+``clip_grad_norm_f64`` (float64 sums, torch's rounding points) is checked against it
+within torch's fp32 accumulation error, with the coefficient bit for bit, and
+``scale_grads`` against the single rounding of an fp32 product to the gradient dtype.
 """
 
 from __future__ import annotations
