@@ -48,6 +48,66 @@ def test_error_path_reports_message():
         _lib.clip_coefficient(table, 1.0, 64, 64, 0)
 
 
+def _row(**m2):
+    """A well-formed fp32 row with fake (aligned, never dereferenced) addresses: ZIP-SR-like m1
+    and the given m2 fields."""
+    t = np.zeros(1, dtype=_lib.TENSOR)
+    t["param"], t["grad"], t["numel"] = 1 << 20, 2 << 20, 4096
+    t["param_dtype"] = t["grad_dtype"] = _lib.F32
+    m1 = t["m1"]
+    m1["codes"], m1["scales"], m1["codebook"], m1["rounding"] = 3 << 20, 4 << 20, _lib.CB_NF4, _lib.ROUND_RTN
+    base = dict(codes=5 << 20, scales=6 << 20, codebook=_lib.CB_DYN4, rounding=_lib.ROUND_LOOKAHEAD_SR,
+                la_beta2=0.95, la_fresh_weight=0.05, la_bias=0.05, la_eps=1e-8)
+    base.update(m2)
+    for k, v in base.items():
+        t["m2"][k] = v
+    return t
+
+
+@pytest.mark.parametrize("m2,message", [
+    (dict(codebook=_lib.CB_LIN4), "dyn4 m2 only"),
+    (dict(flags=_lib.MOMENT_FRESH_PROXY | _lib.MOMENT_PENDING), "FRESH_PROXY and PENDING"),
+    (dict(flags=_lib.MOMENT_SAMPLED_READ), "read-back or EDEN"),
+    (dict(flags=_lib.MOMENT_EDEN), "read-back or EDEN"),
+    (dict(la_bias=0.0), "bias > 0"),
+    (dict(la_beta2=1.0), "beta2 in"),
+    (dict(flags=_lib.MOMENT_PENDING, values=0), "pending lookahead m2 without"),
+    (dict(flags=_lib.MOMENT_PENDING, values=(7 << 20) + 4), "pending lookahead m2 without"),
+    (dict(rounding=_lib.ROUND_UPDATE_SR, flags=_lib.MOMENT_PENDING, sr_bias=1.0), "lookahead flags without"),
+    (dict(rounding=5), "has rounding 5"),
+    (dict(rng_offset=100), "multiple of 128"),
+])
+def test_lookahead_rows_are_validated_on_the_host(m2, message):
+    # check_moment rejects malformed lookahead rows before any device work
+    with pytest.raises(_lib.HipLibraryError, match=message):
+        _lib.fused_step(_row(**m2), 0)
+
+
+def test_grad_scale_and_clip_arguments_are_validated_on_the_host():
+    t = _row()
+    t["flags"] = _lib.TENSOR_GRAD_SCALE  # without an address
+    with pytest.raises(_lib.HipLibraryError, match="GRAD_SCALE"):
+        _lib.fused_step(t, 0)
+    t["grad_scale"] = (8 << 20) + 2  # misaligned
+    with pytest.raises(_lib.HipLibraryError, match="GRAD_SCALE"):
+        _lib.fused_step(t, 0)
+    c = _row()
+    c["grad_dtype"] = 7
+    with pytest.raises(_lib.HipLibraryError, match="grad dtype"):
+        _lib.clip_coefficient(c, 1.0, 64, 128, 0)
+    c["grad_dtype"], c["flags"], c["grad"] = _lib.F32, _lib.TENSOR_VEC_ALIGNED, (2 << 20) + 4
+    with pytest.raises(_lib.HipLibraryError, match="VEC_ALIGNED"):
+        _lib.clip_coefficient(c, 1.0, 64, 128, 0)
+    with pytest.raises(_lib.HipLibraryError, match="4-byte aligned"):
+        _lib.clip_coefficient(_row(), 1.0, 66, 128, 0)
+    lib = _lib.library()
+    assert lib.aw4_clip_coefficient(None, 1, 1.0, 64, 128, None) == _lib.EINVAL
+    assert lib.aw4_clip_coefficient(_row().ctypes.data, 0, 1.0, 64, 128, None) == _lib.EINVAL
+    q = _row()["m2"].copy()
+    assert lib.aw4_quantize(1 << 20, 4096, q.ctypes.data, None) == _lib.EINVAL
+    assert b"lookahead" in lib.aw4_last_error()
+
+
 def test_struct_layout_matches_header():
     src = r"""
 #include <stddef.h>
