@@ -326,9 +326,10 @@ __device__ __forceinline__ BlockScales encode_block(const aw4_moment& M, const M
             } else {
                 // P(lo) = (f(x) - f(b)) / max(f(a) - f(b), 1e-30), 1 on invalid intervals
                 // (_compiled_quantization.py:74-109).  On a valid interval P is 0 at x == b, so
-                // x >= b picks hi with or without the guards; the guards add x <= a -> lo, which
-                // holds exactly when no level is below x (idx == 0), and let x >= b override an
-                // invalid interval.
+                // x >= b picks hi with or without the guards; the guards let x >= b override an
+                // invalid interval, and add x <= a -> lo, which holds exactly when no level is
+                // below x (idx == 0), where lo and hi are both code 0: that guard changes no code
+                // (nor the level EDEN reads) and is not evaluated.
                 UpdEntry ue[4];
                 bool dl[4];
 #pragma unroll
@@ -345,7 +346,7 @@ __device__ __forceinline__ BlockScales encode_block(const aw4_moment& M, const M
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
                     const bool valid = ue[t].den_u > 0.0f, at_b = x[t] >= b[t];
-                    lower[t] = guards ? (((!valid) | dl[t]) & !at_b) | (idx[t] == 0) : (!valid) | (dl[t] & !at_b);
+                    lower[t] = guards ? ((!valid) | dl[t]) & !at_b : (!valid) | (dl[t] & !at_b);
                 }
             }
 #pragma unroll
