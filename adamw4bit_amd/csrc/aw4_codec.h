@@ -281,8 +281,14 @@ __device__ __forceinline__ BlockScales encode_block(const aw4_moment& M, const M
 #pragma unroll
             for (int t = 0; t < 4; ++t) x[t] = div_by_rcp(mq[t], s, y);
         } else {
+            // torch.searchsorted orders NaN above every level.  A NaN x (only in blocks whose
+            // scale is not finite, which all take this path) becomes the positive quiet NaN, so
+            // the signed lookup, which reads the sign bit, puts it in the top bucket too.
 #pragma unroll
-            for (int t = 0; t < 4; ++t) x[t] = mq[t] / s;
+            for (int t = 0; t < 4; ++t) {
+                const float v = mq[t] / s;
+                x[t] = v != v ? __builtin_nanf("") : v;
+            }
         }
         uint32_t code[4];
         float lv[4];

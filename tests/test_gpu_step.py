@@ -424,6 +424,65 @@ def test_fused_clip_matches_torch_clip(kind):
     compare_pair(opt, params, oracle, cpu_params, parted, f"clip {kind}", steps=3)
 
 
+def _same_or_both_nan(a: torch.Tensor, b: torch.Tensor) -> bool:
+    a, b = a.detach().cpu().reshape(-1), b.detach().cpu().reshape(-1)
+    nan = torch.isnan(a.float())
+    return bool(torch.equal(nan, torch.isnan(b.float()))) and torch.equal(H.bits(a[~nan]), H.bits(b[~nan]))
+
+
+@pytest.mark.parametrize("recipe", ["zeeden", "zipsr"])
+def test_non_finite_gradients_match_oracle(recipe):
+    """NaN, +Inf and -Inf gradient values (in quantized tensors and an fp32-state tensor) follow
+    the reference: the NaN / Inf block scales, the codes of a block whose scale is not finite
+    (the kernel's IEEE forms), and the propagation into moments and parameters on the next
+    steps.  Codes, fp32 states and scales equal the oracle's (NaN == NaN); parameters have the
+    same NaNs and their finite values are within the usual tolerance."""
+    log(f"non-finite gradients, {recipe} x 3 steps")
+    shapes = [(64, 128), (4096,), (1000,)]
+    gen = torch.Generator().manual_seed(13)
+    init = [torch.randn(sh, generator=gen) * 0.02 for sh in shapes]
+    params = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
+    args = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True)
+    if recipe == "zeeden":
+        opt = aw.ZEEDENAdamW4Bit(params, **args)
+        m2, eden = "dyn4_nz", True
+    else:
+        opt = aw.ZIPSRAdamW4Bit(params, quant_rng_seed=6, **args)
+        m2, eden = "dyn4_upd_sr_fp32read", False
+    cpu = [t.clone() for t in init]
+    oracle = ref.Oracle(cpu, ref.Hyper(1e-3, (0.9, 0.95), 1e-8, 0.1), ["nf4"] * 3, [m2] * 3, [eden] * 3,
+                        seed=6 if recipe == "zipsr" else None, draw_fn=H.PhiloxMirror(opt, H.DEVICE))
+    for step in range(3):
+        grads = [H.heavy_tailed(sh, gen) for sh in shapes]
+        if step == 1:
+            g0 = grads[0].view(-1)
+            g0[3 * 128 + 5] = float("nan")      # one NaN in block 3
+            g0[7 * 128 + 100] = float("inf")    # +Inf in block 7
+            g0[9 * 128 + 1] = float("-inf")     # -Inf in block 9
+            grads[1][2 * 128 + 64] = float("inf")
+            grads[2][5] = float("nan")          # fp32-state tensor
+        for p, g in zip(params, grads):
+            p.grad = g.to(H.DEVICE)
+        opt.step()
+        oracle.step(grads)
+        torch.cuda.synchronize()
+        for i, p in enumerate(params):
+            st = H.state_of(opt, p)
+            ost = H.oracle_state((oracle.states[i].m1, oracle.states[i].m2))
+            for key, val in ost.items():
+                if key.endswith("_code"):
+                    assert torch.equal(st[key].cpu(), val), (recipe, step, i, key, H.code_mismatch(st[key], val))
+                else:
+                    assert _same_or_both_nan(st[key], val), (recipe, step, i, key)
+            # parameters: the same NaNs, and the finite values within the usual tolerance
+            got = p.detach().cpu().reshape(-1)
+            want = cpu[i].reshape(-1)
+            nan = torch.isnan(want)
+            assert torch.equal(torch.isnan(got), nan), (recipe, step, i)
+            H.assert_params_close(got[~nan], want[~nan], f"non-finite {recipe} step {step} p{i}", steps=step + 1)
+    assert any(bool(torch.isnan(p.detach()).any()) for p in params)  # the NaN reached the parameters
+
+
 def test_tensor_beyond_2_31_values():
     """One fp32 parameter of 2^31 + 4096 values (64-bit element, code and scale offsets): the 4096
     values straddling element 2^31 are stepped exactly as a separate 4096-value parameter holding
