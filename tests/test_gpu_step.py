@@ -430,7 +430,7 @@ def _same_or_both_nan(a: torch.Tensor, b: torch.Tensor) -> bool:
     return bool(torch.equal(nan, torch.isnan(b.float()))) and torch.equal(H.bits(a[~nan]), H.bits(b[~nan]))
 
 
-@pytest.mark.parametrize("recipe", ["zeeden", "zipsr"])
+@pytest.mark.parametrize("recipe", ["zeeden", "zipsr", "research"])
 def test_non_finite_gradients_match_oracle(recipe):
     """NaN, +Inf and -Inf gradient values (in quantized tensors and an fp32-state tensor) follow
     the reference: the NaN / Inf block scales, the codes of a block whose scale is not finite
@@ -443,15 +443,20 @@ def test_non_finite_gradients_match_oracle(recipe):
     init = [torch.randn(sh, generator=gen) * 0.02 for sh in shapes]
     params = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
     args = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True)
+    m1s = ["nf4"] * 3
     if recipe == "zeeden":
         opt = aw.ZEEDENAdamW4Bit(params, **args)
-        m2, eden = "dyn4_nz", True
-    else:
+        m2s, eden = ["dyn4_nz"] * 3, True
+    elif recipe == "zipsr":
         opt = aw.ZIPSRAdamW4Bit(params, quant_rng_seed=6, **args)
-        m2, eden = "dyn4_upd_sr_fp32read", False
+        m2s, eden = ["dyn4_upd_sr_fp32read"] * 3, False
+    else:  # the research kernel: lookahead (float64 probabilities) and read-back m2
+        m1s, m2s, eden = ["nf4", "fp32", "nf4"], ["dyn4_la_upd_sr", "dyn4_vproxy_la_upd_sr", "dyn4_upd_sr"], False
+        groups = [dict(params=[p], m1_quant_scheme=a, m2_quant_scheme=b) for p, a, b in zip(params, m1s, m2s)]
+        opt = aw.QuantizedAdamW(groups, quant_rng_seed=6, m1_quant_scheme="nf4", m2_quant_scheme="dyn4_nz", **args)
     cpu = [t.clone() for t in init]
-    oracle = ref.Oracle(cpu, ref.Hyper(1e-3, (0.9, 0.95), 1e-8, 0.1), ["nf4"] * 3, [m2] * 3, [eden] * 3,
-                        seed=6 if recipe == "zipsr" else None, draw_fn=H.PhiloxMirror(opt, H.DEVICE))
+    oracle = ref.Oracle(cpu, ref.Hyper(1e-3, (0.9, 0.95), 1e-8, 0.1), m1s, m2s, [eden] * 3,
+                        seed=None if recipe == "zeeden" else 6, draw_fn=H.PhiloxMirror(opt, H.DEVICE))
     for step in range(3):
         grads = [H.heavy_tailed(sh, gen) for sh in shapes]
         if step == 1:
