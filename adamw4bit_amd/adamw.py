@@ -133,6 +133,30 @@ def _vec_aligned(p: torch.Tensor, grad: torch.Tensor) -> bool:
     return p.data_ptr() % psize == 0 and grad.data_ptr() % gsize == 0
 
 
+def _launch(params: List[torch.Tensor], written: List[torch.Tensor], read: List[torch.Tensor],
+            table: np.ndarray) -> None:
+    """Launch one step's table on the parameters' device and current stream.
+
+    Under ``torch.compile`` the launch is the custom operator ``adamw4bit_hip::fused_step_``,
+    which declares the tensors it writes and reads.  In eager mode the operator's dispatch
+    (argument flattening and one version bump per tensor) costs about 5 us per tensor, so the
+    library is called directly and the version counters of everything written in place are
+    bumped in one call, as the operator would; ``read`` is referenced by the caller until the
+    call returns, and the kernels are ordered on the stream like any torch kernel."""
+    if torch.compiler.is_compiling():
+        _ops.fused_step_(params, written, read, torch.from_numpy(table.view(np.uint8)))
+        return
+    device = params[0].device
+    if device.type != "cuda":
+        raise ValueError("the fused 4-bit step runs on HIP devices only")
+    if torch.cuda.current_device() != device.index:
+        with torch.cuda.device(device):
+            _lib.fused_step(table, torch.cuda.current_stream(device).cuda_stream)
+    else:
+        _lib.fused_step(table, torch.cuda.current_stream(device).cuda_stream)
+    torch.autograd.graph.increment_version(params + written)
+
+
 def _moment_tensors(state: Dict[str, Any]) -> List[torch.Tensor]:
     """Writable moment buffers of one parameter (``_moment_buffer.py:22-41``)."""
     out = []
@@ -519,7 +543,12 @@ class QuantizedAdamW(Optimizer):
         table["grad_dtype"] = [_DTYPES[g.dtype] for g in grads]
         table["flags"] = [_lib.TENSOR_VEC_ALIGNED if g.data_ptr() % (4 * g.element_size()) == 0 else 0 for g in grads]
         out = torch.empty(2, dtype=torch.float32, device=device)  # [total norm, coefficient]
-        _ops.clip_coefficient_(grads, out, torch.from_numpy(table.view(np.uint8)), float(max_norm))
+        if torch.compiler.is_compiling():
+            _ops.clip_coefficient_(grads, out, torch.from_numpy(table.view(np.uint8)), float(max_norm))
+        else:  # the operator's dispatch over every gradient costs more than the call (see _launch)
+            with torch.cuda.device(device):
+                _lib.clip_coefficient(table, float(max_norm), out.data_ptr(), out.data_ptr() + 4,
+                                      torch.cuda.current_stream(device).cuda_stream)
         result_dtype = grads[0].dtype
         for g in grads[1:]:
             if g.dtype != result_dtype:
@@ -573,7 +602,7 @@ class QuantizedAdamW(Optimizer):
                 table["grad_scale"] = coef.data_ptr()
                 table["flags"] |= _lib.TENSOR_GRAD_SCALE
                 read = read + [coef]
-            _ops.fused_step_(params, written, read, torch.from_numpy(table.view(np.uint8)))
+            _launch(params, written, read, table)
         self._grad_clip = None
         self._launch_plan = _LaunchPlan.build(self, per_device, tables, info)
         return loss
@@ -807,15 +836,11 @@ class _LaunchPlan:
         self.groups: list = []     # (group, structure, parameter count)
         self.params: List[torch.Tensor] = []
         self.devices: list = []    # per device: table, params, written, rows
-
-    @classmethod
-    def _state_ids(cls, state) -> tuple:
-        ids = [id(state.get(k)) for k in cls._STATE_KEYS]
-        for k in ("m1_quant_state", "m2_quant_state"):
-            q = state.get(k)
-            ids.append(id(q.absmax) if isinstance(q, QuantState) else 0)
-        ids.append(state.get(_FALLBACK_KEY, False))
-        return tuple(ids)
+        # what the tables were built from, checked by identity each step: (param, state dict),
+        # (state dict, key, value) for every state key, (QuantState, its absmax tensor)
+        self.owners: list = []
+        self.state_refs: list = []
+        self.quant_refs: list = []
 
     @classmethod
     def build(cls, opt: "QuantizedAdamW", per_device, tables, info) -> Optional["_LaunchPlan"]:
@@ -853,7 +878,11 @@ class _LaunchPlan:
                 sr = tuple((moment, opt._stream(moment, p.device))
                            for moment, scheme in (("m1", schemes[0]), ("m2", schemes[1]))
                            if scheme != "fp32" and SCHEMES[scheme][1] in _SR_ROUNDINGS)
-                entries.append((p, state, cls._state_ids(state), group_of[id(p)], schemes[1], sr, p.numel()))
+                entries.append((p, state, None, group_of[id(p)], schemes[1], sr, p.numel()))
+                plan.owners.append((p, state))
+                plan.state_refs.extend((state, k, state.get(k)) for k in cls._STATE_KEYS + (_FALLBACK_KEY,))
+                plan.quant_refs.extend((q, q.absmax) for q in (state.get("m1_quant_state"), state.get("m2_quant_state"))
+                                       if isinstance(q, QuantState))
             table = tables[device]
             gbytes = np.array([p.numel() * p.element_size() for p in params], dtype=np.int64)
             pvec = np.array([p.data_ptr() % (4 * p.element_size()) == 0 for p in params], dtype=bool)
@@ -868,30 +897,34 @@ class _LaunchPlan:
             return None
         params = self.params
         i = 0
+        n = len(params)
+        strided = torch.strided
         for (group, structure, count), current in zip(self.groups, opt.param_groups):
             if current is not group or len(group["params"]) != count:
                 return None
             if tuple(group.get(k) for k in self._STRUCTURE_KEYS) != structure:
                 return None
             for p in group["params"]:
-                if p.grad is None:
+                g = p.grad
+                if g is None:
                     continue
-                if i >= len(params) or p is not params[i]:
+                if i >= n or p is not params[i] or g.layout != strided or not g.is_contiguous():
                     return None
                 i += 1
-        if i != len(params):
+        if i != n:
             return None
-        state_ids = self._state_ids
         state_map = opt.state
-        strided = torch.strided
+        for p, state in self.owners:
+            if state_map.get(p) is not state or type(state.get("step")) is not int:
+                return None
+        for state, key, value in self.state_refs:
+            if state.get(key) is not value:
+                return None
+        for q, absmax in self.quant_refs:
+            if q.absmax is not absmax:
+                return None
         out = []
         for table, dparams, written, entries, lo, hi, gbytes, pvec, gvec in self.devices:
-            for p, state, ids, _, _, _, _ in entries:
-                if state_map.get(p) is not state or type(state.get("step")) is not int or state_ids(state) != ids:
-                    return None
-                g = p.grad
-                if g.layout != strided or not g.is_contiguous():
-                    return None
             g0 = np.fromiter((p.grad.data_ptr() for p in dparams), dtype=np.int64, count=len(dparams))
             g1 = g0 + gbytes
             if bool(((lo < g1[:, None]) & (g0[:, None] < hi)).any()):
@@ -938,7 +971,7 @@ class _LaunchPlan:
             if coef is not None:
                 table["flags"] |= _lib.TENSOR_GRAD_SCALE
                 read.append(coef)
-            _ops.fused_step_(params, written, read, torch.from_numpy(table.view(np.uint8)))
+            _launch(params, written, read, table)
         return True
 
 
