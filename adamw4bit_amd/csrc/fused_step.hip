@@ -655,7 +655,7 @@ int aw4_fused_step(const aw4_tensor* tensors, int32_t count, void* stream) {
     // Measured on MI355X against persistent grids of contiguous per-wave ranges, which
     // stream from thousands of far-apart addresses at once and leave a load-imbalance tail.
     // The kernel picks which tiles a wave takes (consecutive ones, or one per grid-sized
-    // stride); either way the grid is ceil(tiles / kTilesPerWave) waves.
+    // stride); either way the grid is ceil(tiles / tiles per wave) waves.
     std::vector<int64_t> grid(plan.size());
     for (size_t g = 0; g < plan.size(); ++g) {
         const LaunchGroup& lg = plan[g];
@@ -671,14 +671,18 @@ int aw4_fused_step(const aw4_tensor* tensors, int32_t count, void* stream) {
             acc += (rows[k].numel + kWaveTile - 1) / kWaveTile;
         }
         starts[n] = acc;
-        const int64_t waves = (acc + kTilesPerWave - 1) / kTilesPerWave;
+        // Small launches take fewer tiles per wave so that their waves still spread over every
+        // CU: 4 tiles per wave from 16 tiles per CU (4 workgroups of 4 waves), down to 1.
+        const int64_t per_cu = acc / (int64_t)ds->num_cus;
+        const int tiles_per_wave = per_cu >= 16 ? kTilesPerWave : per_cu >= 8 ? 2 : 1;
+        const int64_t waves = (acc + tiles_per_wave - 1) / tiles_per_wave;
         grid[g] = (waves + kWavesPerGroup - 1) / kWavesPerGroup;
         if (grid[g] > 0x7fffffff)
             return set_error(AW4_EINVAL, "aw4_fused_step: %lld tiles exceed one launch", (long long)acc);
         h->count = n;
         h->cb1 = lg.cb1; h->lut1 = lg.lut1; h->cb2 = lg.cb2; h->lut2 = lg.lut2;
         h->total_tiles = acc;
-        h->tiles_per_wave = kTilesPerWave;
+        h->tiles_per_wave = tiles_per_wave;
     }
 
     hipStream_t s = (hipStream_t)stream;
