@@ -672,9 +672,10 @@ int aw4_fused_step(const aw4_tensor* tensors, int32_t count, void* stream) {
         }
         starts[n] = acc;
         // Small launches take fewer tiles per wave so that their waves still spread over every
-        // CU: 4 tiles per wave from 16 tiles per CU (4 workgroups of 4 waves), down to 1.
+        // CU: 4 tiles per wave from 128 tiles per CU, 2 from 8, else 1 (measured on one 4096^2
+        // and one 1024^2 tensor, and the GPT-2-small list).
         const int64_t per_cu = acc / (int64_t)ds->num_cus;
-        const int tiles_per_wave = per_cu >= 16 ? kTilesPerWave : per_cu >= 8 ? 2 : 1;
+        const int tiles_per_wave = per_cu >= 128 ? kTilesPerWave : per_cu >= 8 ? 2 : 1;
         const int64_t waves = (acc + tiles_per_wave - 1) / tiles_per_wave;
         grid[g] = (waves + kWavesPerGroup - 1) / kWavesPerGroup;
         if (grid[g] > 0x7fffffff)
