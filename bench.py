@@ -29,6 +29,12 @@ import time
 HBM_PEAK_GBS = 8000.0
 HERE = os.path.dirname(os.path.abspath(__file__))
 RECIPE_KERNELS = {"ZE-EDEN": "step_kernel<RTN, RTN, F32>", "ZIP-SR": "step_kernel<RTN, UPDATE_SR, F32>"}
+# --recipes names of the reference step's research m2 schemes -> (scheme, extra bytes per value)
+RESEARCH_M2 = {
+    "la": ("dyn4_la_upd_sr", 0.0), "proxy-la": ("dyn4_proxy_la_upd_sr", 0.0),
+    "vproxy-la": ("dyn4_vproxy_la_upd_sr", 0.0), "upd-sr": ("dyn4_upd_sr", 0.0),
+    "store-eden": ("dyn4_upd_sr_store_eden", 4.0),
+}
 
 
 def llama3_8b_shapes():
@@ -158,7 +164,8 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="llama3-8b", choices=sorted(CONFIGS))
-    ap.add_argument("--recipes", default="zeeden,zipsr")
+    ap.add_argument("--recipes", default="zeeden,zipsr",
+                    help="comma-separated: zeeden, zipsr, or a research m2 scheme: " + ", ".join(RESEARCH_M2))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--clip-grad-norm", type=float, default=None, metavar="MAX_NORM",
@@ -228,6 +235,16 @@ def main():
                 recipes.append(("ZE-EDEN", aw.ZEEDENAdamW4Bit(params, optimized=True), algo))
             elif r == "zipsr":
                 recipes.append(("ZIP-SR", aw.ZIPSRAdamW4Bit(params, optimized=True, quant_rng_seed=0), algo))
+            elif r in RESEARCH_M2:
+                # the reference step's research m2 schemes (one generic-kernel instance), NF4 m1
+                m2, extra = RESEARCH_M2[r]
+                opt = aw.QuantizedAdamW(params, m1_quant_scheme="nf4", m2_quant_scheme=m2, optimized=True,
+                                        quant_rng_seed=0)
+                # the pending lookahead m2 is fp32 state; store-EDEN also writes 1 / denominator
+                m2_kind = "fp32" if m2 == "dyn4_la_upd_sr" else "dyn4"
+                research = sum(n * (bytes_per_value(n, m2=m2_kind) + (extra if n >= 4096 and n % 128 == 0 else 0))
+                               for n in numels)
+                recipes.append((m2, opt, research))
             else:
                 raise SystemExit(f"unknown recipe {r}")
     algo_bytes = {name: a for name, _, a in recipes}
