@@ -42,6 +42,8 @@ constexpr int flags_of(int spec) { return spec >> 4; }
 constexpr int spec_flags_mask(int kind) {
     return kind == K_FP32 ? 0
          : kind == K_RTN ? AW4_MOMENT_EDEN
+         : kind == K_USR ? (AW4_MOMENT_EDEN | AW4_MOMENT_GUARDS | AW4_MOMENT_ZERO_FLOOR | AW4_MOMENT_SAMPLED_READ |
+                            AW4_MOMENT_READ_RAW_SCALE)
                          : (AW4_MOMENT_EDEN | AW4_MOMENT_GUARDS | AW4_MOMENT_ZERO_FLOOR);
 }
 

@@ -537,8 +537,11 @@ __device__ __forceinline__ bool values_only(const aw4_tensor& T) {
 // its loads early; a kernel bound by its arithmetic (update-SR) pays for the prefetched
 // registers and runs the plain order.  The generic kernel (run-time kinds and dtype) has
 // the register pressure of every variant at once and loads each tile when it starts it.
+// (Not for an m2 read back after its encode: the registers of a prefetched tile leave those
+// kernels at 2 waves per SIMD, 21% slower than 3 without the prefetch.)
 constexpr bool prefetch_next_tile(int m1k, int m2k, int d) {
-    return kind_of(m1k) != K_ANY && kind_of(m2k) != K_ANY && d != D_ANY;
+    return kind_of(m1k) != K_ANY && kind_of(m2k) != K_ANY && d != D_ANY &&
+           !(flags_of(m2k) & AW4_MOMENT_SAMPLED_READ);
 }
 constexpr bool tile_order_grid(int m1k, int m2k, int d) {
     return prefetch_next_tile(m1k, m2k, d) && kind_of(m2k) != K_USR;
@@ -632,9 +635,9 @@ __device__ __forceinline__ void run_tiles(const StepHeader* hdr, const LdsT& lds
                     else if (T.param_dtype == D_BF16)
                         sampled_read_update<D_BF16>(T, tl, L2, ws.block(tl.grp), bs, m1, p1);
                     else sampled_read_update<D_F16>(T, tl, L2, ws.block(tl.grp), bs, m1, p1);
-                } else {
+                } else if constexpr (kind_of(M2K) == K_ANY) {
                     // lookahead update-SR: sample the pending state before the update, or encode
-                    // the new m2 after it
+                    // the new m2 after it (the generic research instance only)
                     float g[16];
                     tile_grads(T, in, g);
                     const bool pending = (T.m2.flags & AW4_MOMENT_PENDING) != 0;

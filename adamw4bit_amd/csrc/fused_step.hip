@@ -151,8 +151,12 @@ constexpr int kRtn = mspec(K_RTN), kRtnEden = mspec(K_RTN, AW4_MOMENT_EDEN), kFp
 constexpr int kSsrGuarded = mspec(K_SSR, AW4_MOMENT_GUARDS);
 constexpr int kUsrGuarded = mspec(K_USR, AW4_MOMENT_GUARDS);
 constexpr int kUsrGuardedEden = mspec(K_USR, AW4_MOMENT_GUARDS | AW4_MOMENT_EDEN);
-// Any m2 kind, read back after its encode (dyn4_upd_sr / lin4_upd_sr / *_upd_sr_store_eden).
-constexpr int kAnyResearch = mspec(K_ANY, AW4_MOMENT_SAMPLED_READ);  // read-back and lookahead m2
+// The reference step's update-SR m2 read back after its encode: dyn4_upd_sr / lin4_upd_sr,
+// and *_upd_sr_store_eden (read at the scale before EDEN, EDEN on the stored scale).
+constexpr int kUsrRead = mspec(K_USR, AW4_MOMENT_SAMPLED_READ);
+constexpr int kUsrReadEden = mspec(K_USR, AW4_MOMENT_SAMPLED_READ | AW4_MOMENT_READ_RAW_SCALE | AW4_MOMENT_EDEN);
+// Any m2 kind of the research schemes (read-back and lookahead), any dtype.
+constexpr int kAnyResearch = mspec(K_ANY, AW4_MOMENT_SAMPLED_READ);
 struct KernelVariant {
     int m1, m2, dtype;
     const void* fn;
@@ -164,6 +168,7 @@ const KernelVariant kVariants[] = {
     AW4_VARIANT(kSsrGuarded, kUsrGuarded, D_F32), AW4_VARIANT(kSsrGuarded, kUsrGuarded, D_BF16),
     AW4_VARIANT(kRtn, kFp32, D_F32),              AW4_VARIANT(kRtn, kFp32, D_BF16),
     AW4_VARIANT(kRtn, kUsrGuardedEden, D_F32),    AW4_VARIANT(kRtn, kUsrGuardedEden, D_BF16),
+    AW4_VARIANT(kRtn, kUsrRead, D_F32),           AW4_VARIANT(kRtn, kUsrReadEden, D_F32),
     AW4_VARIANT(K_ANY, kAnyResearch, D_ANY),
     AW4_VARIANT(K_ANY, K_ANY, D_ANY),
 };
@@ -536,14 +541,17 @@ std::vector<LaunchGroup> plan_launches(const aw4_tensor* ts, int32_t count) {
             if (t.param_dtype != t.grad_dtype) generic.members.push_back(i); else values.push_back(i);
             continue;
         }
-        if (research_m2(t.m2)) { research.members.push_back(i); continue; }
-        if (t.param_dtype != t.grad_dtype) { generic.members.push_back(i); continue; }
+        const bool research_tensor = research_m2(t.m2);
         const int s1 = mspec(t.m1.rounding, t.m1.flags & spec_flags_mask(t.m1.rounding));
         const int s2 = mspec(t.m2.rounding, t.m2.flags & spec_flags_mask(t.m2.rounding));
         int v = kGenericVariant;
-        for (int k = 0; k < kNumSpecialised; ++k)
-            if (kVariants[k].dtype == t.param_dtype && kVariants[k].m1 == s1 && kVariants[k].m2 == s2) { v = k; break; }
-        if (v == kGenericVariant) { generic.members.push_back(i); continue; }
+        if (t.param_dtype == t.grad_dtype)
+            for (int k = 0; k < kNumSpecialised; ++k)
+                if (kVariants[k].dtype == t.param_dtype && kVariants[k].m1 == s1 && kVariants[k].m2 == s2) {
+                    v = k;
+                    break;
+                }
+        if (v == kGenericVariant) { (research_tensor ? research : generic).members.push_back(i); continue; }
         const bool f1 = t.m1.rounding == AW4_ROUND_FP32, f2 = t.m2.rounding == AW4_ROUND_FP32;
         const int c1 = f1 ? -1 : t.m1.codebook, c2 = f2 ? -1 : t.m2.codebook;
         const int l1 = f1 ? -1 : lut_id_of(t.m1.rounding, c1, t.m1.flags);
