@@ -44,6 +44,7 @@ constexpr int spec_flags_mask(int kind) {
          : kind == K_RTN ? AW4_MOMENT_EDEN
          : kind == K_USR ? (AW4_MOMENT_EDEN | AW4_MOMENT_GUARDS | AW4_MOMENT_ZERO_FLOOR | AW4_MOMENT_SAMPLED_READ |
                             AW4_MOMENT_READ_RAW_SCALE)
+         : kind == K_LA  ? AW4_MOMENT_PENDING  // a pending lookahead m2 keeps fp32 values, no codes
                          : (AW4_MOMENT_EDEN | AW4_MOMENT_GUARDS | AW4_MOMENT_ZERO_FLOOR);
 }
 

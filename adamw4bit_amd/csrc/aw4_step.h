@@ -537,19 +537,20 @@ __device__ __forceinline__ bool values_only(const aw4_tensor& T) {
 // its loads early; a kernel bound by its arithmetic (update-SR) pays for the prefetched
 // registers and runs the plain order.  The generic kernel (run-time kinds and dtype) has
 // the register pressure of every variant at once and loads each tile when it starts it.
-// (Not for an m2 read back after its encode: the registers of a prefetched tile leave those
+// Kernel instances for the reference step's research m2 variants: m2 read back after its
+// encode (AW4_MOMENT_SAMPLED_READ in the m2 spec's flags) and lookahead update-SR
+// (AW4_ROUND_LOOKAHEAD_SR); the generic one (any kind, marked by the flag) runs both.
+constexpr bool research_kernel(int m2k) {
+    return (flags_of(m2k) & AW4_MOMENT_SAMPLED_READ) != 0 || kind_of(m2k) == K_LA;
+}
+// (Not for the research m2 variants: the registers of a prefetched tile leave the read-back
 // kernels at 2 waves per SIMD, 21% slower than 3 without the prefetch.)
 constexpr bool prefetch_next_tile(int m1k, int m2k, int d) {
-    return kind_of(m1k) != K_ANY && kind_of(m2k) != K_ANY && d != D_ANY &&
-           !(flags_of(m2k) & AW4_MOMENT_SAMPLED_READ);
+    return kind_of(m1k) != K_ANY && kind_of(m2k) != K_ANY && d != D_ANY && !research_kernel(m2k);
 }
 constexpr bool tile_order_grid(int m1k, int m2k, int d) {
     return prefetch_next_tile(m1k, m2k, d) && kind_of(m2k) != K_USR;
 }
-// The generic kernel instance for the reference step's research m2 variants (marked by
-// AW4_MOMENT_SAMPLED_READ in the m2 spec's flags): m2 read back after its encode
-// (AW4_MOMENT_SAMPLED_READ) and lookahead update-SR (AW4_ROUND_LOOKAHEAD_SR).
-constexpr bool research_kernel(int m2k) { return (flags_of(m2k) & AW4_MOMENT_SAMPLED_READ) != 0; }
 // Update-SR kernels stage the new second moments in LDS (M2Staged) so that the prefetched
 // inputs fit in the registers of four waves per SIMD.
 constexpr bool stage_m2(int m1k, int m2k, int d) { return prefetch_next_tile(m1k, m2k, d) && kind_of(m2k) == K_USR; }
@@ -625,7 +626,10 @@ __device__ __forceinline__ void run_tiles(const StepHeader* hdr, const LdsT& lds
                 // every block tile of this kernel has a research m2 (the host groups them)
                 float m2v[16];
                 M2Regs m2{m2v};
-                if (T.m2.flags & AW4_MOMENT_SAMPLED_READ) {
+                bool sampled = false;  // m2 read back after its encode (else lookahead)
+                if constexpr (kind_of(M2K) != K_LA) sampled = (T.m2.flags & AW4_MOMENT_SAMPLED_READ) != 0;
+                if constexpr (kind_of(M2K) != K_LA) {
+                  if (sampled) {
                     float p1[16];
                     update_tile_any<M1K, M2K, D, true>(T, tl, in, L1, L2, m1, m2, p1);
                     finish_moment<M1K, false>(T.m1, L1, tl, RegValues{m1}, ws);
@@ -635,27 +639,41 @@ __device__ __forceinline__ void run_tiles(const StepHeader* hdr, const LdsT& lds
                     else if (T.param_dtype == D_BF16)
                         sampled_read_update<D_BF16>(T, tl, L2, ws.block(tl.grp), bs, m1, p1);
                     else sampled_read_update<D_F16>(T, tl, L2, ws.block(tl.grp), bs, m1, p1);
-                } else if constexpr (kind_of(M2K) == K_ANY) {
-                    // lookahead update-SR: sample the pending state before the update, or encode
-                    // the new m2 after it (the generic research instance only)
+                  }
+                }
+                if constexpr (kind_of(M2K) == K_ANY || kind_of(M2K) == K_LA) {
+                  if (!sampled) {
+                    // lookahead update-SR: sample the pending state before the update (the
+                    // generic instance; the K_LA instance takes the code-storing proxies only),
+                    // or encode the new m2 after it
                     float g[16];
                     tile_grads(T, in, g);
-                    const bool pending = (T.m2.flags & AW4_MOMENT_PENDING) != 0;
+                    const bool pending = kind_of(M2K) == K_ANY && (T.m2.flags & AW4_MOMENT_PENDING) != 0;
                     const float w2f = (float)T.m2.la_fresh_weight;
                     float prior[16];
-                    if (pending) {
-                        float z[16];
+                    if constexpr (kind_of(M2K) == K_ANY) {
+                        if (pending) {
+                            float z[16];
 #pragma unroll
-                        for (int i = 0; i < 16; ++i) z[i] = in.v2[i];
-                        encode_block_la(T.m2, L2, tl.blk0, tl.grp, tl.j, tl.active, z, g, w2f, false, prior,
-                                        ws.block(tl.grp));
+                            for (int i = 0; i < 16; ++i) z[i] = in.v2[i];
+                            encode_block_la(T.m2, L2, tl.blk0, tl.grp, tl.j, tl.active, z, g, w2f, false, prior,
+                                            ws.block(tl.grp));
+                        }
                     }
                     update_tile_any<M1K, M2K, D, false>(T, tl, in, L1, L2, m1, m2, nullptr, pending ? prior : nullptr);
                     finish_moment<M1K, false>(T.m1, L1, tl, RegValues{m1}, ws);
                     prefetch();
-                    if (pending) finish_moment<M2K, true>(T.m2, L2, tl, m2.values(), ws);
-                    else encode_block_la(T.m2, L2, tl.blk0, tl.grp, tl.j, tl.active, m2v, g, w2f, true, nullptr,
-                                         ws.block(tl.grp));
+                    bool stored = false;
+                    if constexpr (kind_of(M2K) == K_ANY) {
+                        if (pending) {
+                            finish_moment<M2K, true>(T.m2, L2, tl, m2.values(), ws);
+                            stored = true;
+                        }
+                    }
+                    if (!stored)
+                        encode_block_la(T.m2, L2, tl.blk0, tl.grp, tl.j, tl.active, m2v, g, w2f, true, nullptr,
+                                        ws.block(tl.grp));
+                  }
                 }
             } else if constexpr (stage_m2(M1K, M2K, D)) {
                 M2Staged m2{m2_stage + lane, 0.0f};

@@ -155,6 +155,8 @@ constexpr int kUsrGuardedEden = mspec(K_USR, AW4_MOMENT_GUARDS | AW4_MOMENT_EDEN
 // and *_upd_sr_store_eden (read at the scale before EDEN, EDEN on the stored scale).
 constexpr int kUsrRead = mspec(K_USR, AW4_MOMENT_SAMPLED_READ);
 constexpr int kUsrReadEden = mspec(K_USR, AW4_MOMENT_SAMPLED_READ | AW4_MOMENT_READ_RAW_SCALE | AW4_MOMENT_EDEN);
+// Lookahead update-SR m2 stored as codes (dyn4_proxy_la_upd_sr, dyn4_vproxy_la_upd_sr).
+constexpr int kLaStore = mspec(K_LA);
 // Any m2 kind of the research schemes (read-back and lookahead), any dtype.
 constexpr int kAnyResearch = mspec(K_ANY, AW4_MOMENT_SAMPLED_READ);
 struct KernelVariant {
@@ -169,6 +171,7 @@ const KernelVariant kVariants[] = {
     AW4_VARIANT(kRtn, kFp32, D_F32),              AW4_VARIANT(kRtn, kFp32, D_BF16),
     AW4_VARIANT(kRtn, kUsrGuardedEden, D_F32),    AW4_VARIANT(kRtn, kUsrGuardedEden, D_BF16),
     AW4_VARIANT(kRtn, kUsrRead, D_F32),           AW4_VARIANT(kRtn, kUsrReadEden, D_F32),
+    AW4_VARIANT(kRtn, kLaStore, D_F32),
     AW4_VARIANT(K_ANY, kAnyResearch, D_ANY),
     AW4_VARIANT(K_ANY, K_ANY, D_ANY),
 };

@@ -19,11 +19,13 @@ from adamw4bit_amd import build
 # (m1 spec, m2 spec, dtype) template arguments -> minimum waves per SIMD
 # m1: 1 = NF4 round-to-nearest, 66 = value-space SR with guards;
 # m2: 33 = round-to-nearest + EDEN, 67 = update-SR with guards, 99 = update-SR + EDEN, 0 = fp32,
-# 259 = update-SR read back after its encode, 803 = the same with the store-EDEN flags;
+# 259 = update-SR read back after its encode, 803 = the same with the store-EDEN flags,
+# 4 = lookahead update-SR stored as codes;
 # dtype: 0 = fp32, 1 = bf16.
 MIN_WAVES = {
     (1, 33, 0): 3, (1, 67, 0): 4, (1, 33, 1): 4, (1, 67, 1): 4, (66, 67, 0): 3, (66, 67, 1): 4,
     (1, 0, 0): 4, (1, 0, 1): 4, (1, 99, 0): 3, (1, 99, 1): 4, (1, 259, 0): 3, (1, 803, 0): 2,
+    (1, 4, 0): 2,
 }
 
 
