@@ -28,12 +28,15 @@ on a HIP device; there is no CPU implementation.
 
 from __future__ import annotations
 
+import functools
 import math
+import operator
 from collections.abc import Mapping
 from typing import Any, Dict, Iterable, Iterator, List, Optional, Tuple
 
 import numpy as np
 import torch
+from torch.optim import optimizer as _torch_optimizer
 from torch.optim.optimizer import Optimizer
 
 from . import _lib, _ops
@@ -80,6 +83,31 @@ def _rcp32(x: float) -> float:
     return float(np.float32(1.0) / np.float32(x))
 
 
+def _step_fields() -> np.dtype:
+    """View of a launch-table row holding only what a reused plan rewrites each step: the
+    gradient address and scale pointer, the flags word with the seven fp32 step constants
+    after it (``words``, 8 x 32 bits), the m2 update-SR constants (``m2_sr``, 3 x 32 bits)
+    and both random-stream positions."""
+    T = _lib.TENSOR
+    m1, m2 = T.fields["m1"][1], T.fields["m2"][1]
+    M = T.fields["m2"][0]
+    words = ("flags", "w1", "w2", "decay", "step_coef", "bc2_sqrt", "bc2_sqrt_rcp", "eps")
+    assert [T.fields[k][1] for k in words] == [T.fields["flags"][1] + 4 * i for i in range(8)]
+    assert [M.fields[k][1] for k in ("sr_bias", "sr_bias_rcp", "sr_eps")] == [M.fields["sr_bias"][1] + 4 * i
+                                                                            for i in range(3)]
+    return np.dtype({"names": ["grad", "grad_scale", "words", "m2_sr", "m1_rng_offset", "m2_rng_offset"],
+                     "formats": ["<u8", "<u8", ("<u4", 8), ("<u4", 3), "<u8", "<u8"],
+                     "offsets": [T.fields["grad"][1], T.fields["grad_scale"][1], T.fields["flags"][1],
+                                 m2 + M.fields["sr_bias"][1], m1 + M.fields["rng_offset"][1],
+                                 m2 + M.fields["rng_offset"][1]],
+                     "itemsize": T.itemsize})
+
+
+_STEP_FIELDS = _step_fields()
+_STEP_WORDS = np.dtype([("flags", "<i4")] + [(k, "<f4") for k in ("w1", "w2", "decay", "step_coef", "bc2_sqrt",
+                                                                   "bc2_sqrt_rcp", "eps")])
+
+
 def _byte_range(t: torch.Tensor) -> Tuple[str, int, int]:
     """Storage interval of a tensor (``_moment_buffer.py:13-20``)."""
     if t.is_contiguous():
@@ -97,8 +125,7 @@ class _StepConstants:
     """The fp32 step constants of one (group, step), computed in float64 and rounded once to
     fp32 as the reference does (``_optimized.py:168-173``)."""
 
-    __slots__ = ("lerp_flags", "w1", "w2", "decay", "step_coef", "bc2_sqrt", "bc2_sqrt_rcp", "eps", "storage_bias",
-                 "rows")
+    __slots__ = ("lerp_flags", "w1", "w2", "decay", "step_coef", "bc2_sqrt", "bc2_sqrt_rcp", "eps", "storage_bias")
 
     def __init__(self, group, step: int, m2_scheme: str):
         beta1, beta2 = group["betas"]
@@ -155,6 +182,31 @@ def _launch(params: List[torch.Tensor], written: List[torch.Tensor], read: List[
     else:
         _lib.fused_step(table, torch.cuda.current_stream(device).cuda_stream)
     torch.autograd.graph.increment_version(params + written)
+
+
+def _lean_step(func):
+    """``Optimizer.step`` wrapper with torch's behaviour and less fixed cost.
+
+    torch wraps every optimizer's ``step`` (``Optimizer.profile_hook_step``) in a profiler range
+    ``Optimizer.step#<class>.step`` around the step pre-hooks, the step and the post-hooks; the
+    range alone costs about 15 us per call, a third of the host time of a one-tensor step.  This
+    wrapper runs torch's own wrapper whenever a profiler is running or a step hook is registered
+    (globally or on the optimizer), and otherwise calls the step and ``_optimizer_step_code``
+    directly.  ``hooked`` tells ``Optimizer._patch_step_function`` not to wrap it again."""
+    torch_wrapped = Optimizer.profile_hook_step(func)
+
+    @functools.wraps(func)
+    def step(self, *args, **kwargs):
+        if (torch.autograd._profiler_enabled() or self._optimizer_step_pre_hooks
+                or self._optimizer_step_post_hooks or _torch_optimizer._global_optimizer_pre_hooks
+                or _torch_optimizer._global_optimizer_post_hooks):
+            return torch_wrapped(self, *args, **kwargs)
+        out = func(self, *args, **kwargs)
+        self._optimizer_step_code()
+        return out
+
+    step.hooked = True
+    return step
 
 
 def _moment_tensors(state: Dict[str, Any]) -> List[torch.Tensor]:
@@ -574,6 +626,7 @@ class QuantizedAdamW(Optimizer):
             return None
         return clip[1]
 
+    @_lean_step
     def step(self, closure=None):  # type: ignore[override]
         loss = None
         if closure is not None:
@@ -836,11 +889,12 @@ class _LaunchPlan:
         self.groups: list = []     # (group, structure, parameter count)
         self.params: List[torch.Tensor] = []
         self.devices: list = []    # per device: table, params, written, rows
-        # what the tables were built from, checked by identity each step: (param, state dict),
-        # (state dict, key, value) for every state key, (QuantState, its absmax tensor)
-        self.owners: list = []
-        self.state_refs: list = []
-        self.quant_refs: list = []
+        # what the tables were built from, checked by identity each step, as parallel lists:
+        # (params, their state dicts), (state dict, key, value) for every state key,
+        # (QuantState, its absmax tensor)
+        self.owners: Tuple[list, list] = ([], [])
+        self.state_refs: Tuple[list, list, list] = ([], [], [])
+        self.quant_refs: Tuple[list, list] = ([], [])
 
     @classmethod
     def build(cls, opt: "QuantizedAdamW", per_device, tables, info) -> Optional["_LaunchPlan"]:
@@ -879,15 +933,23 @@ class _LaunchPlan:
                            for moment, scheme in (("m1", schemes[0]), ("m2", schemes[1]))
                            if scheme != "fp32" and SCHEMES[scheme][1] in _SR_ROUNDINGS)
                 entries.append((p, state, None, group_of[id(p)], schemes[1], sr, p.numel()))
-                plan.owners.append((p, state))
-                plan.state_refs.extend((state, k, state.get(k)) for k in cls._STATE_KEYS + (_FALLBACK_KEY,))
-                plan.quant_refs.extend((q, q.absmax) for q in (state.get("m1_quant_state"), state.get("m2_quant_state"))
-                                       if isinstance(q, QuantState))
+                plan.owners[0].append(p)
+                plan.owners[1].append(state)
+                for k in cls._STATE_KEYS + (_FALLBACK_KEY,):
+                    plan.state_refs[0].append(state)
+                    plan.state_refs[1].append(k)
+                    plan.state_refs[2].append(state.get(k))
+                for q in (state.get("m1_quant_state"), state.get("m2_quant_state")):
+                    if isinstance(q, QuantState):
+                        plan.quant_refs[0].append(q)
+                        plan.quant_refs[1].append(q.absmax)
             table = tables[device]
             gbytes = np.array([p.numel() * p.element_size() for p in params], dtype=np.int64)
             pvec = np.array([p.data_ptr() % (4 * p.element_size()) == 0 for p in params], dtype=bool)
             gvec = np.array([4 * p.element_size() for p in params], dtype=np.int64)
-            plan.devices.append((table, list(params), list(written), entries, lo, hi, gbytes, pvec, gvec))
+            qrows = np.flatnonzero(table["m2"]["rounding"] != _lib.ROUND_FP32)
+            plan.devices.append((table, list(params), list(written), entries, lo, hi, gbytes, pvec, gvec,
+                                 table.view(_STEP_FIELDS), qrows))
             plan.params.extend(params)
         return plan
 
@@ -913,18 +975,21 @@ class _LaunchPlan:
                 i += 1
         if i != n:
             return None
+        # identity checks in C-level loops (map/all): about 1,300 of them for 148 parameters
         state_map = opt.state
-        for p, state in self.owners:
-            if state_map.get(p) is not state or type(state.get("step")) is not int:
-                return None
-        for state, key, value in self.state_refs:
-            if state.get(key) is not value:
-                return None
-        for q, absmax in self.quant_refs:
-            if q.absmax is not absmax:
-                return None
+        owners, states = self.owners
+        if not all(map(operator.is_, map(state_map.get, owners), states)):
+            return None
+        if not all(type(state.get("step")) is int for state in states):
+            return None
+        ref_states, ref_keys, ref_values = self.state_refs
+        if not all(map(operator.is_, map(dict.get, ref_states, ref_keys), ref_values)):
+            return None
+        quant, absmax = self.quant_refs
+        if not all(map(operator.is_, map(operator.attrgetter("absmax"), quant), absmax)):
+            return None
         out = []
-        for table, dparams, written, entries, lo, hi, gbytes, pvec, gvec in self.devices:
+        for table, dparams, written, entries, lo, hi, gbytes, pvec, gvec, _, _ in self.devices:
             g0 = np.fromiter((p.grad.data_ptr() for p in dparams), dtype=np.int64, count=len(dparams))
             g1 = g0 + gbytes
             if bool(((lo < g1[:, None]) & (g0[:, None] < hi)).any()):
@@ -937,39 +1002,42 @@ class _LaunchPlan:
         grads = self._valid(opt)
         if grads is None:
             return False
-        constants: Dict[Tuple[int, int], _StepConstants] = {}
-        for (table, params, written, entries, lo, hi, gbytes, pvec, gvec), g0 in zip(self.devices, grads):
-            per_row = []
-            offsets = {"m1": table["m1"]["rng_offset"].copy(), "m2": table["m2"]["rng_offset"].copy()}
+        # one _StepConstants per (group, step, m2 scheme): the update-SR storage bias depends on
+        # the tensor's m2 scheme (an fp32-state tensor of a group has the fp32 scheme)
+        constants: Dict[Tuple[int, int, str], int] = {}
+        consts: List[_StepConstants] = []
+        for (table, params, written, entries, lo, hi, gbytes, pvec, gvec, fields, qrows), g0 in zip(self.devices,
+                                                                                                      grads):
+            index = np.empty(len(entries), dtype=np.intp)
+            offsets = {"m1": fields["m1_rng_offset"].copy(), "m2": fields["m2_rng_offset"].copy()}
             for i, (p, state, _, gi, m2_scheme, sr, numel) in enumerate(entries):
                 step = state["step"] + 1
                 state["step"] = step
-                c = constants.get((gi, step))
-                if c is None:
-                    c = constants[(gi, step)] = _StepConstants(self.groups[gi][0], step, m2_scheme)
-                    sr_bias = _f32(max(float(c.storage_bias), 1e-12))
-                    c.rows = (c.w1, c.w2, c.decay, c.step_coef, c.bc2_sqrt, c.bc2_sqrt_rcp, c.eps,
-                              sr_bias, _rcp32(sr_bias), c.eps, c.lerp_flags)
-                per_row.append(c.rows)
+                k = constants.get((gi, step, m2_scheme))
+                if k is None:
+                    k = constants[(gi, step, m2_scheme)] = len(consts)
+                    consts.append(_StepConstants(self.groups[gi][0], step, m2_scheme))
+                index[i] = k
                 for moment, stream in sr:
                     offsets[moment][i] = stream.take(numel)
-            cols = np.array(per_row, dtype=np.float64).T
-            table["grad"] = g0.astype(np.uint64)
-            aligned = pvec & (g0 % gvec == 0)
-            table["flags"] = cols[10].astype(np.int32) | np.where(aligned, _lib.TENSOR_VEC_ALIGNED, 0)
-            for k, name in enumerate(("w1", "w2", "decay", "step_coef", "bc2_sqrt", "bc2_sqrt_rcp", "eps")):
-                table[name] = cols[k].astype(np.float32)
-            m1, m2 = table["m1"], table["m2"]  # views into the table
-            quantized = m2["rounding"] != _lib.ROUND_FP32
-            for k, name in enumerate(("sr_bias", "sr_bias_rcp", "sr_eps")):
-                m2[name] = np.where(quantized, cols[7 + k].astype(np.float32), m2[name])
-            m1["rng_offset"] = offsets["m1"]
-            m2["rng_offset"] = offsets["m2"]
-            read = [p.grad for p in params]
+            # the flags word and the seven fp32 step constants (bit patterns), and the m2
+            # update-SR constants of the rows whose m2 is quantized
+            words = np.array([(c.lerp_flags, c.w1, c.w2, c.decay, c.step_coef, c.bc2_sqrt, c.bc2_sqrt_rcp, c.eps)
+                              for c in consts], dtype=_STEP_WORDS)[index]
             coef = opt._take_grad_clip(params[0].device)
-            table["grad_scale"] = 0 if coef is None else coef.data_ptr()
+            words["flags"] |= np.where(pvec & (g0 % gvec == 0), _lib.TENSOR_VEC_ALIGNED, 0) | (
+                0 if coef is None else _lib.TENSOR_GRAD_SCALE)
+            fields["words"] = words.view(np.uint32).reshape(-1, 8)
+            if len(qrows):
+                sr_bias = [_f32(max(float(c.storage_bias), 1e-12)) for c in consts]
+                fields["m2_sr"][qrows] = np.array([(b, _rcp32(b), c.eps) for b, c in zip(sr_bias, consts)],
+                                                  dtype=np.float32)[index[qrows]].view(np.uint32)
+            fields["grad"] = g0
+            fields["grad_scale"] = 0 if coef is None else coef.data_ptr()
+            fields["m1_rng_offset"] = offsets["m1"]
+            fields["m2_rng_offset"] = offsets["m2"]
+            read = [p.grad for p in params]
             if coef is not None:
-                table["flags"] |= _lib.TENSOR_GRAD_SCALE
                 read.append(coef)
             _launch(params, written, read, table)
         return True

@@ -610,19 +610,30 @@ def test_mixed_recipes_split_launches(dtype):
     compare_pair(*out, f"mixed recipes {dtype}", steps=4)
 
 
-def test_launch_plan_reuse_matches_full_path():
+@pytest.mark.parametrize("m2_scheme", [None, "dyn4_upd_sr_fp32read_nextbc"])
+def test_launch_plan_reuse_matches_full_path(m2_scheme):
     """Steps reusing the previous step's launch tables are bit-identical to steps that rebuild
     them, through a learning-rate change, a parameter without gradient, an m1 retarget, and
     state tensors replaced by equal copies (a code tensor, a QuantState's absmax), which the
-    plan must not keep writing through its old addresses."""
-    log("launch plan reuse vs full path")
+    plan must not keep writing through its old addresses.  With the next-step storage bias
+    the group's first tensor is an fp32-state one, whose m2 scheme (fp32) has the other bias:
+    the step constants must not be shared across the two."""
+    log(f"launch plan reuse vs full path ({m2_scheme or 'ZIP-SR'})")
     shapes = [(256, 512), (768,), (64, 1024), (1000,), (128, 384)]
+    q0 = 0
+    if m2_scheme is not None:
+        shapes[0], shapes[1] = shapes[1], shapes[0]
+        q0 = 1  # the first parameter with quantized state
     gen = torch.Generator().manual_seed(21)
     init = [torch.randn(s, generator=gen) * 0.02 for s in shapes]
     pa = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
     pb = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
     args = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True, quant_rng_seed=4)
-    oa, ob = aw.ZIPSRAdamW4Bit(pa, **args), aw.ZIPSRAdamW4Bit(pb, **args)
+    if m2_scheme is None:
+        oa, ob = aw.ZIPSRAdamW4Bit(pa, **args), aw.ZIPSRAdamW4Bit(pb, **args)
+    else:
+        args.update(m1_quant_scheme="nf4", m2_quant_scheme=m2_scheme)
+        oa, ob = aw.QuantizedAdamW(pa, **args), aw.QuantizedAdamW(pb, **args)
     reused = 0
     for k in range(7):
         for a, b, s in zip(pa, pb, shapes):
@@ -634,11 +645,11 @@ def test_launch_plan_reuse_matches_full_path():
             for o in (oa, ob):
                 o.param_groups[0]["lr"] = 5e-4
         if k == 5:
-            oa.set_m1_quant_scheme_for_parameters([pa[0]], "nf4_sr")
-            ob.set_m1_quant_scheme_for_parameters([pb[0]], "nf4_sr")
+            oa.set_m1_quant_scheme_for_parameters([pa[q0]], "nf4_sr")
+            ob.set_m1_quant_scheme_for_parameters([pb[q0]], "nf4_sr")
         if k == 6:
             for o, ps in ((oa, pa), (ob, pb)):
-                o.state[ps[0]]["m2_code"] = o.state[ps[0]]["m2_code"].clone()
+                o.state[ps[q0]]["m2_code"] = o.state[ps[q0]]["m2_code"].clone()
                 q = o.state[ps[4]]["m1_quant_state"]
                 q.absmax = q.absmax.clone()
         before = oa._launch_plan

@@ -109,3 +109,40 @@ def test_clip_grad_norm_host_checks():
         opt.clip_grad_norm_(1.0, norm_type=float("inf"))
     with pytest.raises(NotImplementedError, match="one HIP device"):
         opt.clip_grad_norm_(1.0)
+
+
+class _CountingOptimizer(torch.optim.Optimizer):
+    """A one-parameter optimizer whose step is wrapped like ``QuantizedAdamW.step``."""
+
+    def __init__(self, params):
+        super().__init__(params, {})
+        self.calls = []
+
+    @aw.adamw._lean_step
+    def step(self, closure=None, scale=1.0):
+        self.calls.append(scale)
+        return scale
+
+
+def test_lean_step_keeps_torch_hooks_and_profiler_range():
+    from torch.optim.optimizer import register_optimizer_step_post_hook, register_optimizer_step_pre_hook
+    assert aw.QuantizedAdamW.step.hooked and aw.ZIPSRAdamW4Bit.step is aw.QuantizedAdamW.step
+    opt = _CountingOptimizer([torch.nn.Parameter(torch.zeros(1))])
+    assert type(opt).step.__wrapped__.__name__ == "step"  # not wrapped again by torch
+    assert opt.step() == 1.0 and opt.calls == [1.0]
+    seen = []
+    pre = opt.register_step_pre_hook(lambda o, args, kwargs: (args, {**kwargs, "scale": 2.0}))
+    post = opt.register_step_post_hook(lambda o, args, kwargs: seen.append(("post", kwargs["scale"])))
+    gpre = register_optimizer_step_pre_hook(lambda o, args, kwargs: seen.append(("gpre", o is opt)))
+    gpost = register_optimizer_step_post_hook(lambda o, args, kwargs: seen.append(("gpost", o is opt)))
+    try:
+        assert opt.step() == 2.0
+        assert seen == [("gpre", True), ("post", 2.0), ("gpost", True)]
+    finally:
+        for h in (pre, post, gpre, gpost):
+            h.remove()
+    assert opt.step() == 1.0 and opt.calls == [1.0, 2.0, 1.0]
+    with torch.profiler.profile(activities=[torch.profiler.ProfilerActivity.CPU]) as prof:
+        opt.step()
+    names = {e.name for e in prof.events()}
+    assert "Optimizer.step#_CountingOptimizer.step" in names
