@@ -408,6 +408,9 @@ struct DeviceState {
     int num_cus = 0;
     StagingSlot slots[kSlots];
     int next = 0;
+    // Host buffers of slots that have grown.  The device has read them uncached; they are kept
+    // until the process ends rather than freed and their pages handed out again.
+    std::vector<void*> retired_host;
 };
 
 std::mutex g_mutex;
@@ -625,7 +628,7 @@ int acquire_slot(DeviceState* ds, size_t bytes, StagingSlot** out) {
         slot.pending = false;
     }
     if (slot.cap < bytes) {
-        if (slot.host) AW4_HIP_CHECK(hipHostFree(slot.host));
+        if (slot.host) ds->retired_host.push_back(slot.host);
         if (slot.dev) AW4_HIP_CHECK(hipFree(slot.dev));
         slot.host = slot.dev = nullptr;
         slot.host_dev = nullptr;
