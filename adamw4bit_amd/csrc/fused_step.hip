@@ -644,7 +644,11 @@ int acquire_slot(DeviceState* ds, size_t bytes, StagingSlot** out) {
         AW4_HIP_CHECK(hipMalloc(&slot.dev, cap));
         slot.cap = cap;
     }
-    if (!slot.done) AW4_HIP_CHECK(hipEventCreateWithFlags(&slot.done, hipEventDisableTiming));
+    // The event only tells the host that the launch which read the slot has finished; no data
+    // flows from the device to the host through it, so it records without a system-scope fence
+    // (a cache write-back between consecutive launches).
+    if (!slot.done)
+        AW4_HIP_CHECK(hipEventCreateWithFlags(&slot.done, hipEventDisableTiming | hipEventDisableSystemFence));
     *out = &slot;
     return AW4_OK;
 }
