@@ -312,3 +312,40 @@ def test_torch_custom_op_schema_and_argument_checks():
         "adamw4bit_hip::clip_coefficient_(Tensor[] grads, Tensor(a1!) out, Tensor table, float max_norm)")
     with pytest.raises(ValueError, match="HIP device"):
         clip([torch.zeros(4)], torch.zeros(2), torch.zeros(row, dtype=torch.uint8), 1.0)
+
+
+def test_plan_step_view_covers_exactly_the_per_step_fields():
+    """The launch plan rewrites each step through one fixed view of the table rows; writing
+    through it changes the per-step fields and leaves every other byte of the row alone."""
+    import numpy as np
+    from adamw4bit_amd import _lib
+    from adamw4bit_amd.adamw import _STEP_FIELDS, _STEP_WORDS
+    T = _lib.TENSOR
+    assert _STEP_FIELDS.itemsize == T.itemsize == 280 and _STEP_WORDS.itemsize == 32
+    row = np.zeros(2, dtype=T)
+    raw = row.view(np.uint8).reshape(2, -1)
+    raw[:] = 0xA5
+    before = raw.copy()
+    view = row.view(_STEP_FIELDS)
+    view["grad"] = [11, 12]
+    view["grad_scale"] = [13, 14]
+    words = np.array([(3, 0.5, 0.25, 0.75, -1e-3, 0.125, 8.0, 1e-8)] * 2, dtype=_STEP_WORDS)
+    view["words"] = words.view(np.uint32).reshape(-1, 8)
+    view["m2_sr"] = np.array([[1.5, 2.5, 3.5]] * 2, dtype=np.float32).view(np.uint32)
+    view["m1_rng_offset"] = [21, 22]
+    view["m2_rng_offset"] = [23, 24]
+    assert list(row["grad"]) == [11, 12] and list(row["grad_scale"]) == [13, 14]
+    assert list(row["flags"]) == [3, 3]
+    for name, value in zip(("w1", "w2", "decay", "step_coef", "bc2_sqrt", "bc2_sqrt_rcp", "eps"),
+                           (0.5, 0.25, 0.75, -1e-3, 0.125, 8.0, 1e-8)):
+        assert np.all(row[name] == np.float32(value)), name
+    assert np.all(row["m2"]["sr_bias"] == 1.5) and np.all(row["m2"]["sr_bias_rcp"] == 2.5)
+    assert np.all(row["m2"]["sr_eps"] == 3.5)
+    assert list(row["m1"]["rng_offset"]) == [21, 22] and list(row["m2"]["rng_offset"]) == [23, 24]
+    # every byte outside those fields is untouched
+    written = np.zeros(T.itemsize, dtype=bool)
+    for name in _STEP_FIELDS.names:
+        dt, off = _STEP_FIELDS.fields[name][:2]
+        written[off:off + dt.itemsize] = True
+    assert written.sum() == 8 + 8 + 32 + 12 + 8 + 8
+    assert np.array_equal(raw[:, ~written], before[:, ~written])
