@@ -124,6 +124,7 @@ class _CountingOptimizer(torch.optim.Optimizer):
         return scale
 
 
+@pytest.mark.filterwarnings("ignore:Warning. Profiler clears events:UserWarning")
 def test_lean_step_keeps_torch_hooks_and_profiler_range():
     from torch.optim.optimizer import register_optimizer_step_post_hook, register_optimizer_step_pre_hook
     assert aw.QuantizedAdamW.step.hooked and aw.ZIPSRAdamW4Bit.step is aw.QuantizedAdamW.step
