@@ -161,27 +161,32 @@ def _vec_aligned(p: torch.Tensor, grad: torch.Tensor) -> bool:
 
 
 def _launch(params: List[torch.Tensor], written: List[torch.Tensor], read: List[torch.Tensor],
-            table: np.ndarray) -> None:
-    """Launch one step's table on the parameters' device and current stream.
+            table: torch.Tensor, refs: torch.Tensor, copy_back: List[Tuple[torch.Tensor, torch.Tensor]]) -> None:
+    """Launch one device's step on its current stream (a launch record of ``_DeviceBatch.launch``).
 
     Under ``torch.compile`` the launch is the custom operator ``adamw4bit_hip::fused_step_``,
-    which declares the tensors it writes and reads.  In eager mode the operator's dispatch
-    (argument flattening and one version bump per tensor) costs about 5 us per tensor, so the
-    library is called directly and the version counters of everything written in place are
-    bumped in one call, as the operator would; ``read`` is referenced by the caller until the
-    call returns, and the kernels are ordered on the stream like any torch kernel."""
+    which declares the tensors it writes and reads and takes their addresses from the tensors it
+    receives (``refs``).  In eager mode the operator's dispatch (argument flattening and one
+    version bump per tensor) costs about 5 us per tensor, so the library is called directly on
+    the table, whose addresses are already filled in, and the version counters of everything
+    written in place are bumped in one call, as the operator would; ``read`` is referenced by
+    the caller until the call returns, and the kernels are ordered on the stream like any torch
+    kernel.  Strided parameters were stepped as contiguous copies, copied back here."""
     if torch.compiler.is_compiling():
-        _ops.fused_step_(params, written, read, torch.from_numpy(table.view(np.uint8)))
-        return
-    device = params[0].device
-    if device.type != "cuda":
-        raise ValueError("the fused 4-bit step runs on HIP devices only")
-    if torch.cuda.current_device() != device.index:
-        with torch.cuda.device(device):
-            _lib.fused_step(table, torch.cuda.current_stream(device).cuda_stream)
+        _ops.fused_step_(params, written, read, table, refs)
     else:
-        _lib.fused_step(table, torch.cuda.current_stream(device).cuda_stream)
-    torch.autograd.graph.increment_version(params + written)
+        device = params[0].device
+        if device.type != "cuda":
+            raise ValueError("the fused 4-bit step runs on HIP devices only")
+        rows = table.numpy().view(_lib.TENSOR)
+        if torch.cuda.current_device() != device.index:
+            with torch.cuda.device(device):
+                _lib.fused_step(rows, torch.cuda.current_stream(device).cuda_stream)
+        else:
+            _lib.fused_step(rows, torch.cuda.current_stream(device).cuda_stream)
+        torch.autograd.graph.increment_version(params + written)
+    for p, staged in copy_back:
+        p.copy_(staged)
 
 
 def _lean_step(func):
@@ -354,6 +359,7 @@ class QuantizedAdamW(Optimizer):
         # on-device Philox draws of a stochastic write (bit-exact comparisons with fed draws).
         self._draw_provider = None
         self._launch_plan: Optional[_LaunchPlan] = None
+        self._pending_finish = None  # commit / undo of the step being launched
         # Gradient clipping computed by clip_grad_norm_ and applied by the next step:
         # (device, fp32 coefficient on that device) or None.
         self._grad_clip: Optional[Tuple[torch.device, torch.Tensor]] = None
@@ -432,6 +438,11 @@ class QuantizedAdamW(Optimizer):
         if key not in streams:
             streams[key] = PhiloxStream(int(torch.randint(0, (1 << 62) - 1, (1,)).item()))
         return streams[key]
+
+    def _all_streams(self) -> List[PhiloxStream]:
+        """Every random stream this optimizer has opened."""
+        return [s for table in (self._quant_generators, self._global_streams) for streams in table.values()
+                for s in streams.values()]
 
     # ------------------------------------------------------------------
     # Checkpoints (adamw.py:326-470, _optimized.py:53-83)
@@ -549,10 +560,6 @@ class QuantizedAdamW(Optimizer):
                     optimizer.state[parameter][_FALLBACK_KEY] = True
 
     # ------------------------------------------------------------------
-    # The step
-    # ------------------------------------------------------------------
-    @torch.no_grad()
-    # ------------------------------------------------------------------
     # Gradient clipping fused into the step
     # ------------------------------------------------------------------
     @torch.no_grad()
@@ -574,11 +581,34 @@ class QuantizedAdamW(Optimizer):
         """
         if float(norm_type) != 2.0:
             raise NotImplementedError("the fused clip computes the 2-norm only")
+        prepared = self._prepare_clip()
+        if prepared is None:
+            return torch.tensor(0.0)
+        grads, table, out, result_dtype = prepared
+        if torch.compiler.is_compiling():
+            _ops.clip_coefficient_(grads, out, table, float(max_norm))
+        else:  # the operator's dispatch over every gradient costs more than the call (see _launch)
+            with torch.cuda.device(out.device):
+                _lib.clip_coefficient(table.numpy().view(_lib.TENSOR), float(max_norm), out.data_ptr(),
+                                      out.data_ptr() + 4, torch.cuda.current_stream(out.device).cuda_stream)
+        total = out[0].to(result_dtype)
+        if error_if_nonfinite and bool(torch.logical_or(total.isnan(), total.isinf())):
+            raise RuntimeError(
+                f"The total norm of order {float(norm_type)} for gradients from `parameters` is non-finite, so it "
+                "cannot be clipped. To disable this error and scale the gradients by the non-finite norm anyway, "
+                "set `error_if_nonfinite=False`")
+        self._set_grad_clip(out)
+        return total
+
+    @torch.compiler.disable
+    def _prepare_clip(self):
+        """Gradients, launch table (as a CPU uint8 tensor) and the output pair of a clip, or None
+        without gradients."""
         if self._grad_clip is not None:
             raise RuntimeError("a gradient clip is already pending: call step() before clipping again")
         params = [p for group in self.param_groups for p in group["params"] if p.grad is not None]
         if not params:
-            return torch.tensor(0.0)
+            return None
         devices = {p.device for p in params}
         device = params[0].device
         if len(devices) != 1 or device.type != "cuda":
@@ -595,24 +625,15 @@ class QuantizedAdamW(Optimizer):
         table["grad_dtype"] = [_DTYPES[g.dtype] for g in grads]
         table["flags"] = [_lib.TENSOR_VEC_ALIGNED if g.data_ptr() % (4 * g.element_size()) == 0 else 0 for g in grads]
         out = torch.empty(2, dtype=torch.float32, device=device)  # [total norm, coefficient]
-        if torch.compiler.is_compiling():
-            _ops.clip_coefficient_(grads, out, torch.from_numpy(table.view(np.uint8)), float(max_norm))
-        else:  # the operator's dispatch over every gradient costs more than the call (see _launch)
-            with torch.cuda.device(device):
-                _lib.clip_coefficient(table, float(max_norm), out.data_ptr(), out.data_ptr() + 4,
-                                      torch.cuda.current_stream(device).cuda_stream)
         result_dtype = grads[0].dtype
         for g in grads[1:]:
             if g.dtype != result_dtype:
                 result_dtype = torch.float32  # torch.stack promotes the per-tensor norms
-        total = out[0].to(result_dtype)
-        if error_if_nonfinite and bool(torch.logical_or(total.isnan(), total.isinf())):
-            raise RuntimeError(
-                f"The total norm of order {float(norm_type)} for gradients from `parameters` is non-finite, so it "
-                "cannot be clipped. To disable this error and scale the gradients by the non-finite norm anyway, "
-                "set `error_if_nonfinite=False`")
-        self._grad_clip = (device, out[1:])
-        return total
+        return grads, torch.from_numpy(table.view(np.uint8)), out, result_dtype
+
+    @torch.compiler.disable
+    def _set_grad_clip(self, out: torch.Tensor) -> None:
+        self._grad_clip = (out.device, out[1:])
 
     def zero_grad(self, set_to_none: bool = True) -> None:
         """``Optimizer.zero_grad``; also drops a pending gradient clip, whose gradients are gone
@@ -626,47 +647,115 @@ class QuantizedAdamW(Optimizer):
             return None
         return clip[1]
 
+    # ------------------------------------------------------------------
+    # The step
+    # ------------------------------------------------------------------
     @_lean_step
+    @torch.no_grad()
     def step(self, closure=None):  # type: ignore[override]
+        """One fused launch per device over every parameter with a gradient (``adamw.py:472-502``).
+
+        The host work -- validation, state initialisation, the launch tables -- runs eagerly, also
+        under ``torch.compile`` (``_prepare_launches`` is compiler-disabled); the launch itself is
+        the custom operator ``adamw4bit_hip::fused_step_`` when compiled and a direct library call
+        otherwise.  A step changes nothing unless it launches: every parameter is checked before
+        any state changes, and a failed launch restores step counts, moment state and random
+        stream positions."""
         loss = None
         if closure is not None:
             with torch.enable_grad():
                 loss = closure()
-        plan = self._launch_plan
-        if plan is not None and plan.step(self):
-            self._grad_clip = None
-            return loss
-        # per device: launch rows, parameters, written states, read inputs (gradients, draws)
-        per_device: Dict[torch.device, Tuple[List[Tuple], List[torch.Tensor], List[torch.Tensor],
-                                             List[torch.Tensor]]] = {}
-        info: list = []
-        for group in self.param_groups:
-            for p in group["params"]:
-                if p.grad is None:
-                    continue
-                rows, params, written, read = per_device.setdefault(p.device, ([], [], [], []))
-                rows.append(self._prepare(p, group, read, written, info))
-                params.append(p)
-        tables = {}
-        for device, (rows, params, written, read) in per_device.items():
-            table = tables[device] = np.array(rows, dtype=_lib.TENSOR)
-            coef = self._take_grad_clip(device)
-            if coef is not None:
-                table["grad_scale"] = coef.data_ptr()
-                table["flags"] |= _lib.TENSOR_GRAD_SCALE
-                read = read + [coef]
-            _launch(params, written, read, table)
-        self._grad_clip = None
-        self._launch_plan = _LaunchPlan.build(self, per_device, tables, info)
+        launches = self._prepare_launches()
+        done = 0
+        try:
+            for launch in launches:
+                _launch(*launch)
+                done += 1
+        finally:
+            self._finish_step(done, len(launches))
         return loss
 
-    def _plan_accepts(self, p: torch.Tensor, grad: torch.Tensor, group, requested, schemes, state) -> bool:
-        """Whether the optimized backend's preflight takes this parameter (``_optimized.py:85-126``)."""
+    @torch.compiler.disable
+    def _finish_step(self, done: int, total: int) -> None:
+        """Commit the prepared step after its launches (``done == total``), or undo it if none ran."""
+        finish, self._pending_finish = self._pending_finish, None
+        if finish is not None:
+            finish(done, total)
+
+    @torch.compiler.disable
+    def _prepare_launches(self):
+        """Launch records of this step (see ``_launch``); leaves the step's commit / undo in
+        ``_pending_finish`` for ``_finish_step``."""
+        self._pending_finish = None
+        plan = self._launch_plan
+        if plan is not None:
+            prepared = plan.prepare(self)
+            if prepared is not None:
+                launches, self._pending_finish = prepared
+                return launches
+        self._launch_plan = None
+        checked = [self._preflight(p, group) for group in self.param_groups for p in group["params"]
+                   if p.grad is not None]
+        undo = _StepUndo(self, [c.state for c in checked])
+        batches: Dict[torch.device, _DeviceBatch] = {}
+        try:
+            for c in checked:
+                batch = batches.get(c.param.device)
+                if batch is None:
+                    batch = batches[c.param.device] = _DeviceBatch()
+                self._prepare(c, batch)
+            launches = [batch.launch(self._take_grad_clip(device)) for device, batch in batches.items()]
+        except BaseException:
+            undo.restore()
+            raise
+
+        def finish(done: int, total: int) -> None:
+            if done == total:
+                self._grad_clip = None
+                self._launch_plan = _LaunchPlan.build(self, list(batches.values()), checked)
+            elif done == 0:
+                undo.restore()
+
+        self._pending_finish = finish
+        return launches
+
+    def _moment_compatible(self, state, key: str, scheme: str, size: int, p: torch.Tensor) -> bool:
+        """The optimized backend's check of existing moment state (``_moment_buffer.py:54-87``)."""
+        if "step" not in state:
+            return True
+        if scheme == "fp32":
+            value = state.get(key)
+            return (isinstance(value, torch.Tensor) and value.layout == torch.strided and value.is_contiguous()
+                    and value.shape == p.shape and value.device == p.device and value.dtype == torch.float32)
+        codes = state.get(f"{key}_code")
+        meta = state.get(f"{key}_quant_state")
+        if not isinstance(codes, torch.Tensor) or not isinstance(meta, QuantState):
+            return False
+        n = p.numel()
+        absmax = meta.absmax
+        if not (codes.layout == torch.strided and codes.is_contiguous() and codes.dtype == torch.uint8
+                and codes.device == p.device and meta.shape == p.shape and meta.blocksize == size
+                and meta.dtype == torch.float32 and isinstance(absmax, torch.Tensor) and absmax.ndim == 1
+                and absmax.numel() == n // size and absmax.is_contiguous() and absmax.dtype == torch.float32
+                and absmax.device == p.device):
+            return False
+        if getattr(meta, "packed", False):
+            return codes.numel() == (n + 1) // 2
+        return codes.numel() in {n, (n + 1) // 2}
+
+    def _plan_accepts(self, p: torch.Tensor, grad: torch.Tensor, group, requested, sizes, schemes, state) -> bool:
+        """Whether the optimized backend's preflight takes this parameter (``_optimized.py:85-136``):
+        otherwise it follows the reference step."""
         if not self._optimized or state.get(_FALLBACK_KEY, False):
             return False
         if requested[0] not in _OPT_M1_SCHEMES or requested[1] not in _OPT_M2_SCHEMES:
             return False
-        if not grad.is_contiguous() or ("step" in state and not isinstance(state["step"], int)):
+        if not p.is_contiguous() or not grad.is_contiguous():
+            return False
+        if "step" in state and not isinstance(state["step"], int):
+            return False
+        if not all(self._moment_compatible(state, key, scheme, size, p)
+                   for key, scheme, size in zip(("m1", "m2"), schemes, sizes)):
             return False
         occupied = [_byte_range(p), _byte_range(grad)]
         if _overlaps(occupied[0], occupied[1]):
@@ -686,14 +775,14 @@ class QuantizedAdamW(Optimizer):
         align = _lib.BLOCK if any(s != "fp32" for s in schemes) else 1
         return limit // align * align
 
-    def _prepare(self, p: torch.Tensor, group, keep: List[torch.Tensor], written: List[torch.Tensor],
-                 info: Optional[list] = None) -> Tuple:
+    def _preflight(self, p: torch.Tensor, group) -> "_Checked":
+        """Everything that can reject this parameter, checked without changing its state."""
         if not p.is_cuda:
             raise NotImplementedError("the fused 4-bit step runs on HIP devices only; move the parameters to the GPU")
         if p.dtype not in _DTYPES:
             raise NotImplementedError(f"parameter dtype {p.dtype} (supported: float32, bfloat16, float16)")
-        if p.layout != torch.strided or not p.is_contiguous():
-            raise NotImplementedError("the fused step updates contiguous dense parameters in place")
+        if p.layout != torch.strided:
+            raise NotImplementedError("the fused step updates dense (strided) parameters in place")
         grad = p.grad
         if grad.layout != torch.strided or grad.dtype not in _DTYPES or grad.device != p.device:
             raise NotImplementedError("gradients must be dense float32/bfloat16/float16 tensors on the parameter's device")
@@ -704,15 +793,31 @@ class QuantizedAdamW(Optimizer):
         sizes = tuple(group["block_size"] if group["block_size"] is not None else default_block_size(m)
                       for m in requested)
         schemes = tuple(self._effective_scheme(p, m, s) for m, s in zip(requested, sizes))
-        optimized = self._plan_accepts(p, grad, group, requested, schemes, state)
+        optimized = self._plan_accepts(p, grad, group, requested, sizes, schemes, state)
+        if "step" in state:
+            for moment, scheme in zip(("m1", "m2"), schemes):
+                self._check_moment(p, state, moment, scheme)
+        # Streams are opened (and checkpointed streams restored) before any state changes, so a
+        # restore failure leaves every parameter untouched (_optimized.py:157-158).
+        for moment in ("m1", "m2"):
+            self._stream(moment, p.device)
+        return _Checked(p, group, grad, state, schemes, sizes, optimized)
+
+    def _prepare(self, c: "_Checked", batch: "_DeviceBatch") -> None:
+        """State initialisation, step count and the launch-table row of one checked parameter."""
+        p, group, grad, state, schemes, sizes, optimized = (c.param, c.group, c.grad, c.state, c.schemes, c.sizes,
+                                                             c.optimized)
         if optimized:
             group.setdefault(_CHUNK_KEY, _CHUNK_NUMEL)
         else:
-            # The reference step writes fresh tensors: detach aliased state and gradients.
+            # The reference step writes fresh tensors: detach state and gradients that alias the
+            # parameter, each other, or what an earlier row of this launch writes in place (state
+            # shared between parameters after a checkpoint load, _optimized.py:53-83).
             occupied = [_byte_range(p)]
             if _overlaps(occupied[0], _byte_range(grad)):
                 grad = grad.clone()
             occupied.append(_byte_range(grad))
+            occupied.extend(batch.occupied)
             for key in ("m1", "m2", "m1_code", "m2_code", PENDING_KEY):
                 value = state.get(key)
                 if isinstance(value, torch.Tensor):
@@ -727,11 +832,13 @@ class QuantizedAdamW(Optimizer):
                     occupied.append(_byte_range(meta.absmax))
         if not grad.is_contiguous():
             grad = grad.contiguous()
-        keep.append(grad)
-        # Streams are opened (and checkpointed streams restored) before any state
-        # changes, so a restore failure leaves the parameter untouched (_optimized.py:157-158).
-        self._quant_generator("m1", p.device)
-        self._quant_generator("m2", p.device)
+        target = p
+        if not p.is_contiguous():
+            # The reference step updates a strided parameter element by element in logical order;
+            # the kernel updates a contiguous copy in that order, which is copied back after it.
+            target = p.detach().contiguous()
+            batch.copy_back.append((p, target))
+        c.staged = target is not p
 
         n = p.numel()
         if "step" not in state:
@@ -742,17 +849,18 @@ class QuantizedAdamW(Optimizer):
             state["step"] = 0
         else:
             for moment, scheme in zip(("m1", "m2"), schemes):
-                self._check_moment(p, state, moment, scheme)
+                self._normalize_moment(p, state, moment, scheme)
         state["step"] = int(state["step"]) + 1
         step = state["step"]
 
-        c = _step_constants(group, step, schemes[1])
-        flags = c.lerp_flags
-        if _vec_aligned(p, grad):
+        c_ = _step_constants(group, step, schemes[1])
+        flags = c_.lerp_flags
+        if _vec_aligned(target, grad):
             flags |= _lib.TENSOR_VEC_ALIGNED
-        m1 = self._moment_row(p, state, "m1", schemes[0], False, optimized, 1.0, 1e-8, keep, written)
+        refs = {_COL["param"]: batch.ref("p", target), _COL["grad"]: batch.ref("r", grad)}
+        m1 = self._moment_row(p, state, "m1", schemes[0], False, optimized, 1.0, 1e-8, batch, refs)
         m2 = self._moment_row(p, state, "m2", schemes[1], group["use_eden_m2"], optimized,
-                              c.storage_bias, group["eps"], keep, written)
+                              c_.storage_bias, group["eps"], batch, refs)
         if schemes[1] in LOOKAHEAD_SCHEMES:
             # adamw.py:566-614: the pending form samples the fp32 state with bias_c2 before the
             # update; the proxies encode the new m2 for the next step's bias correction.
@@ -765,19 +873,20 @@ class QuantizedAdamW(Optimizer):
             # Reads with the scale before EDEN; stores the calibrated scale and 1/denominator.
             pre = state.get("m2_read_preconditioner")
             if not (isinstance(pre, torch.Tensor) and pre.shape == p.shape and pre.dtype == torch.float32
-                    and pre.device == p.device and pre.is_contiguous()):
+                    and pre.device == p.device and pre.is_contiguous() and pre.data_ptr() % 16 == 0):
                 pre = state["m2_read_preconditioner"] = torch.empty(p.shape, dtype=torch.float32, device=p.device)
-            written.append(pre)
-            m2 = m2[:2] + (pre.data_ptr(),) + m2[3:8] + (
-                m2[8] | _lib.MOMENT_SAMPLED_READ | _lib.MOMENT_READ_RAW_SCALE | _lib.MOMENT_EDEN,) + m2[9:]
+            refs[_COL["m2.values"]] = batch.ref("w", pre)
+            m2 = m2[:8] + (m2[8] | _lib.MOMENT_SAMPLED_READ | _lib.MOMENT_READ_RAW_SCALE | _lib.MOMENT_EDEN,) + m2[9:]
         else:
             state.pop("m2_read_preconditioner", None)  # adamw.py:568-686, _optimized.py:156
             if schemes[1] in SAMPLED_READ_SCHEMES:
                 m2 = m2[:8] + (m2[8] | _lib.MOMENT_SAMPLED_READ,) + m2[9:]
-        if info is not None:
-            info.append((p, optimized, schemes))
-        return (p.data_ptr(), grad.data_ptr(), 0, n, _DTYPES[p.dtype], _DTYPES[grad.dtype], flags,
-                c.w1, c.w2, c.decay, c.step_coef, c.bc2_sqrt, c.bc2_sqrt_rcp, c.eps, m1, m2)
+        batch.rows.append((0, 0, 0, n, _DTYPES[p.dtype], _DTYPES[grad.dtype], flags, c_.w1, c_.w2, c_.decay,
+                           c_.step_coef, c_.bc2_sqrt, c_.bc2_sqrt_rcp, c_.eps, m1, m2))
+        batch.refs.append(refs)
+        pre = state.get("m2_read_preconditioner")
+        batch.occupied.extend(_byte_range(t) for t in [target] + _moment_tensors(state)
+                              + ([pre] if isinstance(pre, torch.Tensor) else []))
 
     def _init_moment(self, p, state, moment, scheme, size, eden, chunk) -> None:
         """Zero state (``_moment_buffer.py:89-126`` / ``adamw.py:524-545``)."""
@@ -802,7 +911,8 @@ class QuantizedAdamW(Optimizer):
             self._stream(moment, p.device).advance(tile)
 
     def _check_moment(self, p, state, moment, scheme) -> None:
-        """Accept existing state in the layout the kernel writes (``_moment_buffer.py:54-87,127-141``)."""
+        """Reject existing state the kernel cannot step (``_moment_buffer.py:54-87,127-141``); changes
+        nothing (``_normalize_moment`` then brings accepted state into the kernel's layout)."""
         n = p.numel()
         if scheme == "fp32" or scheme in PENDING_LOOKAHEAD_SCHEMES:
             key = moment if scheme == "fp32" else PENDING_KEY
@@ -812,39 +922,56 @@ class QuantizedAdamW(Optimizer):
             if not (isinstance(value, torch.Tensor) and value.device == p.device and value.dtype == torch.float32
                     and value.numel() == n):
                 raise ValueError(f"{key}: fp32 state does not match the parameter")
-            if not value.is_contiguous():
-                state[key] = value.contiguous()
             return
         codes = state.get(f"{moment}_code")
         meta = state.get(f"{moment}_quant_state")
         if not isinstance(codes, torch.Tensor) or not isinstance(meta, QuantState):
             raise NotImplementedError(f"{moment}: fp32 state found where the scheme is quantized")
+        if not isinstance(meta.absmax, torch.Tensor):
+            raise ValueError(f"{moment}: quantization scales must be a tensor")
         if meta.blocksize != _lib.BLOCK or meta.absmax.numel() != n // _lib.BLOCK:
             raise NotImplementedError(f"{moment}: block size {meta.blocksize} state")
         if codes.dtype != torch.uint8 or codes.device != p.device:
             raise ValueError(f"{moment}: codes must be uint8 on {p.device}")
+        legacy = codes.numel() == n and not getattr(meta, "packed", False)
+        if not legacy and codes.numel() != (n + 1) // 2:
+            raise ValueError(f"{moment}: {codes.numel()} code bytes for {n} values")
+
+    def _normalize_moment(self, p, state, moment, scheme) -> None:
+        """Bring state that ``_check_moment`` accepted into the kernel's layout: contiguous, on the
+        parameter's device, packed codes (legacy unpacked codes are repacked), codes 8-byte and
+        fp32 values 16-byte aligned (the kernel's vector accesses)."""
+        if scheme == "fp32" or scheme in PENDING_LOOKAHEAD_SCHEMES:
+            key = moment if scheme == "fp32" else PENDING_KEY
+            value = state[key]
+            if not value.is_contiguous() or value.data_ptr() % 16:
+                state[key] = value.contiguous() if not value.is_contiguous() else value.clone()
+            return
+        codes = state[f"{moment}_code"]
+        meta = state[f"{moment}_quant_state"]
+        n = p.numel()
         if meta.absmax.device != p.device or meta.absmax.dtype != torch.float32 or not meta.absmax.is_contiguous():
             meta.absmax = meta.absmax.to(device=p.device, dtype=torch.float32).contiguous()
         if codes.numel() == n and not getattr(meta, "packed", False):
             codes = pack_4bit_codes(codes.reshape(-1))  # legacy unpacked codes
-        elif codes.numel() != (n + 1) // 2:
-            raise ValueError(f"{moment}: {codes.numel()} code bytes for {n} values")
         if not codes.is_contiguous():
             codes = codes.contiguous()
+        if codes.data_ptr() % 8:
+            codes = codes.clone()
         state[f"{moment}_code"] = codes
         meta.packed = True
 
-    def _moment_row(self, p, state, moment, scheme, eden, optimized, bias, eps, keep, written) -> Tuple:
+    def _moment_row(self, p, state, moment, scheme, eden, optimized, bias, eps, batch, refs) -> Tuple:
+        """The ``aw4_moment`` fields of one moment (addresses 0: ``refs`` names their tensors)."""
         n = p.numel()
         if scheme == "fp32":
-            written.append(state[moment])
-            return (0, 0, state[moment].data_ptr(), 0, 0, 0, 0, _lib.ROUND_FP32, 0, 1.0, 1.0, _f32(1e-8),
-                    0.0, 0.0, 0.0, 0.0)
+            refs[_COL[f"{moment}.values"]] = batch.ref("w", state[moment])
+            return (0, 0, 0, 0, 0, 0, 0, _lib.ROUND_FP32, 0, 1.0, 1.0, _f32(1e-8), 0.0, 0.0, 0.0, 0.0)
         codebook, rounding, floor_zero = SCHEMES[scheme]
         flags = (_lib.MOMENT_ZERO_FLOOR if floor_zero else 0) | (_lib.MOMENT_EDEN if eden else 0)
         if optimized:
             flags |= _lib.MOMENT_GUARDS
-        seed = offset = draws = 0
+        seed = offset = 0
         if rounding in _SR_ROUNDINGS:
             stream = self._stream(moment, p.device)
             seed, offset = stream.seed, stream.take(n)
@@ -855,29 +982,103 @@ class QuantizedAdamW(Optimizer):
                 if u.dtype != dtype or u.numel() != n or u.device != p.device:
                     raise ValueError(f"draw provider must return n {dtype} uniforms on the parameter's device")
                 u = u.contiguous()
-                keep.append(u)
-                draws = u.data_ptr()
+                if u.data_ptr() % 16:
+                    u = u.clone()
+                refs[_COL[f"{moment}.draws"]] = batch.ref("r", u)
                 flags |= _lib.MOMENT_EXT_DRAWS
         sr_bias = _f32(max(float(bias), 1e-12))
         if scheme in PENDING_LOOKAHEAD_SCHEMES:
-            written.append(state[PENDING_KEY])
-            return (0, 0, state[PENDING_KEY].data_ptr(), draws, seed, offset, codebook, rounding,
-                    flags | _lib.MOMENT_PENDING, sr_bias, _rcp32(sr_bias), _f32(eps), 0.0, 0.0, 0.0, 0.0)
-        written.append(state[f"{moment}_code"])
-        written.append(state[f"{moment}_quant_state"].absmax)
-        return (state[f"{moment}_code"].data_ptr(), state[f"{moment}_quant_state"].absmax.data_ptr(), 0, draws,
-                seed, offset, codebook, rounding, flags, sr_bias, _rcp32(sr_bias), _f32(eps), 0.0, 0.0, 0.0, 0.0)
+            refs[_COL[f"{moment}.values"]] = batch.ref("w", state[PENDING_KEY])
+            return (0, 0, 0, 0, seed, offset, codebook, rounding, flags | _lib.MOMENT_PENDING, sr_bias,
+                    _rcp32(sr_bias), _f32(eps), 0.0, 0.0, 0.0, 0.0)
+        refs[_COL[f"{moment}.codes"]] = batch.ref("w", state[f"{moment}_code"])
+        refs[_COL[f"{moment}.scales"]] = batch.ref("w", state[f"{moment}_quant_state"].absmax)
+        return (0, 0, 0, 0, seed, offset, codebook, rounding, flags, sr_bias, _rcp32(sr_bias), _f32(eps),
+                0.0, 0.0, 0.0, 0.0)
+
+
+# Column of each address field in a launch record's ``refs`` (adamw4bit_amd._ops.ADDRESS_FIELDS).
+_COL = {".".join(path): k for k, path in enumerate(_ops.ADDRESS_FIELDS)}
+
+
+class _Checked:
+    """A parameter that passed ``_preflight``: what its step will do."""
+
+    __slots__ = ("param", "group", "grad", "state", "schemes", "sizes", "optimized", "staged")
+
+    def __init__(self, param, group, grad, state, schemes, sizes, optimized):
+        self.param, self.group, self.grad, self.state = param, group, grad, state
+        self.schemes, self.sizes, self.optimized = schemes, sizes, optimized
+        self.staged = False
+
+
+class _DeviceBatch:
+    """The rows of one device's launch and the tensors their addresses point into."""
+
+    __slots__ = ("rows", "refs", "params", "written", "read", "copy_back", "occupied")
+
+    def __init__(self):
+        self.occupied: list = []  # byte ranges the rows so far write in place
+        self.rows: List[Tuple] = []
+        self.refs: List[Dict[int, Tuple[str, int]]] = []  # per row: column -> (list, index)
+        self.params: List[torch.Tensor] = []   # updated in place
+        self.written: List[torch.Tensor] = []  # moment state, updated in place
+        self.read: List[torch.Tensor] = []     # gradients, clip coefficient, caller draws
+        self.copy_back: List[Tuple[torch.Tensor, torch.Tensor]] = []  # (strided parameter, its staged copy)
+
+    def ref(self, kind: str, tensor: torch.Tensor) -> Tuple[str, int]:
+        target = self.params if kind == "p" else self.written if kind == "w" else self.read
+        target.append(tensor)
+        return kind, len(target) - 1
+
+    def launch(self, coef: Optional[torch.Tensor]) -> Tuple:
+        """The launch record: (params, written, read, table, refs, copy_back), the table a CPU uint8
+        tensor of rows with every address filled in, refs its (rows, fields) int64 references."""
+        table = np.array(self.rows, dtype=_lib.TENSOR)
+        if coef is not None:
+            k = self.ref("r", coef)
+            for r in self.refs:
+                r[_COL["grad_scale"]] = k
+            table["flags"] |= _lib.TENSOR_GRAD_SCALE
+        base = {"p": 0, "w": len(self.params), "r": len(self.params) + len(self.written)}
+        refs = np.full((len(self.rows), len(_ops.ADDRESS_FIELDS)), -1, dtype=np.int64)
+        for i, row in enumerate(self.refs):
+            for col, (kind, index) in row.items():
+                refs[i, col] = base[kind] + index
+        _ops.resolve_addresses(table, refs, self.params + self.written + self.read)
+        return (self.params, self.written, self.read, torch.from_numpy(table.view(np.uint8)),
+                torch.from_numpy(refs), self.copy_back)
+
+
+class _StepUndo:
+    """What preparing a step changes before it launches: the state entries of its parameters
+    (and the scales and packing flag of their QuantStates), and every random stream's position."""
+
+    def __init__(self, opt: "QuantizedAdamW", states: List[Dict[str, Any]]):
+        self.states = [(st, dict(st), [(q, q.absmax, q.packed) for q in st.values() if isinstance(q, QuantState)])
+                       for st in states]
+        self.streams = [(s, s.offset) for s in opt._all_streams()]
+
+    def restore(self) -> None:
+        for st, saved, quants in self.states:
+            st.clear()
+            st.update(saved)
+            for q, absmax, packed in quants:
+                q.absmax, q.packed = absmax, packed
+        for s, offset in self.streams:
+            s.offset = offset
 
 
 class _LaunchPlan:
     """Launch tables of the last full step, reused by the next steps while only per-step values
     change: gradient addresses, step counts, the fp32 step constants (one per group and step,
     computed by the same code as the full path), random-stream positions and the update-SR
-    storage bias.  Any structural change -- other parameters with gradients, new state
+    storage bias.  Any structural change -- other parameters with gradients, a parameter whose
+    storage, dtype, size or layout changed (``p.data = ...``, ``module.to(dtype)``), new state
     objects, other schemes or chunking in a group, an m1 retarget, a checkpoint load, a draw
-    provider, a gradient that is not contiguous or overlaps its parameter or state -- sends
-    the step through the full path, which rebuilds the plan.  (A gradient always has its
-    parameter's dtype, shape and device: the ``.grad`` setter enforces it.)
+    provider, a gradient that is not contiguous or overlaps its parameter or state -- sends the
+    step through the full path, which rebuilds the plan.  (A gradient always has its parameter's
+    dtype, shape and device: the ``.grad`` setter enforces it.)
     """
 
     _STRUCTURE_KEYS = ("m1_quant_scheme", "m2_quant_scheme", "use_eden_m2", "block_size", _CHUNK_KEY)
@@ -888,7 +1089,9 @@ class _LaunchPlan:
     def __init__(self):
         self.groups: list = []     # (group, structure, parameter count)
         self.params: List[torch.Tensor] = []
-        self.devices: list = []    # per device: table, params, written, rows
+        self.pdtypes: list = []    # each parameter's dtype, numel at build time
+        self.pnumel: list = []
+        self.devices: list = []    # per device: see build
         # what the tables were built from, checked by identity each step, as parallel lists:
         # (params, their state dicts), (state dict, key, value) for every state key,
         # (QuantState, its absmax tensor)
@@ -897,17 +1100,18 @@ class _LaunchPlan:
         self.quant_refs: Tuple[list, list] = ([], [])
 
     @classmethod
-    def build(cls, opt: "QuantizedAdamW", per_device, tables, info) -> Optional["_LaunchPlan"]:
-        if opt._draw_provider is not None or any(schemes[1] in LOOKAHEAD_SCHEMES for _, _, schemes in info):
+    def build(cls, opt: "QuantizedAdamW", batches: List[_DeviceBatch], checked: List[_Checked]):
+        if opt._draw_provider is not None or any(c.schemes[1] in LOOKAHEAD_SCHEMES or c.staged for c in checked):
             return None  # lookahead rows carry per-step constants the plan does not refresh
         plan = cls()
-        meta = {id(p): schemes for p, _, schemes in info}
+        meta = {id(c.param): c.schemes for c in checked}
         group_of = {}
         for gi, group in enumerate(opt.param_groups):
             plan.groups.append((group, tuple(group.get(k) for k in cls._STRUCTURE_KEYS), len(group["params"])))
             for p in group["params"]:
                 group_of[id(p)] = gi
-        for device, (rows, params, written, read) in per_device.items():
+        for batch in batches:
+            params = batch.params
             n = len(params)
             lo = np.zeros((n, cls._MAX_RANGES), dtype=np.int64)
             hi = np.zeros((n, cls._MAX_RANGES), dtype=np.int64)
@@ -932,7 +1136,7 @@ class _LaunchPlan:
                 sr = tuple((moment, opt._stream(moment, p.device))
                            for moment, scheme in (("m1", schemes[0]), ("m2", schemes[1]))
                            if scheme != "fp32" and SCHEMES[scheme][1] in _SR_ROUNDINGS)
-                entries.append((p, state, None, group_of[id(p)], schemes[1], sr, p.numel()))
+                entries.append((state, group_of[id(p)], schemes[1], sr, p.numel()))
                 plan.owners[0].append(p)
                 plan.owners[1].append(state)
                 for k in cls._STATE_KEYS + (_FALLBACK_KEY,):
@@ -943,14 +1147,33 @@ class _LaunchPlan:
                     if isinstance(q, QuantState):
                         plan.quant_refs[0].append(q)
                         plan.quant_refs[1].append(q.absmax)
-            table = tables[device]
+            table = np.array(batch.rows, dtype=_lib.TENSOR)
+            refs = np.full((n, len(_ops.ADDRESS_FIELDS)), -1, dtype=np.int64)
+            # the plan's read list is [p.grad for p in params] (+ the clip coefficient)
+            n_p, n_w = n, len(batch.written)
+            base = {"p": 0, "w": n_p, "r": n_p + n_w}
+            for i, row in enumerate(batch.refs):
+                for col, (kind, index) in row.items():
+                    if col == _COL["grad_scale"]:
+                        continue  # set per step
+                    if kind == "r":
+                        if col != _COL["grad"]:
+                            return None  # caller draws: never planned (draw provider)
+                        refs[i, col] = base["r"] + i
+                    else:
+                        refs[i, col] = base[kind] + index
+            _ops.resolve_addresses(table, refs, list(params) + list(batch.written) + [p.grad for p in params])
             gbytes = np.array([p.numel() * p.element_size() for p in params], dtype=np.int64)
+            pptr = np.array([p.data_ptr() for p in params], dtype=np.int64)
             pvec = np.array([p.data_ptr() % (4 * p.element_size()) == 0 for p in params], dtype=bool)
             gvec = np.array([4 * p.element_size() for p in params], dtype=np.int64)
             qrows = np.flatnonzero(table["m2"]["rounding"] != _lib.ROUND_FP32)
-            plan.devices.append((table, list(params), list(written), entries, lo, hi, gbytes, pvec, gvec,
-                                 table.view(_STEP_FIELDS), qrows))
+            plan.devices.append((table, list(params), list(batch.written), entries, lo, hi, gbytes, pptr, pvec, gvec,
+                                 table.view(_STEP_FIELDS), qrows, refs, torch.from_numpy(table.view(np.uint8)),
+                                 torch.from_numpy(refs)))
             plan.params.extend(params)
+            plan.pdtypes.extend(p.dtype for p in params)
+            plan.pnumel.extend(p.numel() for p in params)
         return plan
 
     def _valid(self, opt: "QuantizedAdamW"):
@@ -958,6 +1181,7 @@ class _LaunchPlan:
         if opt._draw_provider is not None or len(self.groups) != len(opt.param_groups):
             return None
         params = self.params
+        dtypes = self.pdtypes
         i = 0
         n = len(params)
         strided = torch.strided
@@ -970,10 +1194,13 @@ class _LaunchPlan:
                 g = p.grad
                 if g is None:
                     continue
-                if i >= n or p is not params[i] or g.layout != strided or not g.is_contiguous():
+                if (i >= n or p is not params[i] or p.dtype is not dtypes[i] or g.layout != strided
+                        or not g.is_contiguous() or not p.is_contiguous()):
                     return None
                 i += 1
         if i != n:
+            return None
+        if list(map(torch.Tensor.numel, params)) != self.pnumel:
             return None
         # identity checks in C-level loops (map/all): about 1,300 of them for 148 parameters
         state_map = opt.state
@@ -989,7 +1216,13 @@ class _LaunchPlan:
         if not all(map(operator.is_, map(operator.attrgetter("absmax"), quant), absmax)):
             return None
         out = []
-        for table, dparams, written, entries, lo, hi, gbytes, pvec, gvec, _, _ in self.devices:
+        for dev in self.devices:
+            dparams, lo, hi, gbytes, pptr = dev[1], dev[4], dev[5], dev[6], dev[7]
+            # the parameters' storage is still where the tables point (p.data can be swapped
+            # without changing the Parameter object)
+            if not np.array_equal(np.fromiter(map(torch.Tensor.data_ptr, dparams), dtype=np.int64,
+                                              count=len(dparams)), pptr):
+                return None
             g0 = np.fromiter((p.grad.data_ptr() for p in dparams), dtype=np.int64, count=len(dparams))
             g1 = g0 + gbytes
             if bool(((lo < g1[:, None]) & (g0[:, None] < hi)).any()):
@@ -997,20 +1230,24 @@ class _LaunchPlan:
             out.append(g0)
         return out
 
-    def step(self, opt: "QuantizedAdamW") -> bool:
-        """Launch the step from the cached tables; False (nothing changed) if the plan is stale."""
+    def prepare(self, opt: "QuantizedAdamW"):
+        """Launch records and ``finish`` of the step from the cached tables (as
+        ``QuantizedAdamW._prepare_launches``), or None (nothing changed) if the plan is stale."""
         grads = self._valid(opt)
         if grads is None:
-            return False
+            return None
+        saved_steps = [(state, state["step"]) for dev in self.devices for state, *_ in dev[3]]
+        saved_streams = [(s, s.offset) for s in opt._all_streams()]
         # one _StepConstants per (group, step, m2 scheme): the update-SR storage bias depends on
         # the tensor's m2 scheme (an fp32-state tensor of a group has the fp32 scheme)
         constants: Dict[Tuple[int, int, str], int] = {}
         consts: List[_StepConstants] = []
-        for (table, params, written, entries, lo, hi, gbytes, pvec, gvec, fields, qrows), g0 in zip(self.devices,
-                                                                                                      grads):
+        launches = []
+        for (table, params, written, entries, lo, hi, gbytes, pptr, pvec, gvec, fields, qrows, refs, table_t,
+             refs_t), g0 in zip(self.devices, grads):
             index = np.empty(len(entries), dtype=np.intp)
             offsets = {"m1": fields["m1_rng_offset"].copy(), "m2": fields["m2_rng_offset"].copy()}
-            for i, (p, state, _, gi, m2_scheme, sr, numel) in enumerate(entries):
+            for i, (state, gi, m2_scheme, sr, numel) in enumerate(entries):
                 step = state["step"] + 1
                 state["step"] = step
                 k = constants.get((gi, step, m2_scheme))
@@ -1039,8 +1276,19 @@ class _LaunchPlan:
             read = [p.grad for p in params]
             if coef is not None:
                 read.append(coef)
-            _launch(params, written, read, table)
-        return True
+            refs[:, _COL["grad_scale"]] = -1 if coef is None else len(params) + len(written) + len(params)
+            launches.append((params, written, read, table_t, refs_t, []))
+
+        def finish(done: int, total: int) -> None:
+            if done == total:
+                opt._grad_clip = None
+            elif done == 0:
+                for state, step in saved_steps:
+                    state["step"] = step
+                for s, offset in saved_streams:
+                    s.offset = offset
+
+        return launches, finish
 
 
 class AdamW8bit(QuantizedAdamW):

@@ -474,8 +474,9 @@ int check_moment(const aw4_moment& m, int64_t numel, int index, const char* name
     } else {
         if (!m.codes || !m.scales)
             return set_error(AW4_EINVAL, "tensor %d: %s quantized without codes/scales", index, name);
-        if (!aligned(m.codes, 2) || !aligned(m.scales, 4))
-            return set_error(AW4_EALIGN, "tensor %d: %s codes/scales misaligned", index, name);
+        // codes: each lane stores its 16 codes as one 8-byte word
+        if (!aligned(m.codes, 8) || !aligned(m.scales, 4))
+            return set_error(AW4_EALIGN, "tensor %d: %s codes not 8-byte or scales not 4-byte aligned", index, name);
     }
     if (m.rounding != AW4_ROUND_RTN) {
         if (m.flags & AW4_MOMENT_EXT_DRAWS) {
@@ -551,8 +552,11 @@ std::vector<LaunchGroup> plan_launches(const aw4_tensor* ts, int32_t count) {
         const bool research_tensor = research_m2(t.m2);
         const int s1 = mspec(t.m1.rounding, t.m1.flags & spec_flags_mask(t.m1.rounding));
         const int s2 = mspec(t.m2.rounding, t.m2.flags & spec_flags_mask(t.m2.rounding));
+        // Specialised kernels access parameters and gradients as 4-value vectors; a row whose
+        // addresses do not allow that (a view at an odd offset into a flat buffer) runs the
+        // generic kernel, which reads the flag at run time.
         int v = kGenericVariant;
-        if (t.param_dtype == t.grad_dtype)
+        if (t.param_dtype == t.grad_dtype && (t.flags & AW4_TENSOR_VEC_ALIGNED))
             for (int k = 0; k < kNumSpecialised; ++k)
                 if (kVariants[k].dtype == t.param_dtype && kVariants[k].m1 == s1 && kVariants[k].m2 == s2) {
                     v = k;
@@ -653,6 +657,88 @@ int acquire_slot(DeviceState* ds, size_t bytes, StagingSlot** out) {
     return AW4_OK;
 }
 
+// One step's launches: the kernel groups and where each group's table sits in the staged bytes.
+struct StepLaunch {
+    std::vector<LaunchGroup> plan;
+    std::vector<size_t> offset;
+    std::vector<int64_t> grid;
+    size_t bytes = 0;
+};
+
+// Validate the rows and plan the launches (no device work, no lock needed).
+int prepare_step(const aw4_tensor* tensors, int32_t count, StepLaunch& sl) {
+    if (count < 0 || (count > 0 && !tensors)) return set_error(AW4_EINVAL, "aw4_fused_step: bad tensor list");
+    if (count == 0) return AW4_OK;
+    for (int i = 0; i < count; ++i) {
+        const int rc = check_tensor(tensors[i], i);
+        if (rc) return rc;
+    }
+    sl.plan = plan_launches(tensors, count);
+    // Launch table of each group, 256-byte aligned: header, tensors[n], tile_start[n + 1].
+    sl.offset.resize(sl.plan.size());
+    sl.grid.assign(sl.plan.size(), 0);
+    sl.bytes = 0;
+    for (size_t g = 0; g < sl.plan.size(); ++g) {
+        const size_t n = sl.plan[g].members.size();
+        sl.offset[g] = sl.bytes;
+        sl.bytes += (sizeof(StepHeader) + sizeof(aw4_tensor) * n + sizeof(int64_t) * (n + 1) + 255) & ~(size_t)255;
+    }
+    return AW4_OK;
+}
+
+// Write each group's launch table into `dst` (host memory of sl.bytes) and set its grid.
+//
+// A few tiles per wave and a grid covering all of them: the hardware dispatcher hands each free
+// slot the next workgroup, so the tiles in flight stay a narrow, moving window of the index
+// space (HBM page locality) and no CU waits on a static share at the end.  Measured on MI355X
+// against persistent grids of contiguous per-wave ranges, which stream from thousands of
+// far-apart addresses at once and leave a load-imbalance tail.  The kernel picks which tiles a
+// wave takes (consecutive ones, or one per grid-sized stride); either way the grid is
+// ceil(tiles / tiles per wave) waves.
+int fill_step_tables(const aw4_tensor* tensors, StepLaunch& sl, int num_cus, void* dst) {
+    for (size_t g = 0; g < sl.plan.size(); ++g) {
+        const LaunchGroup& lg = sl.plan[g];
+        const int n = (int)lg.members.size();
+        StepHeader* h = (StepHeader*)((char*)dst + sl.offset[g]);
+        memset(h, 0, sizeof(*h));
+        aw4_tensor* rows = (aw4_tensor*)(h + 1);
+        int64_t* starts = (int64_t*)(rows + n);
+        int64_t acc = 0;
+        for (int k = 0; k < n; ++k) {
+            rows[k] = tensors[lg.members[k]];
+            starts[k] = acc;
+            acc += (rows[k].numel + kWaveTile - 1) / kWaveTile;
+        }
+        starts[n] = acc;
+        // Small launches take fewer tiles per wave so that their waves still spread over every
+        // CU: 4 tiles per wave from 128 tiles per CU, 2 from 8, else 1 (measured on one 4096^2
+        // and one 1024^2 tensor, and the GPT-2-small list).
+        const int64_t per_cu = acc / (int64_t)num_cus;
+        const int tiles_per_wave = per_cu >= 128 ? kTilesPerWave : per_cu >= 8 ? 2 : 1;
+        const int64_t waves = (acc + tiles_per_wave - 1) / tiles_per_wave;
+        sl.grid[g] = (waves + kWavesPerGroup - 1) / kWavesPerGroup;
+        if (sl.grid[g] > 0x7fffffff)
+            return set_error(AW4_EINVAL, "aw4_fused_step: %lld tiles exceed one launch", (long long)acc);
+        h->count = n;
+        h->cb1 = lg.cb1; h->lut1 = lg.lut1; h->cb2 = lg.cb2; h->lut2 = lg.lut2;
+        h->total_tiles = acc;
+        h->tiles_per_wave = tiles_per_wave;
+    }
+    return AW4_OK;
+}
+
+// Launch every group whose table is at dev_base + offset.
+int launch_step(const StepLaunch& sl, const char* dev_base, const Tables* tables, hipStream_t s) {
+    for (size_t g = 0; g < sl.plan.size(); ++g) {
+        if (sl.grid[g] == 0) continue;
+        const StepHeader* dh = (const StepHeader*)(dev_base + sl.offset[g]);
+        void* args[] = {(void*)&dh, (void*)&tables};
+        AW4_HIP_CHECK(hipLaunchKernel(kVariants[sl.plan[g].variant].fn, dim3((unsigned)sl.grid[g]), dim3(kThreads),
+                                      args, 0, s));
+    }
+    return AW4_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -673,78 +759,24 @@ int64_t aw4_encode_tables(void* out, int64_t bytes) {
 
 int aw4_fused_step(const aw4_tensor* tensors, int32_t count, void* stream) {
     g_error.clear();
-    if (count < 0 || (count > 0 && !tensors)) return set_error(AW4_EINVAL, "aw4_fused_step: bad tensor list");
-    if (count == 0) return AW4_OK;
-    for (int i = 0; i < count; ++i) {
-        const int rc = check_tensor(tensors[i], i);
-        if (rc) return rc;
-    }
-    const std::vector<LaunchGroup> plan = plan_launches(tensors, count);
-    // Launch table of each group, 256-byte aligned: header, tensors[n], tile_start[n + 1].
-    std::vector<size_t> offset(plan.size());
-    size_t bytes = 0;
-    for (size_t g = 0; g < plan.size(); ++g) {
-        const size_t n = plan[g].members.size();
-        offset[g] = bytes;
-        bytes += (sizeof(StepHeader) + sizeof(aw4_tensor) * n + sizeof(int64_t) * (n + 1) + 255) & ~(size_t)255;
-    }
-
+    StepLaunch sl;
+    int rc = prepare_step(tensors, count, sl);
+    if (rc || sl.plan.empty()) return rc;
     std::lock_guard<std::mutex> lock(g_mutex);
     DeviceState* ds = nullptr;
-    int rc = device_state(&ds);
+    rc = device_state(&ds);
     if (rc) return rc;
     StagingSlot* sp = nullptr;
-    rc = acquire_slot(ds, bytes, &sp);
+    rc = acquire_slot(ds, sl.bytes, &sp);
     if (rc) return rc;
     StagingSlot& slot = *sp;
-
-    // A few tiles per wave and a grid covering all of them: the hardware dispatcher hands
-    // each free slot the next workgroup, so the tiles in flight stay a narrow, moving window
-    // of the index space (HBM page locality) and no CU waits on a static share at the end.
-    // Measured on MI355X against persistent grids of contiguous per-wave ranges, which
-    // stream from thousands of far-apart addresses at once and leave a load-imbalance tail.
-    // The kernel picks which tiles a wave takes (consecutive ones, or one per grid-sized
-    // stride); either way the grid is ceil(tiles / tiles per wave) waves.
-    std::vector<int64_t> grid(plan.size());
-    for (size_t g = 0; g < plan.size(); ++g) {
-        const LaunchGroup& lg = plan[g];
-        const int n = (int)lg.members.size();
-        StepHeader* h = (StepHeader*)((char*)slot.host + offset[g]);
-        memset(h, 0, sizeof(*h));
-        aw4_tensor* rows = (aw4_tensor*)(h + 1);
-        int64_t* starts = (int64_t*)(rows + n);
-        int64_t acc = 0;
-        for (int k = 0; k < n; ++k) {
-            rows[k] = tensors[lg.members[k]];
-            starts[k] = acc;
-            acc += (rows[k].numel + kWaveTile - 1) / kWaveTile;
-        }
-        starts[n] = acc;
-        // Small launches take fewer tiles per wave so that their waves still spread over every
-        // CU: 4 tiles per wave from 128 tiles per CU, 2 from 8, else 1 (measured on one 4096^2
-        // and one 1024^2 tensor, and the GPT-2-small list).
-        const int64_t per_cu = acc / (int64_t)ds->num_cus;
-        const int tiles_per_wave = per_cu >= 128 ? kTilesPerWave : per_cu >= 8 ? 2 : 1;
-        const int64_t waves = (acc + tiles_per_wave - 1) / tiles_per_wave;
-        grid[g] = (waves + kWavesPerGroup - 1) / kWavesPerGroup;
-        if (grid[g] > 0x7fffffff)
-            return set_error(AW4_EINVAL, "aw4_fused_step: %lld tiles exceed one launch", (long long)acc);
-        h->count = n;
-        h->cb1 = lg.cb1; h->lut1 = lg.lut1; h->cb2 = lg.cb2; h->lut2 = lg.lut2;
-        h->total_tiles = acc;
-        h->tiles_per_wave = tiles_per_wave;
-    }
-
-    hipStream_t s = (hipStream_t)stream;
-    rc = upload_slot(slot, bytes, s);
+    rc = fill_step_tables(tensors, sl, ds->num_cus, slot.host);
     if (rc) return rc;
-    const Tables* dt = (const Tables*)ds->tables;
-    for (size_t g = 0; g < plan.size(); ++g) {
-        if (grid[g] == 0) continue;
-        const StepHeader* dh = (const StepHeader*)((const char*)slot.dev + offset[g]);
-        void* args[] = {(void*)&dh, (void*)&dt};
-        AW4_HIP_CHECK(hipLaunchKernel(kVariants[plan[g].variant].fn, dim3((unsigned)grid[g]), dim3(kThreads), args, 0, s));
-    }
+    hipStream_t s = (hipStream_t)stream;
+    rc = upload_slot(slot, sl.bytes, s);
+    if (rc) return rc;
+    rc = launch_step(sl, (const char*)slot.dev, ds->tables, s);
+    if (rc) return rc;
     AW4_HIP_CHECK(hipEventRecord(slot.done, s));
     slot.pending = true;
     return AW4_OK;

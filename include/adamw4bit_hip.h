@@ -109,7 +109,7 @@ extern "C" {
  * optimizer.state (_moment_buffer.py:89-142, adamw.py:326-362).
  */
 typedef struct aw4_moment {
-    uint64_t codes;      /* device address, uint8[ceil(numel/2)] or 0 */
+    uint64_t codes;      /* device address, uint8[ceil(numel/2)], 8-byte aligned, or 0 */
     uint64_t scales;     /* device address, float[numel/128] or 0 */
     uint64_t values;     /* device address, float[numel] (fp32 state, or SAMPLED_READ output) or 0 */
     uint64_t draws;      /* device address of numel uniforms (AW4_MOMENT_EXT_DRAWS): float, double for

@@ -279,8 +279,9 @@ def test_aten_elementwise_semantics():
     a = m.abs()
     assert np.array_equal(a.clone().div_(s).numpy(), a.numpy() / np.float32(s))
     # ATen's CPU sqrt (MKL vector math) is not correctly rounded: results are the correctly
-    # rounded square root or 1 ulp below it.  The HIP kernel uses the correctly rounded
-    # square root, so values downstream of a square root agree within 1 ulp per use.
+    # rounded square root or 1 ulp below it.  The kernel's parameter update uses the hardware's
+    # faithful square root (v_sqrt_f32, within 1 ulp), the same precision class, so values
+    # downstream of that square root agree within about 1 ulp per use.
     cr = np.sqrt(a.numpy().astype(np.float64)).astype(np.float32)
     ulps = a.sqrt().numpy().view(np.int32).astype(np.int64) - cr.view(np.int32)
     assert set(np.unique(ulps).tolist()) <= {-1, 0}
@@ -292,7 +293,8 @@ def test_aten_elementwise_semantics():
 
 def test_torch_custom_op_schema_and_argument_checks():
     """The launch is the torch operator adamw4bit_hip::fused_step_: it declares the tensors it
-    writes (parameters, moment states) and reads (gradients, draws), and checks its table."""
+    writes (parameters, moment states) and reads (gradients, draws), and checks its table and
+    address references."""
     import torch
 
     import adamw4bit_amd  # noqa: F401  (registers the operator)
@@ -300,18 +302,52 @@ def test_torch_custom_op_schema_and_argument_checks():
     op = torch.ops.adamw4bit_hip.fused_step_
     schema = str(op.default._schema)
     assert schema.startswith("adamw4bit_hip::fused_step_(Tensor(a0!)[] params, Tensor(a1!)[] states, "
-                             "Tensor[] inputs, Tensor table)")
-    op([], [], [], torch.zeros(0, dtype=torch.uint8))  # nothing to launch
+                             "Tensor[] inputs, Tensor table, Tensor refs)")
+    refs0 = torch.zeros((0, 11), dtype=torch.int64)
+    op([], [], [], torch.zeros(0, dtype=torch.uint8), refs0)  # nothing to launch
     row = _lib.TENSOR.itemsize
     with pytest.raises(ValueError, match="CPU uint8 tensor"):
-        op([torch.zeros(4)], [], [], torch.zeros(row, dtype=torch.float32))
+        op([torch.zeros(4)], [], [], torch.zeros(row, dtype=torch.float32), refs0)
+    with pytest.raises(ValueError, match="CPU int64"):
+        op([torch.zeros(4)], [], [], torch.zeros(row, dtype=torch.uint8), refs0.to(torch.int32))
     with pytest.raises(ValueError, match="HIP devices only"):
-        op([torch.zeros(4)], [], [], torch.zeros(row, dtype=torch.uint8))
+        op([torch.zeros(4)], [], [], torch.zeros(row, dtype=torch.uint8), torch.zeros((1, 11), dtype=torch.int64))
     clip = torch.ops.adamw4bit_hip.clip_coefficient_
     assert str(clip.default._schema).startswith(
         "adamw4bit_hip::clip_coefficient_(Tensor[] grads, Tensor(a1!) out, Tensor table, float max_norm)")
     with pytest.raises(ValueError, match="HIP device"):
         clip([torch.zeros(4)], torch.zeros(2), torch.zeros(row, dtype=torch.uint8), 1.0)
+
+
+def test_operator_takes_addresses_from_its_tensors():
+    """The operator writes each row's address fields from the tensors it receives (reference -1:
+    no buffer), so a copy that functionalization hands it is the memory the kernel writes."""
+    import torch
+
+    from adamw4bit_amd import _ops
+
+    tensors = [torch.zeros(8), torch.zeros(16, dtype=torch.uint8), torch.zeros(4), torch.ones(8)]
+    rows = np.zeros(2, dtype=_lib.TENSOR)
+    rows["numel"] = [8, 8]
+    refs = np.full((2, len(_ops.ADDRESS_FIELDS)), -1, dtype=np.int64)
+    col = {".".join(p): k for k, p in enumerate(_ops.ADDRESS_FIELDS)}
+    refs[0, col["param"]], refs[0, col["grad"]], refs[0, col["m1.codes"]], refs[0, col["m1.scales"]] = 0, 3, 1, 2
+    refs[1, col["param"]], refs[1, col["m2.values"]] = 3, 0
+    rows["param"] = 123  # stale addresses are overwritten
+    _ops.resolve_addresses(rows, refs, tensors)
+    assert rows["param"][0] == tensors[0].data_ptr() and rows["grad"][0] == tensors[3].data_ptr()
+    assert rows["m1"]["codes"][0] == tensors[1].data_ptr() and rows["m1"]["scales"][0] == tensors[2].data_ptr()
+    assert rows["param"][1] == tensors[3].data_ptr() and rows["m2"]["values"][1] == tensors[0].data_ptr()
+    for path in ("grad_scale", "m1.values", "m1.draws", "m2.codes", "m2.scales", "m2.draws"):
+        obj = rows
+        for name in path.split("."):
+            obj = obj[name]
+        assert obj[0] == 0, path
+    assert rows["grad"][1] == 0 and rows["m1"]["codes"][1] == 0 and rows["numel"][1] == 8
+    with pytest.raises(ValueError, match="outside"):
+        _ops.resolve_addresses(rows, np.full_like(refs, 4), tensors)
+    with pytest.raises(ValueError, match="contiguous"):
+        _ops.resolve_addresses(rows, refs, [torch.zeros(4, 4).t()] + tensors[1:])
 
 
 def test_plan_step_view_covers_exactly_the_per_step_fields():
@@ -349,3 +385,4 @@ def test_plan_step_view_covers_exactly_the_per_step_fields():
         written[off:off + dt.itemsize] = True
     assert written.sum() == 8 + 8 + 32 + 12 + 8 + 8
     assert np.array_equal(raw[:, ~written], before[:, ~written])
+

@@ -1,0 +1,361 @@
+"""GPU tests of the host side of the step: which semantics each parameter gets (the optimized
+backend's preflight gates, _optimized.py:85-136), the cached launch plan's validity, atomic
+steps, strided and misaligned parameters, and the compiled path through the torch operator.
+
+Where a gate sends a parameter to the reference step, the check is against a twin optimizer
+with ``optimized=False`` on plain contiguous copies: the same kernel with the reference step's
+stochastic-rounding rules and initial draw count, which the golden trajectories pin."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import adamw4bit_amd as aw
+from adamw4bit_amd import _lib
+from oracle import reference_step as ref
+
+from tests import gpu_helpers as H
+
+pytestmark = pytest.mark.gpu
+
+ARGS = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+
+
+def log(msg):
+    print(msg, flush=True)
+
+
+def same_state(oa, pa, ob, pb, what):
+    """Bit-identical parameters and moment state."""
+    assert torch.equal(H.bits(pa.detach().contiguous()), H.bits(pb.detach().contiguous())), what
+    sa, sb = H.state_of(oa, pa), H.state_of(ob, pb)
+    assert sa.keys() == sb.keys() and sa["step"] == sb["step"], (what, sorted(sa), sorted(sb))
+    for key in sa:
+        if key != "step":
+            assert torch.equal(H.bits(sa[key]), H.bits(sb[key])), (what, key)
+
+
+def _deep_clone(value):
+    if torch.is_tensor(value):
+        return value.clone()
+    if isinstance(value, dict):
+        return {k: _deep_clone(v) for k, v in value.items()}
+    return value
+
+
+def grads_like(shapes, gen, dtype=torch.float32):
+    return [H.heavy_tailed(s, gen).to(dtype).to(H.DEVICE) for s in shapes]
+
+
+# ---------------------------------------------------------------------------
+# The launch plan follows the parameters' storage
+# ---------------------------------------------------------------------------
+
+def test_plan_follows_swapped_parameter_storage():
+    """``p.data`` can change without changing the Parameter object (vector_to_parameters,
+    ``module.to(dtype)``, a manual ``p.data = ...``).  A step after such a swap must update the
+    new storage exactly as a step that rebuilds its tables does; a plan that kept the old
+    addresses would write into freed memory."""
+    log("plan after p.data swaps")
+    shapes = [(256, 512), (768,), (64, 1024)]
+    gen = torch.Generator().manual_seed(31)
+    init = [torch.randn(s, generator=gen) * 0.02 for s in shapes]
+    pa = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
+    pb = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
+    oa = aw.ZIPSRAdamW4Bit(pa, optimized=True, quant_rng_seed=3, **ARGS)
+    ob = aw.ZIPSRAdamW4Bit(pb, optimized=True, quant_rng_seed=3, **ARGS)
+    for k in range(6):
+        if k == 2:
+            # vector_to_parameters: every parameter becomes a view of one new flat buffer
+            for ps in (pa, pb):
+                flat = torch.nn.utils.parameters_to_vector(ps).clone()
+                torch.nn.utils.vector_to_parameters(flat, ps)
+        if k == 4:
+            for ps in (pa, pb):  # a dtype change, as module.to(torch.bfloat16) makes it
+                for p in ps:
+                    p.data = p.data.to(torch.bfloat16)
+        dtype = pa[0].dtype
+        for a, b, g in zip(pa, pb, grads_like(shapes, gen, dtype)):
+            a.grad, b.grad = g.clone(), g.clone()
+        oa.step()
+        ob._launch_plan = None  # always the full path
+        ob.step()
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(pa, pb)):
+            same_state(oa, a, ob, b, (k, i))
+
+
+# ---------------------------------------------------------------------------
+# Parameters that do not allow vector access, strided parameters
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("recipe", ["zeeden", "zipsr"])
+def test_parameter_at_odd_offset_matches_oracle(recipe):
+    """A parameter (and gradient) one element into a flat buffer: its rows cannot take 16-byte
+    vector accesses, so they run the generic kernel; results equal the oracle's."""
+    log(f"parameter at element offset 1 ({recipe})")
+    gen = torch.Generator().manual_seed(8)
+    shape = (96, 256)
+    n = shape[0] * shape[1]
+    init = torch.randn(shape, generator=gen) * 0.02
+    buf = torch.zeros(n + 5, device=H.DEVICE)
+    buf[1:1 + n] = init.reshape(-1).to(H.DEVICE)
+    p = torch.nn.Parameter(buf[1:1 + n].view(shape))  # contiguous, 4 bytes past an aligned address
+    assert p.is_contiguous() and p.data_ptr() % 16 == 4
+    kw = dict(optimized=True, quant_rng_seed=9 if recipe == "zipsr" else None, **ARGS)
+    opt = aw.ZIPSRAdamW4Bit([p], **kw) if recipe == "zipsr" else aw.ZEEDENAdamW4Bit([p], **kw)
+    m2 = "dyn4_upd_sr_fp32read" if recipe == "zipsr" else "dyn4_nz"
+    cpu = [init.clone()]
+    oracle = ref.Oracle(cpu, ref.Hyper(), ["nf4"], [m2], [recipe == "zeeden"], seed=kw["quant_rng_seed"],
+                        draw_fn=H.PhiloxMirror(opt, H.DEVICE))
+    gbuf = torch.zeros(n + 3, device=H.DEVICE)
+    for _ in range(3):
+        g = H.heavy_tailed(shape, gen)
+        gbuf[3:3 + n] = g.reshape(-1).to(H.DEVICE)
+        p.grad = gbuf[3:3 + n].view(shape)
+        opt.step()
+        oracle.step([g])
+    torch.cuda.synchronize()
+    st, ost = H.state_of(opt, p), H.oracle_state((oracle.states[0].m1, oracle.states[0].m2))
+    for key in ost:
+        flips = H.code_mismatch(st[key], ost[key]) if key.endswith("_code") else None
+        if flips is not None:
+            log(f"  {key}: {flips} codes differ")
+            assert flips == 0, key
+        else:
+            assert torch.equal(H.bits(st[key]), H.bits(ost[key])), key
+    H.assert_params_close(p, cpu[0], "odd offset", steps=3)
+    assert float(buf[0]) == 0.0 and bool((buf[1 + n:] == 0).all())  # neighbours untouched
+
+
+def test_strided_parameter_takes_reference_step():
+    """A non-contiguous parameter (a transposed view) is not the optimized backend's
+    (_optimized.py:98): it follows the reference step, which updates it in logical order."""
+    log("strided parameter")
+    gen = torch.Generator().manual_seed(12)
+    base = torch.randn(384, 256, generator=gen) * 0.02
+    pa = torch.nn.Parameter(base.clone().to(H.DEVICE).t())       # (256, 384), strided
+    pb = torch.nn.Parameter(base.clone().t().contiguous().to(H.DEVICE))
+    assert not pa.is_contiguous()
+    oa = aw.ZIPSRAdamW4Bit([pa], optimized=True, quant_rng_seed=6, **ARGS)
+    ob = aw.ZIPSRAdamW4Bit([pb], optimized=False, quant_rng_seed=6, **ARGS)
+    for k in range(3):
+        g = H.heavy_tailed((256, 384), gen).to(H.DEVICE)
+        pa.grad, pb.grad = g.clone(), g.clone()
+        oa.step()
+        ob.step()
+        torch.cuda.synchronize()
+        assert not pa.is_contiguous()
+        same_state(oa, pa, ob, pb, k)
+    assert oa._launch_plan is None  # the staged copy is per step
+
+
+# ---------------------------------------------------------------------------
+# The optimized backend's gates: which parameters take the reference step
+# ---------------------------------------------------------------------------
+
+def test_gradient_overlapping_parameter_takes_reference_step():
+    """A gradient that shares storage with its parameter sends the parameter to the reference
+    step (_optimized.py:110-112), including its initial draw count: n draws for the zero state
+    instead of one 128-value tile."""
+    log("gradient aliasing its parameter")
+    gen = torch.Generator().manual_seed(13)
+    shape = (128, 512)
+    n = shape[0] * shape[1]
+    init = torch.randn(shape, generator=gen) * 1e-3
+    pa = torch.nn.Parameter(init.clone().to(H.DEVICE))
+    pb = torch.nn.Parameter(init.clone().to(H.DEVICE))
+    oa = aw.ZIPSRAdamW4Bit([pa], optimized=True, quant_rng_seed=2, **ARGS)
+    ob = aw.ZIPSRAdamW4Bit([pb], optimized=False, quant_rng_seed=2, **ARGS)
+    for k in range(2):
+        pa.grad = pa.detach()          # the gradient is the parameter's own storage
+        pb.grad = pb.detach().clone()
+        oa.step()
+        ob.step()
+        torch.cuda.synchronize()
+        same_state(oa, pa, ob, pb, k)
+        if k == 0:
+            # reference step: the zero state draws n, the step n (optimized: 128 + n)
+            assert oa._stream("m2", pa.device).offset == 2 * n
+            assert oa._launch_plan is None
+
+
+def test_noncontiguous_gradient_takes_reference_step():
+    log("non-contiguous gradient")
+    gen = torch.Generator().manual_seed(14)
+    shape = (192, 256)
+    init = torch.randn(shape, generator=gen) * 0.02
+    pa = torch.nn.Parameter(init.clone().to(H.DEVICE))
+    pb = torch.nn.Parameter(init.clone().to(H.DEVICE))
+    oa = aw.ZIPSRAdamW4Bit([pa], optimized=True, quant_rng_seed=7, **ARGS)
+    ob = aw.ZIPSRAdamW4Bit([pb], optimized=False, quant_rng_seed=7, **ARGS)
+    for k in range(2):
+        g = H.heavy_tailed((shape[1], shape[0]), gen).to(H.DEVICE)
+        pa.grad = g.t()                # strided view with the parameter's shape
+        pb.grad = g.t().contiguous()
+        assert not pa.grad.is_contiguous()
+        oa.step()
+        ob.step()
+        torch.cuda.synchronize()
+        same_state(oa, pa, ob, pb, k)
+
+
+def test_aliased_state_after_load_takes_reference_step(tmp_path):
+    """Moment state that aliases another parameter's after a checkpoint load marks both
+    parameters for the reference step for good (_optimized.py:53-83): the mark is saved and
+    survives a resume, and the steps match an optimized=False twin."""
+    log("aliased state after load")
+    gen = torch.Generator().manual_seed(15)
+    shapes = [(128, 256), (128, 256)]
+    init = [torch.randn(s, generator=gen) * 0.02 for s in shapes]
+    pa = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
+    oa = aw.ZIPSRAdamW4Bit(pa, optimized=True, quant_rng_seed=4, **ARGS)
+    for p, g in zip(pa, grads_like(shapes, gen)):
+        p.grad = g
+    oa.step()
+    sd = oa.state_dict()
+    # both parameters' m1 codes now share one tensor
+    sd["state"][1]["m1_code"] = sd["state"][0]["m1_code"]
+    pb = [torch.nn.Parameter(p.detach().clone()) for p in pa]
+    ob = aw.ZIPSRAdamW4Bit(pb, optimized=True, quant_rng_seed=4, **ARGS)
+    ob.load_state_dict(sd)
+    assert all(ob.state[p].get("_optimized_full_fallback") is True for p in pb)
+    torch.save(ob.state_dict(), tmp_path / "aliased.pt")
+    pc = [torch.nn.Parameter(p.detach().clone()) for p in pb]
+    oc = aw.ZIPSRAdamW4Bit(pc, optimized=True, quant_rng_seed=4, **ARGS)
+    oc.load_state_dict(torch.load(tmp_path / "aliased.pt", weights_only=True))
+    assert all(oc.state[p].get("_optimized_full_fallback") is True for p in pc)  # persisted
+    # twin on the reference step, from the same (unaliased) starting state
+    pd = [torch.nn.Parameter(p.detach().clone()) for p in pc]
+    od = aw.ZIPSRAdamW4Bit(pd, optimized=False, quant_rng_seed=4, **ARGS)
+    sd2 = oc.state_dict()
+    for i in (0, 1):  # private copies: load_state_dict keeps same-device tensors, as torch's does
+        sd2["state"][i] = {k: _deep_clone(v) for k, v in sd2["state"][i].items() if k != "_optimized_full_fallback"}
+    od.load_state_dict(sd2)
+    for k in range(2):
+        for c, d, g in zip(pc, pd, grads_like(shapes, gen)):
+            c.grad, d.grad = g.clone(), g.clone()
+        oc.step()
+        od.step()
+        torch.cuda.synchronize()
+        for i in (0, 1):
+            assert oc.state[pc[i]]["_optimized_full_fallback"] is True
+            # the reference step wrote fresh codes: the two parameters no longer share them
+            same_state(oc, pc[i], od, pd[i], (k, i))
+    assert oc.state[pc[0]]["m1_code"].data_ptr() != oc.state[pc[1]]["m1_code"].data_ptr()
+
+
+# ---------------------------------------------------------------------------
+# Atomic steps
+# ---------------------------------------------------------------------------
+
+def test_rejected_parameter_leaves_every_state_untouched():
+    """A parameter the step cannot take (float64), listed after one it can, raises before any
+    state changes: the first parameter is not initialised, no stream moved."""
+    log("rejected parameter: no state change")
+    good = torch.nn.Parameter(torch.randn(64, 128, device=H.DEVICE) * 0.02)
+    bad = torch.nn.Parameter(torch.randn(64, 128, device=H.DEVICE, dtype=torch.float64))
+    opt = aw.ZIPSRAdamW4Bit([good, bad], optimized=True, quant_rng_seed=1, **ARGS)
+    good.grad = torch.randn_like(good) * 1e-3
+    bad.grad = torch.randn_like(bad) * 1e-3
+    before = good.detach().clone()
+    with pytest.raises(NotImplementedError, match="float64"):
+        opt.step()
+    torch.cuda.synchronize()
+    assert len(opt.state[good]) == 0
+    assert all(s.offset == 0 for s in opt._all_streams())
+    assert torch.equal(good.detach(), before)
+    # the same parameter stepped alone afterwards matches a fresh optimizer
+    bad.grad = None
+    twin = torch.nn.Parameter(before.clone())
+    ot = aw.ZIPSRAdamW4Bit([twin], optimized=True, quant_rng_seed=1, **ARGS)
+    twin.grad = good.grad.clone()
+    opt.step()
+    ot.step()
+    torch.cuda.synchronize()
+    same_state(opt, good, ot, twin, "after the rejected step")
+
+
+def test_failed_launch_is_undone(monkeypatch):
+    """A launch that fails leaves step counts, moment state and stream positions as they were,
+    through the full path and through the cached plan."""
+    log("failed launch: undone")
+    gen = torch.Generator().manual_seed(17)
+    shapes = [(128, 256), (768,)]
+    init = [torch.randn(s, generator=gen) * 0.02 for s in shapes]
+    pa = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
+    pb = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
+    oa = aw.ZIPSRAdamW4Bit(pa, optimized=True, quant_rng_seed=5, **ARGS)
+    ob = aw.ZIPSRAdamW4Bit(pb, optimized=True, quant_rng_seed=5, **ARGS)
+    real = _lib.fused_step
+
+    def failing(table, stream):
+        raise _lib.HipLibraryError("injected launch failure")
+
+    for k in range(5):
+        gs = grads_like(shapes, gen)
+        if k in (0, 3):  # k == 0: full path (fresh state); k == 3: the cached plan
+            for a, g in zip(pa, gs):
+                a.grad = g.clone()
+            snapshot = [dict(oa.state[a]) for a in pa]
+            offsets = {id(s): s.offset for s in oa._all_streams()}
+            monkeypatch.setattr(_lib, "fused_step", failing)
+            with pytest.raises(_lib.HipLibraryError, match="injected"):
+                oa.step()
+            monkeypatch.setattr(_lib, "fused_step", real)
+            for a, snap in zip(pa, snapshot):
+                st = oa.state[a]
+                assert st.keys() == snap.keys() and all(st[key] is snap[key] for key in st), k
+            # streams opened by the failed step's checks start at 0; the others did not move
+            assert all(s.offset == offsets.get(id(s), 0) for s in oa._all_streams()), k
+        for a, b, g in zip(pa, pb, gs):
+            a.grad, b.grad = g.clone(), g.clone()
+        oa.step()
+        ob.step()
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(pa, pb)):
+            same_state(oa, a, ob, b, (k, i))
+
+
+# ---------------------------------------------------------------------------
+# torch.compile: the launch is the custom operator
+# ---------------------------------------------------------------------------
+
+def test_compiled_step_goes_through_the_operator_and_matches_eager():
+    """``torch.compile`` of a function that calls ``opt.step()``: the host work runs eagerly
+    (compiler-disabled), the launch is traced as ``adamw4bit_hip::fused_step_`` -- which takes
+    its addresses from the tensors it receives, so functionalization copies are the ones
+    written -- and parameters and states are bit-identical to eager steps, with version
+    counters bumped."""
+    log("compiled step through adamw4bit_hip::fused_step_")
+    import torch._dynamo
+    from torch._dynamo.testing import CompileCounterWithBackend
+
+    torch._dynamo.reset()
+    gen = torch.Generator().manual_seed(19)
+    shapes = [(256, 128), (768,), (64, 512)]
+    init = [torch.randn(s, generator=gen) * 0.02 for s in shapes]
+    pa = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
+    pb = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
+    oa = aw.ZIPSRAdamW4Bit(pa, optimized=True, quant_rng_seed=11, **ARGS)
+    ob = aw.ZIPSRAdamW4Bit(pb, optimized=True, quant_rng_seed=11, **ARGS)
+    counter = CompileCounterWithBackend("inductor")
+
+    @torch.compile(backend=counter)
+    def compiled_step():
+        oa.step()
+
+    for k in range(3):
+        for a, b, g in zip(pa, pb, grads_like(shapes, gen)):
+            a.grad, b.grad = g.clone(), g.clone()
+        versions = [a._version for a in pa]
+        compiled_step()
+        ob.step()
+        torch.cuda.synchronize()
+        assert all(a._version > v for a, v in zip(pa, versions)), k
+        for i, (a, b) in enumerate(zip(pa, pb)):
+            same_state(oa, a, ob, b, (k, i))
+    targets = {str(node.target) for gm in counter.graphs for node in gm.graph.nodes if node.op == "call_function"}
+    log(f"  {counter.frame_count} frames compiled; call targets {sorted(targets)}")
+    assert any("adamw4bit_hip.fused_step_" in t for t in targets), targets

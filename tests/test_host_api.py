@@ -147,3 +147,92 @@ def test_lean_step_keeps_torch_hooks_and_profiler_range():
         opt.step()
     names = {e.name for e in prof.events()}
     assert "Optimizer.step#_CountingOptimizer.step" in names
+
+
+# ---------------------------------------------------------------------------
+# The optimized backend's preflight gates (_optimized.py:85-136), decided on the host
+# ---------------------------------------------------------------------------
+
+def _gate(opt, p, state=None):
+    group = opt.param_groups[0]
+    requested = (opt._m1_scheme_for(p, group["m1_quant_scheme"]), group["m2_quant_scheme"])
+    sizes = (128, 128)
+    schemes = tuple(opt._effective_scheme(p, m, s) for m, s in zip(requested, sizes))
+    return opt._plan_accepts(p, p.grad, group, requested, sizes, schemes, opt.state[p] if state is None else state)
+
+
+def _quantized_state(p, packed=True):
+    n = p.numel()
+    codes = torch.zeros((n + 1) // 2 if packed else n, dtype=torch.uint8)
+    st = {"step": 1}
+    for m in ("m1", "m2"):
+        st[f"{m}_code"] = codes.clone()
+        st[f"{m}_quant_state"] = q.QuantState(absmax=torch.zeros(n // 128), shape=p.shape, dtype=torch.float32,
+                                              blocksize=128, packed=packed)
+    return st
+
+
+def test_preflight_gates_follow_the_optimized_backend():
+    """Each gate of _plan that sends a parameter to the reference step: overlapping gradient,
+    strided parameter or gradient, incompatible state, a persisted fallback mark, a non-int step
+    count, a bad chunk limit; everything else takes the optimized semantics."""
+    p = torch.nn.Parameter(torch.zeros(64, 128))
+    opt = aw.ZIPSRAdamW4Bit([p], optimized=True, quant_rng_seed=0)
+    p.grad = torch.zeros_like(p)
+    assert _gate(opt, p)
+    assert _gate(opt, p, _quantized_state(p))
+    assert _gate(opt, p, _quantized_state(p, packed=False))  # legacy unpacked codes are compatible
+    p.grad = p.detach()  # shares the parameter's storage
+    assert not _gate(opt, p)
+    p.grad = torch.zeros(128, 64).t()
+    assert not _gate(opt, p)
+    p.grad = torch.zeros_like(p)
+    st = _quantized_state(p)
+    st["m1_code"] = st["m1_code"][::1].view(-1)[:-1]  # too short
+    assert not _gate(opt, p, st)
+    st = _quantized_state(p)
+    st["m2_quant_state"].absmax = torch.zeros(2 * p.numel() // 128)[::2]  # strided scales
+    assert not _gate(opt, p, st)
+    st = _quantized_state(p)
+    st["m2_code"] = st["m1_code"]  # two moments on one buffer
+    assert not _gate(opt, p, st)
+    st = _quantized_state(p)
+    st["m1_code"] = p.grad.view(torch.uint8)[: p.numel() // 2]  # state on the gradient's storage
+    assert not _gate(opt, p, st)
+    st = _quantized_state(p)
+    st["_optimized_full_fallback"] = True
+    assert not _gate(opt, p, st)
+    st = _quantized_state(p)
+    st["step"] = torch.tensor(1.0)
+    assert not _gate(opt, p, st)
+    opt.param_groups[0]["max_chunk_numel"] = 64  # below the block alignment
+    assert not _gate(opt, p)
+    opt.param_groups[0]["max_chunk_numel"] = 128
+    assert _gate(opt, p)
+    strided = torch.nn.Parameter(torch.zeros(128, 64).t())
+    strided.grad = torch.zeros(64, 128)
+    o2 = aw.ZEEDENAdamW4Bit([strided], optimized=True)
+    assert not _gate(o2, strided)
+    assert not _gate(aw.ZEEDENAdamW4Bit([p], optimized=False), p)  # optimized=False: always the reference
+
+
+def test_aliased_state_load_marks_both_parameters_and_persists():
+    """Moment buffers that share storage after a load mark every owner for the reference step
+    (_optimized.py:53-83); the mark travels in the state dict."""
+    ps = [torch.nn.Parameter(torch.zeros(64, 128)) for _ in range(3)]
+    opt = aw.ZIPSRAdamW4Bit(ps, optimized=True, quant_rng_seed=0)
+    sd = opt.state_dict()
+    states = [_quantized_state(p) for p in ps]
+    states[1]["m2_code"] = states[0]["m2_code"]
+    sd["state"] = {i: {k: (vars(v).copy() if isinstance(v, q.QuantState) else v) for k, v in st.items()}
+                   for i, st in enumerate(states)}
+    opt.load_state_dict(sd)
+    marks = [opt.state[p].get("_optimized_full_fallback", False) for p in ps]
+    assert marks == [True, True, False]
+    o2 = aw.ZIPSRAdamW4Bit(ps, optimized=True, quant_rng_seed=0)
+    sd2 = opt.state_dict()
+    for i in (0, 1):  # un-alias: the mark alone must keep them on the reference step
+        sd2["state"][i] = {k: (v.clone() if torch.is_tensor(v) else dict(v, absmax=v["absmax"].clone())
+                               if isinstance(v, dict) else v) for k, v in sd2["state"][i].items()}
+    o2.load_state_dict(sd2)
+    assert [o2.state[p].get("_optimized_full_fallback", False) for p in ps] == [True, True, False]
