@@ -17,7 +17,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIBRARY = os.path.join(HERE, "libadamw4bit_hip.so")
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 BLOCK = 128
 
 # Error codes
@@ -32,6 +32,7 @@ F32, BF16, F16 = 0, 1, 2
 TENSOR_LERP1_LARGE, TENSOR_LERP2_LARGE, TENSOR_VEC_ALIGNED, TENSOR_GRAD_SCALE = 0x1, 0x2, 0x4, 0x8
 
 NUM_LUTS, LUT_HALF, LUT_EXP0 = 11, 89, 936
+NOALLOC_TABLE_BYTES = 1 << 20
 LUT_ENTRIES = 2 * LUT_HALF
 
 MOMENT = np.dtype([
@@ -55,6 +56,7 @@ SIGNATURES = {
     "aw4_abi_version": (ctypes.c_int, []),
     "aw4_last_error": (ctypes.c_char_p, []),
     "aw4_fused_step": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p]),
+    "aw4_fused_step_noalloc": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p]),
     "aw4_quantize": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]),
     "aw4_dequantize": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]),
     "aw4_uniforms": (ctypes.c_int, [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int64, ctypes.c_void_p,
@@ -104,6 +106,13 @@ def fused_step(table: np.ndarray, stream: int) -> None:
     """Launch one fused step over the rows of ``table`` (dtype :data:`TENSOR`)."""
     assert table.dtype == TENSOR and table.flags.c_contiguous
     check(library().aw4_fused_step(table.ctypes.data, len(table), stream), "aw4_fused_step")
+
+
+def fused_step_noalloc(table: np.ndarray, stream: int) -> None:
+    """``fused_step`` through ``aw4_fused_step_noalloc`` (no device allocation; tables of at most
+    NOALLOC_TABLE_BYTES)."""
+    assert table.dtype == TENSOR and table.flags.c_contiguous
+    check(library().aw4_fused_step_noalloc(table.ctypes.data, len(table), stream), "aw4_fused_step_noalloc")
 
 
 def quantize(values_ptr: int, numel: int, moment: np.ndarray, stream: int) -> None:

@@ -45,6 +45,14 @@
 #include "aw4_prologue.h"
 #include "aw4_step.h"
 
+// Device memory the library holds without allocating it: file-scope arrays, one copy per GPU,
+// kept until the process ends.  g_tables_mem holds the codebook and lookup tables every kernel
+// reads; `scratch` holds the launch tables of aw4_fused_step_noalloc.  In host code these names
+// are stand-ins, not device addresses: the host takes each GPU's address of them with
+// hipGetSymbolAddress (device_state) and uses only that.
+static __device__ __align__(256) uint8_t g_tables_mem[sizeof(aw4::Tables)];
+static __device__ __align__(256) uint8_t scratch[AW4_NOALLOC_TABLE_BYTES];
+
 namespace {
 
 using namespace aw4;
@@ -404,13 +412,15 @@ struct StagingSlot {
 constexpr int kSlots = 4;
 
 struct DeviceState {
-    Tables* tables = nullptr;
+    Tables* tables = nullptr;    // this GPU's address of g_tables_mem
+    uint8_t* scratch = nullptr;  // this GPU's address of `scratch`
     int num_cus = 0;
     StagingSlot slots[kSlots];
     int next = 0;
     // Host buffers of slots that have grown.  The device has read them uncached; they are kept
     // until the process ends rather than freed and their pages handed out again.
     std::vector<void*> retired_host;
+    std::vector<uint8_t> noalloc_host;  // host image of the tables aw4_fused_step_noalloc stages
 };
 
 std::mutex g_mutex;
@@ -423,17 +433,18 @@ int device_state(DeviceState** out) {
     AW4_HIP_CHECK(hipGetDevice(&dev));
     DeviceState& ds = g_devices[dev];
     if (!ds.tables) {
+        // Once per device, with that device current: its addresses of the file-scope arrays, and
+        // the codebook tables copied into them (one synchronous copy; nothing is allocated).
         hipDeviceProp_t prop;
         AW4_HIP_CHECK(hipGetDeviceProperties(&prop, dev));
         ds.num_cus = prop.multiProcessorCount;
-        Tables* d = nullptr;
-        AW4_HIP_CHECK(hipMalloc((void**)&d, sizeof(Tables)));
-        hipError_t e = hipMemcpy(d, &ht.t, sizeof(Tables), hipMemcpyHostToDevice);
-        if (e != hipSuccess) {
-            (void)hipFree(d);
-            return set_error(AW4_EHIP, "hipMemcpy(tables): %s", hipGetErrorString(e));
-        }
-        ds.tables = d;
+        void* tables = nullptr;
+        void* stage = nullptr;
+        AW4_HIP_CHECK(hipGetSymbolAddress(&tables, HIP_SYMBOL(g_tables_mem)));
+        AW4_HIP_CHECK(hipGetSymbolAddress(&stage, HIP_SYMBOL(scratch)));
+        AW4_HIP_CHECK(hipMemcpy(tables, &ht.t, sizeof(Tables), hipMemcpyHostToDevice));
+        ds.scratch = (uint8_t*)stage;
+        ds.tables = (Tables*)tables;
     }
     *out = &ds;
     return AW4_OK;
@@ -739,6 +750,38 @@ int launch_step(const StepLaunch& sl, const char* dev_base, const Tables* tables
     return AW4_OK;
 }
 
+// Staging through kernel arguments: each launch carries up to kArgBytes of the table by value
+// and copies them to their place in device memory, so the bytes need no device buffer of the
+// host's and no copy engine, and the host's buffer is free again when the call returns (the
+// launch packet holds its own copy).  Kernel arguments are limited to 4 KB per launch.
+constexpr int kArgBytes = 3584;
+
+struct __align__(16) ArgChunk {
+    uint64_t dst;    // device address, 16-byte aligned
+    uint32_t n16;    // 16-byte words to copy (at most kArgBytes / 16)
+    uint32_t reserved;
+    uint4 data[kArgBytes / 16];
+};
+
+__global__ void __launch_bounds__(256) stage_args_kernel(const ArgChunk chunk) {
+    const uint4* src = (const uint4*)((const char*)__builtin_amdgcn_kernarg_segment_ptr() + offsetof(ArgChunk, data));
+    for (uint32_t i = threadIdx.x; i < chunk.n16; i += 256) ((uint4*)chunk.dst)[i] = src[i];
+}
+
+int upload_by_arguments(const void* src, size_t bytes, uint8_t* dst, hipStream_t s) {
+    ArgChunk chunk;
+    for (size_t off = 0; off < bytes; off += kArgBytes) {
+        const size_t n = std::min<size_t>(kArgBytes, bytes - off);
+        memset(&chunk, 0, sizeof(chunk));
+        chunk.dst = (uint64_t)(dst + off);
+        chunk.n16 = (uint32_t)((n + 15) / 16);
+        memcpy(chunk.data, (const char*)src + off, n);
+        hipLaunchKernelGGL(stage_args_kernel, dim3(1), dim3(256), 0, s, chunk);
+        AW4_HIP_CHECK(hipGetLastError());
+    }
+    return AW4_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -780,6 +823,30 @@ int aw4_fused_step(const aw4_tensor* tensors, int32_t count, void* stream) {
     AW4_HIP_CHECK(hipEventRecord(slot.done, s));
     slot.pending = true;
     return AW4_OK;
+}
+
+int aw4_fused_step_noalloc(const aw4_tensor* tensors, int32_t count, void* stream) {
+    g_error.clear();
+    StepLaunch sl;
+    int rc = prepare_step(tensors, count, sl);
+    if (rc || sl.plan.empty()) return rc;
+    if (sl.bytes > (size_t)AW4_NOALLOC_TABLE_BYTES)
+        return set_error(AW4_EINVAL,
+                         "aw4_fused_step_noalloc: the launch tables of %d tensors need %zu bytes, more than its "
+                         "%d-byte table area (use aw4_fused_step)",
+                         count, sl.bytes, AW4_NOALLOC_TABLE_BYTES);
+    std::lock_guard<std::mutex> lock(g_mutex);
+    DeviceState* ds = nullptr;
+    rc = device_state(&ds);
+    if (rc) return rc;
+    std::vector<uint8_t>& host = ds->noalloc_host;
+    host.assign(sl.bytes, 0);
+    rc = fill_step_tables(tensors, sl, ds->num_cus, host.data());
+    if (rc) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    rc = upload_by_arguments(host.data(), sl.bytes, ds->scratch, s);
+    if (rc) return rc;
+    return launch_step(sl, (const char*)ds->scratch, ds->tables, s);
 }
 
 int aw4_quantize(const float* values, int64_t numel, const aw4_moment* m, void* stream) {

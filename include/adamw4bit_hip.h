@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define AW4_ABI_VERSION 4
+#define AW4_ABI_VERSION 5
 #define AW4_BLOCK 128 /* values per block scale (quantization.py:694-703, 4-bit default) */
 
 /* Error codes. */
@@ -165,6 +165,22 @@ const char* aw4_last_error(void);
  * chunk update _optimized.py:206-234.
  */
 int aw4_fused_step(const aw4_tensor* tensors, int32_t count, void* stream);
+
+/*
+ * aw4_fused_step for callers that cannot allocate device memory: code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.  It has no counterpart in
+ * the reference (whose step is Python).  Same arguments, checks, kernels and results as
+ * aw4_fused_step, but it calls no hipMalloc, hipFree or other allocating routine: the launch
+ * tables (the step's only device memory besides the caller's tensors) go to a fixed area of
+ * AW4_NOALLOC_TABLE_BYTES that the library holds in a file-scope device array on each GPU
+ * until the process ends, and reach it through the arguments of small copy kernels on
+ * `stream`.  A call whose tables exceed that area (about 3,700 tensors) fails with AW4_EINVAL.
+ * The first call on a device (of any entry point) copies the codebook tables to it once,
+ * synchronously.  Every call on one GPU uses the same area: calls on one stream are ordered,
+ * calls that overlap on different streams of one GPU race.
+ */
+#define AW4_NOALLOC_TABLE_BYTES (1 << 20)
+int aw4_fused_step_noalloc(const aw4_tensor* tensors, int32_t count, void* stream);
 
 /*
  * Encode `numel` fp32 values (numel a multiple of 128) into the quantized

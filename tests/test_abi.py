@@ -386,3 +386,19 @@ def test_plan_step_view_covers_exactly_the_per_step_fields():
     assert written.sum() == 8 + 8 + 32 + 12 + 8 + 8
     assert np.array_equal(raw[:, ~written], before[:, ~written])
 
+
+def test_noalloc_step_rejects_tables_beyond_its_area():
+    """aw4_fused_step_noalloc checks its rows and the size of their launch tables before any
+    device work: tables beyond AW4_NOALLOC_TABLE_BYTES fail with a clear error (no GPU needed)."""
+    lib = _lib.library()
+    n = _lib.NOALLOC_TABLE_BYTES // (_lib.TENSOR.itemsize + 8) + 8
+    rows = np.zeros(n, dtype=_lib.TENSOR)
+    rows["param"], rows["grad"], rows["numel"] = 1 << 20, 2 << 20, 100  # fp32-state rows: never touched
+    rows["m1"]["values"], rows["m2"]["values"] = 3 << 20, 4 << 20
+    rows["m1"]["rounding"] = rows["m2"]["rounding"] = _lib.ROUND_FP32
+    rc = lib.aw4_fused_step_noalloc(rows.ctypes.data, len(rows), None)
+    assert rc == _lib.EINVAL
+    assert b"more than its 1048576-byte table area" in lib.aw4_last_error()
+    rows["numel"][7] = 0
+    assert lib.aw4_fused_step_noalloc(rows.ctypes.data, len(rows), None) == _lib.EINVAL
+    assert b"tensor 7: numel 0" in lib.aw4_last_error()
