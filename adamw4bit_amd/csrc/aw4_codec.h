@@ -71,16 +71,19 @@ struct __align__(16) PairEntry {
     uint32_t lohi;    // lo | hi << 8
 };
 
-// Per-block update-SR quantities for each searchsorted index (update_sr_tables()).
+// Per-block update-SR quantities for each searchsorted index i (update_sr_tables()), with
+// c = sqrt(s / bias) the block's scale factor and E(l) = c * sqrt(l) + eps for a level l, so that
+// the preconditioner of l is 1 / E(l) (_compiled_quantization.py:83-85).
 struct __align__(8) UpdEntry {
-    float f_hi;   // preconditioner at the upper level
-    float den_u;  // max(f(lo) - f(hi), 1e-30) * 2^-24 where the interval is valid
-                  // ((b > a) & (f(lo) - f(hi) > 0)), else -1
+    float sqrt_hi;  // sqrt(b), b the upper level of the interval
+    float g;        // (sqrt(b) - sqrt(a)) * 2^-24 / E(a), a the lower level (0: no interval)
 };
 
 // All tables of all codebooks, built on the host and kept in device memory.
 struct Tables {
     float codebook[AW4_NUM_CODEBOOKS][16];
+    float sqrt_level[AW4_NUM_CODEBOOKS][16];        // RN(sqrt(level)), 0 for negative levels
+    float sqrt_gap[AW4_NUM_CODEBOOKS][kPairs];      // RN(sqrt(b) - sqrt(a)) of each searchsorted index
     PairEntry pairs[AW4_NUM_CODEBOOKS][kPairs];
     float2 dec[AW4_NUM_CODEBOOKS][256];  // code byte -> (level of low nibble, level of high nibble)
     LutEntry lut[AW4_NUM_LUTS][AW4_LUT_ENTRIES];
@@ -92,13 +95,15 @@ struct MomentTables {
     const PairEntry* pairs;
     const float2* dec;
     const LutEntry* lut;
+    const float* sqrt_level;
+    const float* sqrt_gap;
 };
 
 // LDS scratch of one block's encode: update-SR tables of the block and the staging area
 // of its 64 code bytes (written a quarter at a time, stored to memory in one piece).
 struct BlockScratch {
     UpdEntry* upd;      // kPairs entries (update-SR only)
-    float* pre;         // preconditioner of each of the 16 levels (update-SR only)
+    float* pre;         // E(l) of each of the 16 levels (update-SR only)
     uint16_t* stage;    // 32 code words: word 8q + j is lane j's word of quarter q
 };
 
@@ -140,34 +145,67 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Per-block update-SR tables (_compiled_quantization.py:74-109): for every
-// searchsorted index i, f(hi) and max(f(lo) - f(hi), 1e-30) / 2^24 (negative marks an
-// invalid interval), with f(l) = 1 / (sqrt(max((s * l) / bias, 0)) + eps).
-__device__ __forceinline__ void update_sr_tables(const MomentTables& L, int j, float s, float bias, float bias_rcp,
-                                                 float eps, UpdEntry* upd, float* pre) {
+// Update-SR (_compiled_quantization.py:74-109) decides lower with probability
+//   P = (f(x) - f(b)) / (f(a) - f(b)),  f(l) = 1 / (sqrt((s * l) / bias) + eps),
+// for the levels a < x <= b around x.  With c = sqrt(s / bias) and E(l) = c * sqrt(l) + eps,
+// f(l) = 1 / E(l) and, exactly,
+//   P = E(a) * (sqrt(b) - sqrt(x)) / ((sqrt(b) - sqrt(a)) * E(x)),
+// so u < P exactly when
+//   Q = (sqrt(b) - sqrt(x)) - u * ((sqrt(b) - sqrt(a)) / E(a)) * E(x) > 0:
+// one square root and no division per value.  The reference rounds each of its steps in fp32
+// (its f values within 5 ulps with a faithful square root, then a difference and a quotient),
+// and Q here is rounded too; the two decisions provably agree when
+//   |Q| > 2^-19 * (E(b) / c + sqrt(b))
+// (32 units of 2^-24: the bound, first order in 2^-24, is 20.05 units times E(b) / c for the
+// reference's rounding and 24.01 units times sqrt(b) for Q's).  For levels <= 1 this is at most
+// the block's band 2^-19 * (2 + eps / c).  Values inside it (a few in 10^5, where f(a) and f(b)
+// are close) take usr_exact, the reference's own operations.  The interval is valid when b > a
+// and fp32 f(a) > f(b); the latter is certain when c * (sqrt(b) - sqrt(a)) > 2^-20 * E(b) (the
+// true relative gap of f(a) and f(b) against their 5-ulp rounding); a block where it is not
+// (c tiny against eps) decides every value with usr_exact.
+constexpr float kUsrBand = 0x1p-19f;
+
+struct UsrBlock {
+    float c;     // sqrt(s / bias), within 3 ulps
+    float band;  // the block's decision band (+inf: decide every value exactly)
+};
+
+// The block's tables: E(l) of the 16 levels (two per lane), then the 17 UpdEntry of the
+// searchsorted indices (two per lane).
+__device__ __forceinline__ UsrBlock update_sr_tables(const MomentTables& L, int j, float s, const aw4_moment& M,
+                                                     UpdEntry* upd, float* pre) {
+    const float c = sqrt_faithful(s * M.sr_bias_rcp);
+    const float c_rcp = rcp_faithful(c);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int k = j + 8 * h;
-        const float vh = clamp_min_nan(div_by_rcp(s * L.cb[k], bias, bias_rcp), 0.0f);
-        pre[k] = rcp_faithful(sqrt_faithful(vh) + eps);
+        pre[k] = __builtin_fmaf(c, L.sqrt_level[k], M.sr_eps);
     }
     wave_lds_sync();
     // Entries 1..16 in two rounds of the block's 8 lanes; entry 0 (no level below x) has
-    // lo == hi and is always invalid.
+    // lo == hi and no interval.
+    bool certain = true;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int i = 1 + j + 8 * h;
         const PairEntry pe = L.pairs[i];
-        const float flo = pre[pe.lohi & 0xffu], fhi = pre[pe.lohi >> 8];
-        const float den = flo - fhi;
-        const float dc = clamp_min_nan(den, 1e-30f);
-        UpdEntry e;
-        e.f_hi = fhi;
-        e.den_u = (pe.b > pe.a && den > 0.0f) ? dc * 0x1p-24f : -1.0f;  // dc >= 1e-30: stays normal
-        upd[i] = e;
+        const float e_lo = pre[pe.lohi & 0xffu], e_hi = pre[pe.lohi >> 8];
+        const float gap = L.sqrt_gap[i];
+        certain = certain & (!(pe.b > pe.a) | (c * gap > 0x1p-20f * e_hi));  // over the real intervals
+        // E(a) = 0 (a = 0 with eps = 0): f(a) is infinite and P = 0, so g = +inf decides upper
+        // (a draw of exactly 0 gives NaN and takes usr_exact)
+        const float g = e_lo > 0.0f ? gap * 0x1p-24f * rcp_faithful(e_lo) : __builtin_inff();
+        upd[i] = UpdEntry{L.sqrt_level[pe.lohi >> 8], g};
     }
-    if (j == 0) upd[0] = UpdEntry{0.0f, -1.0f};
+    if (j == 0) upd[0] = UpdEntry{0.0f, 0.0f};
+    // every interval of the block certain (its 8 lanes, 16 entries)
+    uint32_t all = certain ? 1u : 0u;
+    all = min(all, dpp_u32<kQuadXor1>(all));
+    all = min(all, dpp_u32<kQuadXor2>(all));
+    all = min(all, dpp_u32<kHalfRowMirror>(all));
     wave_lds_sync();
+    const float band = kUsrBand * __builtin_fmaf(M.sr_eps, c_rcp, 2.0f);
+    return UsrBlock{c, all ? band : __builtin_inff()};
 }
 
 // Uniforms of this lane's 4 values of quarter q in its block (block blk0 + grp of one write
@@ -190,25 +228,34 @@ __device__ __forceinline__ void draws_quarter(const aw4_moment& M, int64_t blk0,
     }
 }
 
-// Update-SR draw test u < P(lo) for one value, with U = u * 2^24 and the table entry of
-// its interval: P(lo) = RN(d / den), d = RN(f(x) - f(b)),
-// f(x) = 1 / (sqrt(max((s * x) / bias, 0)) + eps)  (_compiled_quantization.py:74-97).
-// f(x) and d are rounded as the reference rounds them: where eps dominates the square
-// root, f is nearly flat and P is mostly the rounding of f(x), so that rounding is kept.
-// The final quotient is not formed: u < d / den  <=>  fma(U, den / 2^24, -d) < 0, the
-// exact sign of u * den - d, which differs from u < RN(d / den) only for a draw on the
-// rounding of P itself (about 2^-24 of the values).  Fast form: (s * x) / bias from
-// RN(1 / bias), exact for normal quotients (taken when every block of the wave has a
-// scale below 2^125 and s / bias far from overflow); slow form: IEEE division.
-template <bool kFast, bool kNonNeg>
-__device__ __forceinline__ bool usr_draw_lower(const aw4_moment& M, const UpdEntry& ue, float s, float x, float U) {
-    float v;
-    if constexpr (kFast) v = div_by_rcp(s * x, M.sr_bias, M.sr_bias_rcp);
-    else v = (s * x) / M.sr_bias;
-    if (!kNonNeg || !kFast) v = clamp_min_nan(v, 0.0f);
-    const float z = sqrt_faithful(v) + M.sr_eps;
-    const float fx = kFast ? rcp_faithful(z) : 1.0f / z;
-    return __builtin_fmaf(U, ue.den_u, -(fx - ue.f_hi)) < 0.0f;  // (den / 2^24 is exact)
+// The reference's preconditioner of a level or value l: fp32(1 / (sqrt(max((s * l) / bias, 0))
+// + eps)), each operation correctly rounded (ATen's division, 1.0 / t as a reciprocal) and the
+// square root correctly rounded (ATen's is within an ulp of it).
+__device__ __forceinline__ float usr_precond(const aw4_moment& M, float s, float l) {
+    const float v = clamp_min_nan((s * l) / M.sr_bias, 0.0f);
+    return 1.0f / (sqrt_cr(v) + M.sr_eps);
+}
+
+// Update-SR decision by the reference's operations (_compiled_quantization.py:74-109):
+// valid = (b > a) & (f(a) - f(b) > 0); lower = u < (f(x) - f(b)) / max(f(a) - f(b), 1e-30),
+// u = U * 2^-24.  The clamp of P to [0, 1] never changes u < P for u in [0, 1).
+__device__ __forceinline__ void usr_exact(const aw4_moment& M, float s, float x, float a, float b, float U, bool& valid,
+                                       bool& lower) {
+    const float fa = usr_precond(M, s, a), fb = usr_precond(M, s, b), fx = usr_precond(M, s, x);
+    const float den = fa - fb;
+    valid = (b > a) & (den > 0.0f);
+    lower = U * 0x1p-24f < (fx - fb) / clamp_min_nan(den, 1e-30f);
+}
+
+// The quick decision (see update_sr_tables): Q > 0 means lower; `sure` is false inside the band.
+// U = u * 2^24.
+__device__ __forceinline__ void usr_quick(const UpdEntry& ue, const UsrBlock& ub, float eps, float x, float U,
+                                          bool& lower, bool& sure) {
+    const float w = sqrt_faithful(x);
+    const float ex = __builtin_fmaf(ub.c, w, eps);
+    const float q = __builtin_fmaf(-U, ue.g * ex, ue.sqrt_hi - w);
+    lower = q > 0.0f;
+    sure = __builtin_fabsf(q) > ub.band;
 }
 
 // NaN-propagating max(acc, |v|): v_maximum3_f32 with |.| operands.
@@ -264,8 +311,9 @@ __device__ __forceinline__ BlockScales encode_block(const aw4_moment& M, const M
     const bool eden = (flags & AW4_MOMENT_EDEN) != 0;
     const bool guards = (flags & AW4_MOMENT_GUARDS) != 0;
     const bool floor0 = (flags & AW4_MOMENT_ZERO_FLOOR) != 0;
+    UsrBlock ub{0.0f, 0.0f};
     if constexpr (KIND == K_USR) {
-        update_sr_tables(L, j, s, M.sr_bias, M.sr_bias_rcp, M.sr_eps, sc.upd, sc.pre);
+        ub = update_sr_tables(L, j, s, M, sc.upd, sc.pre);
         fast = fast && s * M.sr_bias_rcp < 0x1p127f;  // (s * x) / bias stays far from overflow
     }
     // One branch for the whole wave: the IEEE forms are exact for every block, so a wave
@@ -339,23 +387,36 @@ __device__ __forceinline__ BlockScales encode_block(const aw4_moment& M, const M
                 // invalid interval, and add x <= a -> lo, which holds exactly when no level is
                 // below x (idx == 0), where lo and hi are both code 0: that guard changes no code
                 // (nor the level EDEN reads) and is not evaluated.
-                UpdEntry ue[4];
-                bool dl[4];
-#pragma unroll
-                for (int t = 0; t < 4; ++t) ue[t] = sc.upd[idx[t]];
+                bool dl[4], valid[4];
+                uint64_t unsure = 1;  // lanes (bits) with a value the quick test leaves open
                 if (__builtin_expect(wave_fast, 1)) {
+                    unsure = 0;
 #pragma unroll
-                    for (int t = 0; t < 4; ++t) dl[t] = usr_draw_lower<true, kNonNeg>(M, ue[t], s, x[t], u[t]);
-                } else {
+                    for (int t = 0; t < 4; ++t) {
+                        const UpdEntry ue = sc.upd[idx[t]];
+                        bool sure;
+                        usr_quick(ue, ub, M.sr_eps, x[t], u[t], dl[t], sure);
+                        valid[t] = true;  // (idx > 0 below: levels increase, so x > cb[0] has an interval)
+                        unsure |= __builtin_amdgcn_ballot_w64(!sure);
+                    }
+                }
+                // A quarter with any open value (a few in a hundred) is decided again by the
+                // reference's operations, every value of it: where the quick test was sure the two
+                // agree, so nothing needs to be selected.  The branch is uniform.
+                if (unsure != 0) {
 #pragma unroll
-                    for (int t = 0; t < 4; ++t) dl[t] = usr_draw_lower<false, kNonNeg>(M, ue[t], s, x[t], u[t]);
+                    for (int t = 0; t < 4; ++t) {
+                        const PairEntry pe = L.pairs[idx[t]];
+                        usr_exact(M, s, x[t], pe.a, pe.b, u[t], valid[t], dl[t]);
+                    }
                 }
                 // Bitwise operators: the operands are all computed, and short-circuit forms
                 // become per-value branches.
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
-                    const bool valid = ue[t].den_u > 0.0f, at_b = x[t] >= b[t];
-                    lower[t] = guards ? ((!valid) | dl[t]) & !at_b : (!valid) | (dl[t] & !at_b);
+                    const bool at_b = x[t] >= b[t];
+                    const bool ok = valid[t] & (idx[t] > 0);
+                    lower[t] = guards ? ((!ok) | dl[t]) & !at_b : (!ok) | (dl[t] & !at_b);
                 }
             }
 #pragma unroll

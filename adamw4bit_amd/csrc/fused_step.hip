@@ -91,6 +91,8 @@ __host__ __device__ inline int lut_id_of(int rounding, int codebook, int flags) 
 template <bool kUpd>
 struct LdsSlots {
     float cb[2][16];
+    float sqrt_level[2][16];
+    float sqrt_gap[2][kPairs];
     PairEntry pairs[2][kPairs];
     float2 dec[2][256];
     LutEntry lut[2][AW4_LUT_ENTRIES];
@@ -98,7 +100,7 @@ struct LdsSlots {
     f32x4 m2_stage[kUpd ? kWavesPerGroup * 4 * 64 : 1];  // second moments of a tile (update-SR kernels)
 
     __device__ MomentTables moment(const aw4_moment&, int which) const {
-        return MomentTables{cb[which], pairs[which], dec[which], lut[which]};
+        return MomentTables{cb[which], pairs[which], dec[which], lut[which], sqrt_level[which], sqrt_gap[which]};
     }
     __device__ f32x4* wave_m2_stage(int wslot) { return kUpd ? &m2_stage[wslot * 4 * 64] : nullptr; }
     __device__ void load(const Tables* g, const StepHeader* h) {
@@ -106,6 +108,8 @@ struct LdsSlots {
         for (int w = 0; w < 2; ++w) {
             if (cbs[w] < 0) continue;
             for (int i = threadIdx.x; i < 16; i += kThreads) cb[w][i] = g->codebook[cbs[w]][i];
+            for (int i = threadIdx.x; i < 16; i += kThreads) sqrt_level[w][i] = g->sqrt_level[cbs[w]][i];
+            for (int i = threadIdx.x; i < kPairs; i += kThreads) sqrt_gap[w][i] = g->sqrt_gap[cbs[w]][i];
             for (int i = threadIdx.x; i < kPairs; i += kThreads) pairs[w][i] = g->pairs[cbs[w]][i];
             for (int i = threadIdx.x; i < 256; i += kThreads) dec[w][i] = g->dec[cbs[w]][i];
             for (int i = threadIdx.x; i < AW4_LUT_ENTRIES; i += kThreads) lut[w][i] = g->lut[luts[w]][i];
@@ -122,7 +126,8 @@ struct LdsAll {
     __device__ MomentTables moment(const aw4_moment& m, int) const {
         const int cbid = m.rounding == AW4_ROUND_FP32 ? 0 : m.codebook;
         return MomentTables{t.codebook[cbid], t.pairs[cbid], t.dec[cbid],
-                            t.lut[m.rounding == AW4_ROUND_FP32 ? 0 : lut_id_of(m.rounding, cbid, m.flags)]};
+                            t.lut[m.rounding == AW4_ROUND_FP32 ? 0 : lut_id_of(m.rounding, cbid, m.flags)],
+                            t.sqrt_level[cbid], t.sqrt_gap[cbid]};
     }
     __device__ f32x4* wave_m2_stage(int) { return nullptr; }
     __device__ void load(const Tables* g, const StepHeader*) {
@@ -142,12 +147,25 @@ struct KernelTraits {
 };
 
 template <int M1K, int M2K, int D>
-__global__ void __launch_bounds__(kThreads) step_kernel(const StepHeader* __restrict__ hdr,
-                                                         const Tables* __restrict__ tables) {
+__device__ __forceinline__ void step_body(const StepHeader* __restrict__ hdr, const Tables* __restrict__ tables) {
     using Lds = typename KernelTraits<M1K, M2K, D>::Lds;
     __shared__ Lds lds;
     const int wslot = threadIdx.x >> 6;
     run_tiles<M1K, M2K, D>(hdr, lds, lds.scratch[wslot], lds.wave_m2_stage(wslot), [&] { lds.load(tables, hdr); });
+}
+
+template <int M1K, int M2K, int D>
+__global__ void __launch_bounds__(kThreads) step_kernel(const StepHeader* __restrict__ hdr,
+                                                         const Tables* __restrict__ tables) {
+    step_body<M1K, M2K, D>(hdr, tables);
+}
+
+// The same kernel held to 128 VGPRs, four waves per SIMD (the fp32 recipes fit without spills;
+// the fourth wave hides memory latency the third leaves exposed).
+template <int M1K, int M2K, int D>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4)))
+step_kernel_4w(const StepHeader* __restrict__ hdr, const Tables* __restrict__ tables) {
+    step_body<M1K, M2K, D>(hdr, tables);
 }
 
 // The instantiated kernels; the host groups a step's tensors by the variant whose moment
@@ -172,8 +190,9 @@ struct KernelVariant {
     const void* fn;
 };
 #define AW4_VARIANT(M1, M2, D) {M1, M2, D, (const void*)&step_kernel<M1, M2, D>}
+#define AW4_VARIANT_4W(M1, M2, D) {M1, M2, D, (const void*)&step_kernel_4w<M1, M2, D>}
 const KernelVariant kVariants[] = {
-    AW4_VARIANT(kRtn, kRtnEden, D_F32),           AW4_VARIANT(kRtn, kUsrGuarded, D_F32),
+    AW4_VARIANT_4W(kRtn, kRtnEden, D_F32),        AW4_VARIANT_4W(kRtn, kUsrGuarded, D_F32),
     AW4_VARIANT(kRtn, kRtnEden, D_BF16),          AW4_VARIANT(kRtn, kUsrGuarded, D_BF16),
     AW4_VARIANT(kSsrGuarded, kUsrGuarded, D_F32), AW4_VARIANT(kSsrGuarded, kUsrGuarded, D_BF16),
     AW4_VARIANT(kRtn, kFp32, D_F32),              AW4_VARIANT(kRtn, kFp32, D_BF16),
@@ -184,6 +203,7 @@ const KernelVariant kVariants[] = {
     AW4_VARIANT(K_ANY, K_ANY, D_ANY),
 };
 #undef AW4_VARIANT
+#undef AW4_VARIANT_4W
 constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 constexpr int kGenericVariant = kNumVariants - 1;
 constexpr int kResearchVariant = kNumVariants - 2;  // generic, for read-back and lookahead m2
@@ -374,8 +394,15 @@ const HostTables& host_tables() {
         memset(&t, 0, sizeof(t));
         for (int c = 0; c < AW4_NUM_CODEBOOKS; ++c) {
             for (int k = 0; k < 16; ++k) t.codebook[c][k] = host_f(kCodebookBits[c][k]);
+            // square roots of the levels and of their gaps, in double, rounded once to fp32
+            for (int k = 0; k < 16; ++k) {
+                const double l = (double)t.codebook[c][k];
+                t.sqrt_level[c][k] = l > 0.0 ? (float)sqrt(l) : 0.0f;
+            }
             for (int i = 0; i < kPairs; ++i) {
                 const int lo = i > 0 ? i - 1 : 0, hi = i < 15 ? i : 15;
+                const double a = (double)t.codebook[c][lo], b = (double)t.codebook[c][hi];
+                t.sqrt_gap[c][i] = (a >= 0.0 && b > a) ? (float)(sqrt(b) - sqrt(a)) : 0.0f;
                 PairEntry& p = t.pairs[c][i];
                 p.a = t.codebook[c][lo];
                 p.b = t.codebook[c][hi];

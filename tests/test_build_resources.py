@@ -23,8 +23,8 @@ from adamw4bit_amd import build
 # 4 = lookahead update-SR stored as codes;
 # dtype: 0 = fp32, 1 = bf16.
 MIN_WAVES = {
-    (1, 33, 0): 3, (1, 67, 0): 4, (1, 33, 1): 4, (1, 67, 1): 4, (66, 67, 0): 3, (66, 67, 1): 4,
-    (1, 0, 0): 4, (1, 0, 1): 4, (1, 99, 0): 3, (1, 99, 1): 4, (1, 259, 0): 3, (1, 803, 0): 2,
+    (1, 33, 0): 4, (1, 67, 0): 4, (1, 33, 1): 4, (1, 67, 1): 4, (66, 67, 0): 3, (66, 67, 1): 4,
+    (1, 0, 0): 4, (1, 0, 1): 4, (1, 99, 0): 3, (1, 99, 1): 3, (1, 259, 0): 3, (1, 803, 0): 2,
     (1, 4, 0): 2,
 }
 
@@ -51,7 +51,7 @@ def kernel_vgprs():
         name = re.search(r"\.name:\s+(\S+)", block)
         if not name or "step_kernel" not in name.group(1):
             continue
-        args = re.search(r"step_kernelILi(\d+)ELi(\d+)ELi(\d+)E", name.group(1))
+        args = re.search(r"step_kernel(?:_4w)?ILi(\d+)ELi(\d+)ELi(\d+)E", name.group(1))
         vgpr = re.search(r"\.vgpr_count:\s+(\d+)", block)
         spill = re.search(r"\.vgpr_spill_count:\s+(\d+)", block)
         found[tuple(int(x) for x in args.groups())] = (int(vgpr.group(1)), int(spill.group(1)))
