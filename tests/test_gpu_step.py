@@ -578,13 +578,14 @@ def test_scheme_groups_reference_step():
 
 
 def test_gpt2_small_shaped_list_zeeden():
-    """GPT-2-small shapes (full 50257x768 embedding, 1024x768 positions, two full-width layers):
-    matrices take the 4-bit path and the 768/2304/3072 LayerNorm and bias vectors the fp32-state
-    path, in one launch."""
-    log("gpt2-small-shaped list, ZE-EDEN x 3 steps")
+    """The GPT-2-small parameter list at full size (50257x768 embedding, 1024x768 positions, all 12
+    layers: 148 tensors, 124,439,808 values): matrices take the 4-bit path and the 768/2304/3072
+    LayerNorm and bias vectors (121,344 values) the fp32-state path, in one launch."""
+    log("gpt2-small list, ZE-EDEN x 3 steps")
     d = 768
     layer = [(d,), (d,), (d, 3 * d), (3 * d,), (d, d), (d,), (d,), (d,), (d, 4 * d), (4 * d,), (4 * d, d), (d,)]
-    shapes = [(50257, d), (1024, d)] + layer * 2 + [(d,), (d,)]
+    shapes = [(50257, d), (1024, d)] + layer * 12 + [(d,), (d,)]
+    assert len(shapes) == 148 and sum(math.prod(s) for s in shapes) == 124_439_808
     args = dict(lr=6e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True)
     out = run_pair(lambda ps: aw.ZEEDENAdamW4Bit(ps, **args), shapes, torch.float32, 3, seed=None)
     compare_pair(*out, "gpt2-small shapes", steps=3)
