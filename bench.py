@@ -108,38 +108,84 @@ def make_grads(shapes, device, seed):
     return grads
 
 
-def cpu_baseline(seconds_target: float = 12.0):
-    """The oracle's eager chunk update (the reference's CPU path, op for op) on a bounded
-    sample: ZE-EDEN steps of one fp32 4096x4096 tensor, on all host threads."""
+CPU_SHAPE = (4096, 4096)
+CPU_RECIPES = {"ZE-EDEN": ("nf4", "dyn4_nz", True), "ZIP-SR": ("nf4", "dyn4_upd_sr_fp32read", False)}
+
+
+def cpu_leg(seconds_target: float) -> dict:
+    """One leg of the CPU baseline, in a process that never touches the GPU: the oracle's eager
+    chunk update (the reference's CPU path, op for op) on one fp32 4096x4096 tensor per recipe,
+    with the draws of ZIP-SR from torch's CPU generator as the reference takes them; the median
+    step time of each recipe after one untimed step."""
     import torch
 
     from oracle import reference_step as ref
 
+    out = {"threads": torch.get_num_threads(), "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
+           "ms_per_step": {}, "steps": {}}
     gen = torch.Generator().manual_seed(0)
-    shape = (4096, 4096)
-    p = torch.randn(shape, generator=gen) * 0.02
-    oracle = ref.Oracle([p], ref.Hyper(), ["nf4"], ["dyn4_nz"], [True])
-    g = torch.randn(shape, generator=gen) * 1e-3
-    oracle.step([g])  # state initialization outside the timed steps
-    times = []
-    start = time.perf_counter()
-    while time.perf_counter() - start < seconds_target or len(times) < 3:
-        t0 = time.perf_counter()
-        oracle.step([g])
-        times.append(time.perf_counter() - t0)
-    per_step = statistics.median(times)
-    n = p.numel()
+    for name, (m1, m2, eden) in CPU_RECIPES.items():
+        p = torch.randn(CPU_SHAPE, generator=gen) * 0.02
+        oracle = ref.Oracle([p], ref.Hyper(), [m1], [m2], [eden], seed=0)
+        g = torch.randn(CPU_SHAPE, generator=gen) * 1e-3
+        oracle.step([g])  # state initialization outside the timed steps
+        times = []
+        start = time.perf_counter()
+        while time.perf_counter() - start < seconds_target / len(CPU_RECIPES) or len(times) < 3:
+            t0 = time.perf_counter()
+            oracle.step([g])
+            times.append(time.perf_counter() - t0)
+        out["ms_per_step"][name] = statistics.median(times) * 1e3
+        out["steps"][name] = len(times)
+    return out
+
+
+def cpu_baseline(seconds_target: float = 20.0):
+    """The CPU baseline: the same sample timed in two fresh child processes, on all host threads
+    and at OMP_NUM_THREADS=2 (the reference's CI setting, .github/workflows/ci.yml:17).  `value`
+    is the all-threads rate over both recipes (values x recipes / time), the unit of the GPU
+    figure; it is measured on a 16.8M-value tensor and quoted as a rate, not on the 8.03G-value
+    parameter set."""
+    import subprocess
+
+    legs = []
+    for threads in (None, 2):
+        env = dict(os.environ)
+        if threads is not None:
+            env["OMP_NUM_THREADS"] = str(threads)
+        env["CUDA_VISIBLE_DEVICES"] = ""
+        env["HIP_VISIBLE_DEVICES"] = ""
+        proc = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-leg",
+                               "--cpu-seconds", str(seconds_target / 2)],
+                              env=env, capture_output=True, text=True, cwd=HERE, timeout=600)
+        if proc.returncode != 0:
+            raise RuntimeError(f"cpu baseline leg failed: {proc.stderr[-2000:]}")
+        legs.append(json.loads(proc.stdout.strip().splitlines()[-1]))
+    n = CPU_SHAPE[0] * CPU_SHAPE[1]
     cpu = "unknown CPU"
     try:
         with open("/proc/cpuinfo") as f:
             cpu = next(line.split(":", 1)[1].strip() for line in f if line.startswith("model name"))
     except (OSError, StopIteration):
         pass
-    return {"value": n / per_step / 1e9, "unit": "Gelem/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"oracle ZE-EDEN eager chunk update, fp32 4096x4096 (16.8M values), median of {len(times)} "
-                      f"steps, {per_step * 1e3:.1f} ms/step, {torch.get_num_threads()} threads "
-                      f"(os.cpu_count {os.cpu_count()}, OMP_NUM_THREADS {os.environ.get('OMP_NUM_THREADS')}), "
-                      f"{cpu}, ATen {torch.backends.cpu.get_cpu_capability()}"}
+    import torch
+
+    def rate(leg):
+        return n * len(CPU_RECIPES) / (sum(leg["ms_per_step"].values()) * 1e-3) / 1e9
+
+    main_leg, ci_leg = legs
+    detail = "; ".join(f"{leg['threads']} threads: " + ", ".join(f"{k} {v:.1f} ms/step ({leg['steps'][k]} steps)"
+                                                                for k, v in leg["ms_per_step"].items())
+                       for leg in legs)
+    return {"value": rate(main_leg), "unit": "Gelem/s", "cores": main_leg["threads"], "kind": "port",
+            "sample": f"oracle eager chunk update (the reference's CPU path), one fp32 4096x4096 tensor "
+                      f"(16.8M values) per recipe, ZE-EDEN + ZIP-SR, median step times, in child processes "
+                      f"off the GPU; {detail}; {cpu}, ATen {torch.backends.cpu.get_cpu_capability()}, "
+                      f"os.cpu_count {os.cpu_count()}",
+            "legs": [{"threads": leg["threads"], "omp_num_threads": leg["omp_num_threads"],
+                      "ms_per_step": {k: round(v, 2) for k, v in leg["ms_per_step"].items()},
+                      "gelem_s": round(rate(leg), 5)} for leg in legs],
+            "ci_threads_value": rate(ci_leg)}
 
 
 def measured_traffic(config: str):
@@ -167,13 +213,17 @@ def main():
     ap.add_argument("--recipes", default="zeeden,zipsr",
                     help="comma-separated: zeeden, zipsr, or a research m2 scheme: " + ", ".join(RESEARCH_M2))
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--cpu-leg", action="store_true", help=argparse.SUPPRESS)  # child process of the CPU baseline
     ap.add_argument("--clip-grad-norm", type=float, default=None, metavar="MAX_NORM",
                     help="clip the gradients to this global 2-norm before every step, fused into the step "
                          "(QuantizedAdamW.clip_grad_norm_), and also time torch.nn.utils.clip_grad_norm_ + step")
     ap.add_argument("--copy-probe-gb", type=float, default=0.0,
                     help="also run plain device copies of this many GB (calibrates HBM byte counters)")
     args = ap.parse_args()
+    if args.cpu_leg:
+        print(json.dumps(cpu_leg(args.cpu_seconds)), flush=True)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the optimizer step is replica-local "
               "and this build runs no multi-GPU configuration", file=sys.stderr)
