@@ -55,3 +55,43 @@ class PhiloxStream:
         if offset % 128:
             raise ValueError(f"quantization RNG position {offset} is not a multiple of 128")
         self.seed, self.offset = seed, offset
+
+
+class GlobalStream:
+    """The stream of a (moment, device) when ``quant_rng_seed`` is None: the reference then draws
+    every stochastic write from torch's default generator of the device
+    (``torch.rand(..., generator=None)``, ``_optimized_quantization.py:37-43``).  Here each write
+    keys Philox4x32-10 with that generator's seed, mixed with the moment's constant, and takes its
+    positions from the generator's offset, which it moves past them.  So reseeding torch, or any
+    other random number torch draws on the device, changes the next writes' draws, and saving and
+    restoring torch's RNG state (``torch.cuda.get_rng_state``) saves and restores them, as with the
+    reference.  Positions are 128-value groups; each group moves the generator's offset by 4 (its
+    offsets are multiples of 4)."""
+
+    __slots__ = ("generator", "mix")
+    UNIT = 4
+
+    def __init__(self, generator: torch.Generator, mix: int):
+        self.generator = generator
+        self.mix = int(mix) & 0xFFFFFFFFFFFFFFFF
+
+    @property
+    def seed(self) -> int:
+        return (self.generator.initial_seed() ^ self.mix) & 0xFFFFFFFFFFFFFFFF
+
+    @property
+    def offset(self) -> int:
+        return -(-self.generator.get_offset() // self.UNIT) * 128
+
+    @offset.setter
+    def offset(self, value: int) -> None:
+        self.generator.set_offset(int(value) // 128 * self.UNIT)
+
+    def take(self, n: int) -> int:
+        """Reserve ``n`` positions and return the first (a multiple of 128)."""
+        first = self.offset
+        self.offset = first + (int(n) + 127) // 128 * 128
+        return first
+
+    def advance(self, n: int) -> None:
+        self.take(n)

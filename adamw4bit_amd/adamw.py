@@ -40,7 +40,7 @@ from torch.optim import optimizer as _torch_optimizer
 from torch.optim.optimizer import Optimizer
 
 from . import _lib, _ops
-from ._rng import PhiloxStream
+from ._rng import GlobalStream, PhiloxStream
 from .quantization import (
     LOOKAHEAD_SCHEMES,
     NEXT_BIAS_SCHEMES,
@@ -87,7 +87,8 @@ def _step_fields() -> np.dtype:
     """View of a launch-table row holding only what a reused plan rewrites each step: the
     gradient address and scale pointer, the flags word with the seven fp32 step constants
     after it (``words``, 8 x 32 bits), the m2 update-SR constants (``m2_sr``, 3 x 32 bits)
-    and both random-stream positions."""
+    and both random-stream keys and positions (a stream drawn from torch's generator takes
+    that generator's current seed)."""
     T = _lib.TENSOR
     m1, m2 = T.fields["m1"][1], T.fields["m2"][1]
     M = T.fields["m2"][0]
@@ -95,10 +96,12 @@ def _step_fields() -> np.dtype:
     assert [T.fields[k][1] for k in words] == [T.fields["flags"][1] + 4 * i for i in range(8)]
     assert [M.fields[k][1] for k in ("sr_bias", "sr_bias_rcp", "sr_eps")] == [M.fields["sr_bias"][1] + 4 * i
                                                                             for i in range(3)]
-    return np.dtype({"names": ["grad", "grad_scale", "words", "m2_sr", "m1_rng_offset", "m2_rng_offset"],
-                     "formats": ["<u8", "<u8", ("<u4", 8), ("<u4", 3), "<u8", "<u8"],
+    return np.dtype({"names": ["grad", "grad_scale", "words", "m2_sr", "m1_rng_seed", "m2_rng_seed",
+                               "m1_rng_offset", "m2_rng_offset"],
+                     "formats": ["<u8", "<u8", ("<u4", 8), ("<u4", 3), "<u8", "<u8", "<u8", "<u8"],
                      "offsets": [T.fields["grad"][1], T.fields["grad_scale"][1], T.fields["flags"][1],
-                                 m2 + M.fields["sr_bias"][1], m1 + M.fields["rng_offset"][1],
+                                 m2 + M.fields["sr_bias"][1], m1 + M.fields["rng_seed"][1],
+                                 m2 + M.fields["rng_seed"][1], m1 + M.fields["rng_offset"][1],
                                  m2 + M.fields["rng_offset"][1]],
                      "itemsize": T.itemsize})
 
@@ -345,7 +348,7 @@ class QuantizedAdamW(Optimizer):
         self._quant_rng_seed = quant_rng_seed
         self._quant_generators: Dict[str, Dict[str, PhiloxStream]] = {"m1": {}, "m2": {}}
         self._pending_quant_rng_states: Dict[str, Dict[str, torch.Tensor]] = {"m1": {}, "m2": {}}
-        self._global_streams: Dict[str, Dict[str, PhiloxStream]] = {"m1": {}, "m2": {}}
+        self._global_streams: Dict[str, Dict[str, GlobalStream]] = {"m1": {}, "m2": {}}
         defaults = dict(lr=lr, betas=betas, eps=eps, weight_decay=weight_decay,
                         block_size=block_size, quant_scheme=quant_scheme, use_eden_m2=use_eden_m2,
                         m1_quant_scheme=m1_scheme, m2_quant_scheme=m2_scheme,
@@ -426,20 +429,26 @@ class QuantizedAdamW(Optimizer):
         generators[device_key] = stream
         return stream
 
-    def _stream(self, moment: str, device: torch.device) -> PhiloxStream:
+    def _stream(self, moment: str, device: torch.device):
         """The stream a stochastic write of ``moment`` draws from on ``device``."""
         stream = self._quant_generator(moment, device)
         if stream is not None:
             return stream
-        # quant_rng_seed=None: the reference draws from torch's global RNG; here a
-        # per-(moment, device) stream keyed once from torch's global generator.
+        # quant_rng_seed=None: the reference draws from torch's default generator of the device;
+        # so does this stream, write by write (GlobalStream).
         key = str(device)
         streams = self._global_streams[moment]
         if key not in streams:
-            streams[key] = PhiloxStream(int(torch.randint(0, (1 << 62) - 1, (1,)).item()))
+            if device.type != "cuda":
+                raise NotImplementedError("the fused 4-bit step runs on HIP devices only")
+            torch.cuda.init()  # fills torch.cuda.default_generators
+            generator = torch.cuda.default_generators[device.index if device.index is not None
+                                                      else torch.cuda.current_device()]
+            # the moment's constant (adamw.py:122-125) spread over 64 bits
+            streams[key] = GlobalStream(generator, (self._QUANT_RNG_OFFSETS[moment] * 0x9E3779B97F4A7C15))
         return streams[key]
 
-    def _all_streams(self) -> List[PhiloxStream]:
+    def _all_streams(self) -> list:
         """Every random stream this optimizer has opened."""
         return [s for table in (self._quant_generators, self._global_streams) for streams in table.values()
                 for s in streams.values()]
@@ -1247,6 +1256,7 @@ class _LaunchPlan:
              refs_t), g0 in zip(self.devices, grads):
             index = np.empty(len(entries), dtype=np.intp)
             offsets = {"m1": fields["m1_rng_offset"].copy(), "m2": fields["m2_rng_offset"].copy()}
+            seeds = {"m1": fields["m1_rng_seed"].copy(), "m2": fields["m2_rng_seed"].copy()}
             for i, (state, gi, m2_scheme, sr, numel) in enumerate(entries):
                 step = state["step"] + 1
                 state["step"] = step
@@ -1256,6 +1266,7 @@ class _LaunchPlan:
                     consts.append(_StepConstants(self.groups[gi][0], step, m2_scheme))
                 index[i] = k
                 for moment, stream in sr:
+                    seeds[moment][i] = stream.seed
                     offsets[moment][i] = stream.take(numel)
             # the flags word and the seven fp32 step constants (bit patterns), and the m2
             # update-SR constants of the rows whose m2 is quantized
@@ -1271,6 +1282,8 @@ class _LaunchPlan:
                                                   dtype=np.float32)[index[qrows]].view(np.uint32)
             fields["grad"] = g0
             fields["grad_scale"] = 0 if coef is None else coef.data_ptr()
+            fields["m1_rng_seed"] = seeds["m1"]
+            fields["m2_rng_seed"] = seeds["m2"]
             fields["m1_rng_offset"] = offsets["m1"]
             fields["m2_rng_offset"] = offsets["m2"]
             read = [p.grad for p in params]

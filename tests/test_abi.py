@@ -368,6 +368,8 @@ def test_plan_step_view_covers_exactly_the_per_step_fields():
     words = np.array([(3, 0.5, 0.25, 0.75, -1e-3, 0.125, 8.0, 1e-8)] * 2, dtype=_STEP_WORDS)
     view["words"] = words.view(np.uint32).reshape(-1, 8)
     view["m2_sr"] = np.array([[1.5, 2.5, 3.5]] * 2, dtype=np.float32).view(np.uint32)
+    view["m1_rng_seed"] = [31, 32]
+    view["m2_rng_seed"] = [33, 34]
     view["m1_rng_offset"] = [21, 22]
     view["m2_rng_offset"] = [23, 24]
     assert list(row["grad"]) == [11, 12] and list(row["grad_scale"]) == [13, 14]
@@ -378,12 +380,13 @@ def test_plan_step_view_covers_exactly_the_per_step_fields():
     assert np.all(row["m2"]["sr_bias"] == 1.5) and np.all(row["m2"]["sr_bias_rcp"] == 2.5)
     assert np.all(row["m2"]["sr_eps"] == 3.5)
     assert list(row["m1"]["rng_offset"]) == [21, 22] and list(row["m2"]["rng_offset"]) == [23, 24]
+    assert list(row["m1"]["rng_seed"]) == [31, 32] and list(row["m2"]["rng_seed"]) == [33, 34]
     # every byte outside those fields is untouched
     written = np.zeros(T.itemsize, dtype=bool)
     for name in _STEP_FIELDS.names:
         dt, off = _STEP_FIELDS.fields[name][:2]
         written[off:off + dt.itemsize] = True
-    assert written.sum() == 8 + 8 + 32 + 12 + 8 + 8
+    assert written.sum() == 8 + 8 + 32 + 12 + 4 * 8
     assert np.array_equal(raw[:, ~written], before[:, ~written])
 
 

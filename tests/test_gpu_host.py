@@ -108,7 +108,7 @@ def test_parameter_at_odd_offset_matches_oracle(recipe):
     m2 = "dyn4_upd_sr_fp32read" if recipe == "zipsr" else "dyn4_nz"
     cpu = [init.clone()]
     oracle = ref.Oracle(cpu, ref.Hyper(), ["nf4"], [m2], [recipe == "zeeden"], seed=kw["quant_rng_seed"],
-                        draw_fn=H.PhiloxMirror(opt, H.DEVICE))
+                        draw_fn=H.PhiloxMirror(opt, H.DEVICE), usr_sqrt="cr")
     gbuf = torch.zeros(n + 3, device=H.DEVICE)
     for _ in range(3):
         g = H.heavy_tailed(shape, gen)
@@ -316,6 +316,76 @@ def test_failed_launch_is_undone(monkeypatch):
         torch.cuda.synchronize()
         for i, (a, b) in enumerate(zip(pa, pb)):
             same_state(oa, a, ob, b, (k, i))
+
+
+# ---------------------------------------------------------------------------
+# quant_rng_seed=None: draws come from torch's generator of the device
+# ---------------------------------------------------------------------------
+
+def test_unseeded_draws_follow_torch_generator(monkeypatch):
+    """With ``quant_rng_seed=None`` the reference's stochastic writes draw from torch's default
+    generator (``_optimized_quantization.py:37-43``): reseeding torch reproduces a run, another
+    seed or another torch draw between steps changes it, and the cached plan takes the
+    generator's current seed and position at every step."""
+    log("unseeded streams follow torch's generator")
+    gen = torch.Generator().manual_seed(23)
+    shapes = [(64, 256), (512,)]
+    init = [torch.randn(s, generator=gen) * 0.02 for s in shapes]
+    grads = [grads_like(shapes, gen) for _ in range(3)]
+    real = _lib.fused_step
+    tables = []
+
+    def recording(table, stream):
+        tables.append(table.copy())
+        real(table, stream)
+
+    monkeypatch.setattr(_lib, "fused_step", recording)
+
+    def run(seeds, between=None):
+        params = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
+        opt = aw.ZIPSRAdamW4Bit(params, optimized=True, quant_rng_seed=None, **ARGS)
+        for k, gs in enumerate(grads):
+            if seeds[k] is not None:
+                torch.manual_seed(seeds[k])
+            if between is not None and k == 1:
+                between()
+            for p, g in zip(params, gs):
+                p.grad = g.clone()
+            opt.step()
+        torch.cuda.synchronize()
+        return opt, params
+
+    def codes(opt, params):
+        return [H.bits(opt.state[p]["m2_code"]) for p in params if "m2_code" in opt.state[p]]
+
+    oa, pa = run([3, None, None])
+    ob, pb = run([3, None, None])
+    for i, (a, b) in enumerate(zip(pa, pb)):
+        same_state(oa, a, ob, b, ("same seed", i))
+    oc, pc = run([4, None, None])
+    assert any(not torch.equal(x, y) for x, y in zip(codes(oa, pa), codes(oc, pc)))
+    # a torch draw on the device between steps moves the stream
+    od, pd = run([3, None, None], between=lambda: torch.rand(1000, device=H.DEVICE))
+    assert any(not torch.equal(x, y) for x, y in zip(codes(oa, pa), codes(od, pd)))
+    # reseeding before the third step: the cached plan's rows take the new key and position
+    from adamw4bit_amd.adamw import _LaunchPlan
+    prepare, planned = _LaunchPlan.prepare, []
+
+    def counting(self, opt):
+        out = prepare(self, opt)
+        planned.append(out is not None)
+        return out
+
+    monkeypatch.setattr(_LaunchPlan, "prepare", counting)
+    tables.clear()
+    oe, pe = run([3, None, 9])
+    assert planned == [True, True]  # steps 2 and 3 reuse the plan
+    mix = aw.QuantizedAdamW._QUANT_RNG_OFFSETS["m2"] * 0x9E3779B97F4A7C15 & (2 ** 64 - 1)
+    last = tables[-1]
+    quantized = last["m2"]["rounding"] != _lib.ROUND_FP32
+    assert quantized.any()
+    assert set(last["m2"]["rng_seed"][quantized].tolist()) == {9 ^ mix}
+    assert last["m2"]["rng_offset"][quantized].min() == 0
 
 
 # ---------------------------------------------------------------------------
