@@ -142,15 +142,29 @@ def _endpoints(x: torch.Tensor, cb: torch.Tensor):
     return lower, upper, cb[lower.long()], cb[upper.long()]
 
 
+def sqrt_correctly_rounded(v: torch.Tensor) -> torch.Tensor:
+    """The correctly rounded fp32 square root: the float64 root of an fp32 value, rounded once
+    to fp32 (float64 carries more than the 2 * 24 + 2 bits that make this single rounding exact)."""
+    return v.to(torch.float64).sqrt().to(torch.float32)
+
+
 def encode(values: torch.Tensor, mode: str, *, eden: bool = False,
            draws: Optional[torch.Tensor] = None, bias: float = 1.0, eps: float = 1e-8,
-           guards: bool = True) -> Tuple[torch.Tensor, torch.Tensor]:
+           guards: bool = True, usr_sqrt: str = "aten") -> Tuple[torch.Tensor, torch.Tensor]:
     """float32 values (length a multiple of 128) -> (unpacked uint8 codes, float32 scales).
 
     ``guards=True`` is the optimized path (``_optimized_quantization.py:46-88`` with the
     rounding of ``_compiled_quantization.py``); ``guards=False`` is the reference
     step's strategies (``quantization.py:254-377``, ``:898-971``).
+
+    ``usr_sqrt`` is the square root of the update-SR preconditioner
+    ``1 / (sqrt((s * l) / bias) + eps)`` (``_compiled_quantization.py:74-109``): ``"aten"``
+    is ATen's CPU ``sqrt`` as the reference calls it (vectorised, within one ulp of the
+    correctly rounded root, host-dependent), ``"cr"`` the correctly rounded root.  Every other
+    operation is the same in both.
     """
+    if usr_sqrt not in ("aten", "cr"):
+        raise ValueError(f"usr_sqrt must be 'aten' or 'cr', got {usr_sqrt!r}")
     blocked = values.view(-1, BLOCK)
     scales = blocked.abs().max(dim=1).values.clamp_min(1e-12)
     x = blocked / scales.unsqueeze(1)
@@ -175,7 +189,8 @@ def encode(values: torch.Tensor, mode: str, *, eden: bool = False,
 
         def preconditioner(level: torch.Tensor) -> torch.Tensor:
             v_hat = (s * level / bias_c).clamp_min(0.0)
-            return torch.reciprocal(v_hat.sqrt() + eps)  # ``1.0 / t`` is reciprocal(t) * 1.0
+            root = v_hat.sqrt() if usr_sqrt == "aten" else sqrt_correctly_rounded(v_hat)
+            return torch.reciprocal(root + eps)  # ``1.0 / t`` is reciprocal(t) * 1.0
 
         f_a, f_b, f_x = preconditioner(a), preconditioner(b), preconditioner(x)
         den = f_a - f_b
@@ -345,7 +360,7 @@ class Oracle:
     def __init__(self, params: List[torch.Tensor], hyper: Hyper, m1_schemes: List[str],
                  m2_schemes: List[str], eden: List[bool], *, seed: Optional[int] = None,
                  optimized: bool = True, chunk: int = CHUNK_NUMEL, record_draws: bool = False,
-                 draw_fn=None):
+                 draw_fn=None, usr_sqrt: str = "aten"):
         self.params = params
         self.hyper = hyper
         self.m1_schemes = list(m1_schemes)
@@ -366,6 +381,9 @@ class Oracle:
         # Optional source of uniforms: draw_fn(moment, n) -> n float32 values, used in place of
         # the CPU generators (to replay the draws a device implementation consumed).
         self.draw_fn = draw_fn
+        # Square root of the update-SR preconditioners (``encode``): "aten" as the reference
+        # computes it on this host, "cr" correctly rounded.
+        self.usr_sqrt = usr_sqrt
         self.draw_log: List[DrawLog] = []
         self.draw_counts = {"m1": 0, "m2": 0}
         self._param_optimized = True  # the optimized backend accepts the parameter's schemes
@@ -401,7 +419,7 @@ class Oracle:
             tile = n  # adamw.py:524-545 encodes the whole zero tensor
         draws = self._draw(moment, tile, index, 0, log=False) if is_stochastic(scheme) else None
         codes, scales = encode(torch.zeros(tile, dtype=torch.float32), scheme, eden=eden,
-                               draws=draws, guards=optimized)
+                               draws=draws, guards=optimized, usr_sqrt=self.usr_sqrt)
         byte = pack(codes)[:1]
         return MomentState(scheme, codes=byte.expand((n + 1) // 2).clone(),
                            scales=scales[:1].expand(n // BLOCK).clone())
@@ -486,10 +504,11 @@ class Oracle:
         draws = self._draw("m2", n, index, st.step, True)
         store_eden = s2 in STORE_EDEN_SCHEMES
         codes, read_scales = encode(m2, s2, eden=eden and not store_eden, draws=draws, bias=bc2, eps=hp.eps,
-                                    guards=False)
+                                    guards=False, usr_sqrt=self.usr_sqrt)
         stored_scales = read_scales
         if store_eden:
-            _, stored_scales = encode(m2, s2, eden=True, draws=draws, bias=bc2, eps=hp.eps, guards=False)
+            _, stored_scales = encode(m2, s2, eden=True, draws=draws, bias=bc2, eps=hp.eps, guards=False,
+                                      usr_sqrt=self.usr_sqrt)
         packed = pack(codes)
         m2_read = decode(packed, read_scales, s2, n)
         den = (m2_read.sqrt() / math.sqrt(bc2)).add_(hp.eps)
@@ -548,6 +567,6 @@ class Oracle:
         if ms.scheme == "fp32":
             return  # the read view was updated in place
         codes, scales = encode(value, ms.scheme, eden=eden, draws=draws, bias=bias, eps=eps,
-                               guards=self.optimized and self._param_optimized)
+                               guards=self.optimized and self._param_optimized, usr_sqrt=self.usr_sqrt)
         ms.codes[start // 2:(stop + 1) // 2] = pack(codes)
         ms.scales[start // BLOCK:stop // BLOCK] = scales

@@ -162,6 +162,62 @@ def test_update_sr_is_preconditioner_unbiased():
     assert ((expectation - target).abs() <= slack).all()
 
 
+def test_correctly_rounded_sqrt_is_correctly_rounded():
+    """sqrt_correctly_rounded(v) = r with (r - ulp/2)^2 <= v <= (r + ulp/2)^2, checked in float64,
+    where these squares are exact (25-bit operands), over every fp32 binade, with subnormals."""
+    rng = np.random.default_rng(21)
+    v = np.concatenate([
+        (rng.random(200_000) * 2.0 ** rng.integers(-149, 128, 200_000)).astype(np.float32),
+        np.array([0.0, 1.0, 2.0, 4.0, 0.25, 1e-45, 3.4e38], dtype=np.float32)])
+    v = v[np.isfinite(v)]
+    r = ref.sqrt_correctly_rounded(torch.from_numpy(v)).numpy().astype(np.float64)
+    h = np.spacing(r.astype(np.float32)).astype(np.float64) / 2
+    lo = np.where(r > 0, (r - h) ** 2, 0.0)
+    hi = (r + h) ** 2
+    assert np.all(lo <= v) and np.all(v <= hi)
+    # ATen's CPU root on this host is within one ulp of it
+    aten = torch.from_numpy(v).sqrt().numpy().astype(np.float64)
+    assert np.all(np.abs(aten - r) <= 2 * h)
+
+
+def test_update_sr_codes_depend_on_the_square_root_only_where_the_roots_differ():
+    """The oracle's two update-SR square roots ("aten", the reference's host call, and "cr")
+    change a code only where ATen's root of one of the value's three preconditioner arguments
+    (its level pair and itself) is not the correctly rounded one.  The draws sit exactly on the
+    correctly rounded probability, the draw most sensitive to the difference, so the check is
+    not vacuous: codes do differ, and each difference is such a value."""
+    gen = torch.Generator().manual_seed(29)
+    blocks = 4096
+    m = (torch.rand(blocks, 128, generator=gen) ** 4) * torch.exp(torch.randn(blocks, 1, generator=gen) * 4 - 14)
+    values = m.reshape(-1)
+    bias, eps = 0.0975, 1e-8
+    scales = m.abs().amax(dim=1).clamp_min(1e-12)
+    x = (m / scales[:, None])
+    cb = ref.codebook("dyn4")
+    _, _, a, b = ref._endpoints(x, cb)
+    s = scales[:, None]
+
+    def arg(level):
+        return (s * level / bias).clamp_min(0.0)
+
+    def f(level, root):
+        return torch.reciprocal(root(arg(level)) + eps)
+
+    cr = ref.sqrt_correctly_rounded
+    fa, fb, fx = f(a, cr), f(b, cr), f(x, cr)
+    p = ((fx - fb) / (fa - fb).clamp_min(1e-30)).clamp(0.0, 1.0)
+    draws = p.contiguous()
+    got = {mode: ref.encode(values, "dyn4_upd_sr_fp32read", draws=draws, bias=bias, eps=eps, usr_sqrt=mode)[0]
+           for mode in ("aten", "cr")}
+    differ = (got["aten"] != got["cr"]).view(blocks, 128)
+    roots_agree = torch.ones_like(differ)
+    for level in (a, b, x):
+        v = arg(level)
+        roots_agree &= v.sqrt() == cr(v)
+    assert int(differ.sum()) > 0
+    assert not bool((differ & roots_agree).any())
+
+
 @pytest.mark.parametrize("recipe", ["zeeden", "zipsr"])
 def test_first_step_equals_torch_adamw(recipe):
     # test_checkpoint_io.py:173-185 (ZE-EDEN) and test_dyn4_la_upd_sr.py:151-191 (ZIP-SR family).
