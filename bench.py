@@ -94,7 +94,9 @@ def make_grads(shapes, device, seed):
 
     gen = torch.Generator(device=device).manual_seed(seed)
     grads = []
-    for s in shapes:
+    for i, s in enumerate(shapes):
+        if i and i % 64 == 0:
+            print(f"[bench] gradients {i}/{len(shapes)}", file=sys.stderr, flush=True)
         z = torch.randn(s, generator=gen, device=device)
         chi2 = torch.zeros(s, device=device)
         for _ in range(3):
@@ -204,60 +206,18 @@ def measured_traffic(config: str):
     return out, os.path.relpath(path, HERE)
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="llama3-8b", choices=sorted(CONFIGS))
-    ap.add_argument("--recipes", default="zeeden,zipsr",
-                    help="comma-separated: zeeden, zipsr, or a research m2 scheme: " + ", ".join(RESEARCH_M2))
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=20.0)
-    ap.add_argument("--cpu-leg", action="store_true", help=argparse.SUPPRESS)  # child process of the CPU baseline
-    ap.add_argument("--clip-grad-norm", type=float, default=None, metavar="MAX_NORM",
-                    help="clip the gradients to this global 2-norm before every step, fused into the step "
-                         "(QuantizedAdamW.clip_grad_norm_), and also time torch.nn.utils.clip_grad_norm_ + step")
-    ap.add_argument("--copy-probe-gb", type=float, default=0.0,
-                    help="also run plain device copies of this many GB (calibrates HBM byte counters)")
-    args = ap.parse_args()
-    if args.cpu_leg:
-        print(json.dumps(cpu_leg(args.cpu_seconds)), flush=True)
-        return
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the optimizer step is replica-local "
-              "and this build runs no multi-GPU configuration", file=sys.stderr)
-        sys.exit(2)
-
+def build_workload(config: str, recipe_names: str, clip, device):
+    """Parameters (with gradients) and optimizers of one workload: (shapes, params, recipes,
+    algorithmic bytes per launch of each recipe, gradient bytes); recipes are (name, optimizer,
+    algorithmic bytes)."""
     import torch
 
     import adamw4bit_amd as aw
 
-    device = torch.device("cuda", 0)
-    torch.cuda.set_device(device)
-    if args.copy_probe_gb > 0:
-        # A plain copy of known size: its FETCH_SIZE / WRITE_SIZE per dispatch calibrate the
-        # counters; copy and add timings give the streaming bandwidth torch's kernels reach.
-        n = int(args.copy_probe_gb * 1e9) // 4
-        src = torch.ones(n, device=device)
-        dst = torch.empty_like(src)
-        for name, fn, nbytes in (("copy", lambda: dst.copy_(src), 8 * n), ("add", lambda: dst.add_(src), 12 * n)):
-            fn()
-            torch.cuda.synchronize()
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
-            for _ in range(5):
-                fn()
-            b.record()
-            torch.cuda.synchronize()
-            ms = a.elapsed_time(b) / 5
-            print(f"[bench] {name} probe: {nbytes} bytes in {ms:.3f} ms = {nbytes / ms / 1e6:.0f} GB/s",
-                  file=sys.stderr, flush=True)
-        del src, dst
-    shapes = CONFIGS[args.config]()
+    shapes = CONFIGS[config]()
     numels = [math.prod(s) for s in shapes]
     total = sum(numels)
-    mixed = args.config == "llama3-8b-bf16-mixed"
+    mixed = config == "llama3-8b-bf16-mixed"
     dtype = torch.bfloat16 if mixed else torch.float32
     esize = 2 if mixed else 4
 
@@ -280,7 +240,7 @@ def main():
         recipes.append(("mixed", opt, algo))
     else:
         algo = sum(n * bytes_per_value(n) for n in numels)
-        for r in args.recipes.split(","):
+        for r in recipe_names.split(","):
             if r == "zeeden":
                 recipes.append(("ZE-EDEN", aw.ZEEDENAdamW4Bit(params, optimized=True), algo))
             elif r == "zipsr":
@@ -299,28 +259,33 @@ def main():
                 raise SystemExit(f"unknown recipe {r}")
     algo_bytes = {name: a for name, _, a in recipes}
     grad_bytes = sum(p.grad.numel() * p.grad.element_size() for p in params)
-    if args.clip_grad_norm is not None:  # the fused clip adds one read of every gradient
+    if clip is not None:  # the fused clip adds one read of every gradient
         algo_bytes = {name: a + grad_bytes for name, a in algo_bytes.items()}
-    print(f"[bench] {args.config}: {len(shapes)} tensors, {total:,} values, "
+    print(f"[bench] {config}: {len(shapes)} tensors, {total:,} values, "
           f"{ {k: round(v / 1e9, 2) for k, v in algo_bytes.items()} } GB algorithmic per launch",
           file=sys.stderr, flush=True)
     torch.cuda.synchronize()
-    print(f"[bench] allocated {torch.cuda.memory_allocated() / 1e9:.1f} GB; warmup {args.warmup}",
-          file=sys.stderr, flush=True)
+    print(f"[bench] allocated {torch.cuda.memory_allocated() / 1e9:.1f} GB", file=sys.stderr, flush=True)
+    return shapes, params, recipes, algo_bytes, grad_bytes
 
-    stream = torch.cuda.current_stream(device)
-    clip = args.clip_grad_norm
-    for _ in range(args.warmup):
+
+
+def time_launches(recipes, steps: int, warmup: int, clip, stream):
+    """``warmup`` untimed steps, then ``steps`` timed steps of every recipe: each launch bracketed
+    by HIP events on the launch stream.  Returns the launch times (ms) per recipe, the wall time
+    of the timed steps (s) and the event pairs around the fused clip prologues."""
+    import torch
+
+    for _ in range(warmup):
         for _, opt, _ in recipes:
             if clip is not None:
                 opt.clip_grad_norm_(clip)
             opt.step()
     torch.cuda.synchronize()
-
     events = {name: [] for name, _, _ in recipes}
     norm_events = []
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         for name, opt, _ in recipes:
             start, mid, stop = (torch.cuda.Event(enable_timing=True) for _ in range(3))
             start.record(stream)
@@ -333,26 +298,93 @@ def main():
             norm_events.append((start, mid))
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    launch_ms = {name: [a.elapsed_time(b) for a, b in ev] for name, ev in events.items()}
+    return {name: [a.elapsed_time(b) for a, b in ev] for name, ev in events.items()}, wall, norm_events
+
+
+def time_unfused(recipes, params, steps: int, warmup: int, clip, stream):
+    """The unfused path a trainer runs: torch's clip (norm pass + in-place multiply), then the
+    step; mean ms per recipe."""
+    import torch
+
+    unfused = {}
+    for name, opt, _ in recipes:
+        for _ in range(warmup):
+            torch.nn.utils.clip_grad_norm_(params, clip)
+            opt.step()
+        ev = []
+        for _ in range(steps):
+            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            torch.nn.utils.clip_grad_norm_(params, clip)
+            opt.step()
+            stop.record(stream)
+            ev.append((start, stop))
+        torch.cuda.synchronize()
+        unfused[name] = statistics.mean(a.elapsed_time(b) for a, b in ev)
+    return unfused
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="llama3-8b", choices=sorted(CONFIGS))
+    ap.add_argument("--recipes", default="zeeden,zipsr",
+                    help="comma-separated: zeeden, zipsr, or a research m2 scheme: " + ", ".join(RESEARCH_M2))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--no-bf16-mixed", action="store_true",
+                    help="with the default fp32 set, skip the bf16 mixed-scheme set measured after it")
+    ap.add_argument("--cpu-leg", action="store_true", help=argparse.SUPPRESS)  # child process of the CPU baseline
+    ap.add_argument("--clip-grad-norm", type=float, default=None, metavar="MAX_NORM",
+                    help="clip the gradients to this global 2-norm before every step, fused into the step "
+                         "(QuantizedAdamW.clip_grad_norm_), and also time torch.nn.utils.clip_grad_norm_ + step")
+    ap.add_argument("--copy-probe-gb", type=float, default=0.0,
+                    help="also run plain device copies of this many GB (calibrates HBM byte counters)")
+    args = ap.parse_args()
+    if args.cpu_leg:
+        print(json.dumps(cpu_leg(args.cpu_seconds)), flush=True)
+        return
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the optimizer step is replica-local "
+              "and this build runs no multi-GPU configuration", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    if args.copy_probe_gb > 0:
+        # A plain copy of known size: its FETCH_SIZE / WRITE_SIZE per dispatch calibrate the
+        # counters; copy and add timings give the streaming bandwidth torch's kernels reach.
+        n = int(args.copy_probe_gb * 1e9) // 4
+        src = torch.ones(n, device=device)
+        dst = torch.empty_like(src)
+        for name, fn, nbytes in (("copy", lambda: dst.copy_(src), 8 * n), ("add", lambda: dst.add_(src), 12 * n)):
+            fn()
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(5):
+                fn()
+            b.record()
+            torch.cuda.synchronize()
+            ms = a.elapsed_time(b) / 5
+            print(f"[bench] {name} probe: {nbytes} bytes in {ms:.3f} ms = {nbytes / ms / 1e6:.0f} GB/s",
+                  file=sys.stderr, flush=True)
+        del src, dst
+    clip = args.clip_grad_norm
+    shapes, params, recipes, algo_bytes, grad_bytes = build_workload(args.config, args.recipes, clip, device)
+    total = sum(math.prod(sh) for sh in shapes)
+    mixed = args.config == "llama3-8b-bf16-mixed"
+    stream = torch.cuda.current_stream(device)
+    print(f"[bench] warmup {args.warmup}, timed steps {args.steps}", file=sys.stderr, flush=True)
+    launch_ms, wall, norm_events = time_launches(recipes, args.steps, args.warmup, clip, stream)
     prologue = None
     if clip is not None:
-        # The unfused path a trainer runs: torch's clip (norm pass + in-place multiply) then step.
         norm_ms = statistics.mean(a.elapsed_time(b) for a, b in norm_events)
-        unfused = {}
-        for name, opt, _ in recipes:
-            for _ in range(args.warmup):
-                torch.nn.utils.clip_grad_norm_(params, clip)
-                opt.step()
-            ev = []
-            for _ in range(args.steps):
-                start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                start.record(stream)
-                torch.nn.utils.clip_grad_norm_(params, clip)
-                opt.step()
-                stop.record(stream)
-                ev.append((start, stop))
-            torch.cuda.synchronize()
-            unfused[name] = statistics.mean(a.elapsed_time(b) for a, b in ev)
+        unfused = time_unfused(recipes, params, args.steps, args.warmup, clip, stream)
         prologue = {
             "max_grad_norm": clip,
             "fused_clip_and_step_ms": {k: round(statistics.mean(v), 4) for k, v in launch_ms.items()},
@@ -363,15 +395,38 @@ def main():
         }
         print(f"[bench] clip prologue: {prologue}", file=sys.stderr, flush=True)
     per_recipe = {name: statistics.mean(v) for name, v in launch_ms.items()}
+    names = [n for n, _, _ in recipes]
     # The dominant kernel is the recipe with the longest launches; its roofline is reported.
     dominant = max(per_recipe, key=per_recipe.get)
     achieved = algo_bytes[dominant] / (per_recipe[dominant] * 1e-3) / 1e9
     traffic, traffic_source = measured_traffic(args.config)
     ms_per_step = wall * 1e3 / args.steps
-    value = total * len(recipes) * args.steps / wall / 1e9
+    value = total * len(names) * args.steps / wall / 1e9
     print(f"[bench] timed {args.steps} steps in {wall:.3f} s; per-launch ms mean "
           f"{ {k: round(v, 3) for k, v in per_recipe.items()} } min "
           f"{ {k: round(min(v), 3) for k, v in launch_ms.items()} }", file=sys.stderr, flush=True)
+
+    bf16_mixed = None
+    if args.config == "llama3-8b" and clip is None and not args.no_bf16_mixed:
+        # The bf16 mixed-scheme set on the same shapes, measured in the same run after the fp32
+        # set is freed: its launches per step and their share of the HBM roofline.
+        recipes = params = None
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        _, mparams, mrecipes, malgo, _ = build_workload("llama3-8b-bf16-mixed", "", None, device)
+        mlaunch, _, _ = time_launches(mrecipes, args.steps, args.warmup, None, stream)
+        ms = statistics.mean(mlaunch["mixed"])
+        bf16_mixed = {
+            "workload": "llama3-8b-bf16-mixed: Llama-3-8B bf16 parameter set, ZIP-SR schemes, nf4_sr LM head, every "
+                        "tenth tensor an fp32-m2 / EDEN-m2 ablation, 1% zero gradient blocks",
+            "steps": args.steps, "warmup": args.warmup,
+            "step_ms": round(ms, 4),
+            "gelem_s": round(total / (ms * 1e-3) / 1e9, 2),
+            "algorithmic_gb_per_step": round(malgo["mixed"] / 1e9, 4),
+            "hbm_frac": round(malgo["mixed"] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        }
+        print(f"[bench] bf16 mixed set: {bf16_mixed}", file=sys.stderr, flush=True)
+        mrecipes = mparams = None
 
     baseline = None
     if not args.no_cpu_baseline:
@@ -396,16 +451,17 @@ def main():
             "workload": (f"{args.config}: Llama-3-8B bf16 parameter set, ZIP-SR schemes, nf4_sr LM head, every "
                          "tenth tensor an fp32-m2 / EDEN-m2 ablation, one optimizer step per timed step"
                          if mixed else
-                         f"{args.config} fp32 parameter set, one {' + one '.join(n for n, _, _ in recipes)} step "
-                         f"per timed step ({len(recipes)} fused launches)")
+                         f"{args.config} fp32 parameter set, one {' + one '.join(names)} step "
+                         f"per timed step ({len(names)} fused launches)")
                         + (f", each after a fused gradient clip to norm {clip}" if clip is not None else ""),
-            "tensors": len(shapes), "values": total, "recipes": [n for n, _, _ in recipes],
+            "tensors": len(shapes), "values": total, "recipes": names,
             "launch_ms": {k: round(v, 4) for k, v in per_recipe.items()},
             "gelem_s_per_recipe": {k: round(total / (v * 1e-3) / 1e9, 2) for k, v in per_recipe.items()},
             "hbm_frac_per_recipe": {k: round(algo_bytes[k] / (v * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
                                     for k, v in per_recipe.items()},
             "algorithmic_gb_per_launch": {k: round(v / 1e9, 4) for k, v in algo_bytes.items()},
             **({"prologue": prologue} if prologue else {}),
+            **({"bf16_mixed": bf16_mixed} if bf16_mixed else {}),
         },
         "roofline": {
             "bound": "hbm",
