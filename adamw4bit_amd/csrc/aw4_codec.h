@@ -193,11 +193,14 @@ __device__ __forceinline__ UsrBlock update_sr_tables(const MomentTables& L, int 
         const float gap = L.sqrt_gap[i];
         certain = certain & (!(pe.b > pe.a) | (c * gap > 0x1p-20f * e_hi));  // over the real intervals
         // E(a) = 0 (a = 0 with eps = 0): f(a) is infinite and P = 0, so g = +inf decides upper
-        // (a draw of exactly 0 gives NaN and takes usr_exact)
+        // (a draw of exactly 0 gives Q = NaN, which counts as sure and decides upper too)
         const float g = e_lo > 0.0f ? gap * 0x1p-24f * rcp_faithful(e_lo) : __builtin_inff();
         upd[i] = UpdEntry{L.sqrt_level[pe.lohi >> 8], g};
     }
-    if (j == 0) upd[0] = UpdEntry{0.0f, 0.0f};
+    // Entry 0: no level below x (x = 0 for dyn4), where the code does not depend on the draw:
+    // Q = NaN marks the value sure in every block, certain or not (an all-zero block's scale is
+    // the 1e-12 floor, which no band covers).
+    if (j == 0) upd[0] = UpdEntry{__builtin_nanf(""), 0.0f};
     // every interval of the block certain (its 8 lanes, 16 entries)
     uint32_t all = certain ? 1u : 0u;
     all = min(all, dpp_u32<kQuadXor1>(all));
@@ -255,7 +258,7 @@ __device__ __forceinline__ void usr_quick(const UpdEntry& ue, const UsrBlock& ub
     const float ex = __builtin_fmaf(ub.c, w, eps);
     const float q = __builtin_fmaf(-U, ue.g * ex, ue.sqrt_hi - w);
     lower = q > 0.0f;
-    sure = __builtin_fabsf(q) > ub.band;
+    sure = !(__builtin_fabsf(q) <= ub.band);  // NaN: sure (entry 0, or a zero draw with g = +inf)
 }
 
 // NaN-propagating max(acc, |v|): v_maximum3_f32 with |.| operands.

@@ -85,11 +85,15 @@ __device__ __forceinline__ float rcp_faithful(float t) {
     return __builtin_fmaf(e0, y0, y0);
 }
 
-// bf16 round-to-nearest-even (c10::BFloat16), NaN kept quiet.
-__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
-    const uint32_t u = f2u(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+// bf16 round-to-nearest-even (c10::BFloat16), NaN kept quiet, by v_cvt_pk_bf16_f32: on MI355X it
+// gives the bits of the integer rule (u + 0x7fff + ((u >> 16) & 1)) >> 16, and (u >> 16) | 0x40 for
+// a NaN, for every one of the 2^32 fp32 inputs, subnormals included.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+// two values, packed (low half: a)
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
 }
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return u2f(h << 16); }
 // IEEE binary16, round-to-nearest-even (v_cvt_f16_f32), subnormals kept.

@@ -84,7 +84,11 @@ __device__ __forceinline__ void store_f32(uint64_t base, int64_t e, bool vec, co
         for (int t = 0; t < 4; ++t) h[t] = D == D_BF16 ? f32_to_bf16(v[t]) : f32_to_f16(v[t]);
         const gptr<uint16_t> p = gaddr<uint16_t>(base) + e;
         if (vec) {
-            __builtin_nontemporal_store(u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)}, (gptr<u32x2>)p);
+            if constexpr (D == D_BF16)
+                __builtin_nontemporal_store(u32x2{f32x2_to_bf16x2(v[0], v[1]), f32x2_to_bf16x2(v[2], v[3])},
+                                            (gptr<u32x2>)p);
+            else
+                __builtin_nontemporal_store(u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)}, (gptr<u32x2>)p);
         } else {
 #pragma unroll
             for (int t = 0; t < 4; ++t) p[t] = (uint16_t)h[t];

@@ -123,6 +123,9 @@ def cpu_leg(seconds_target: float) -> dict:
 
     from oracle import reference_step as ref
 
+    if os.environ.get("OMP_NUM_THREADS"):
+        # ATen sizes its pool from MKL's thread count when MKL is present, which can differ
+        torch.set_num_threads(int(os.environ["OMP_NUM_THREADS"]))
     out = {"threads": torch.get_num_threads(), "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
            "ms_per_step": {}, "steps": {}}
     gen = torch.Generator().manual_seed(0)
@@ -154,7 +157,7 @@ def cpu_baseline(seconds_target: float = 20.0):
     for threads in (None, 2):
         env = dict(os.environ)
         if threads is not None:
-            env["OMP_NUM_THREADS"] = str(threads)
+            env["OMP_NUM_THREADS"] = env["MKL_NUM_THREADS"] = str(threads)
         env["CUDA_VISIBLE_DEVICES"] = ""
         env["HIP_VISIBLE_DEVICES"] = ""
         proc = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-leg",

@@ -76,10 +76,11 @@ def quick(s, bias, eps, a_idx, b_idx, x, U, cb, rng, band_scale=1.0):
     ex = fma32(c, w, eps)
     qv = fma32(-U, (g * ex).astype(F32), (sq[b_idx] - w).astype(F32))
     band = (F32(2.0 ** -19 * band_scale) * fma32(eps, c_rcp, np.full(n, 2, F32))).astype(F32)
+    # a NaN Q counts as sure: a zero draw where g = +inf (E(a) = 0), whose P is 0
     # the block's intervals are all certain when c * gap > 2^-20 * E(b) for each; here the
     # value's own interval stands in (a block where any is uncertain decides exactly anyway)
     certain = (c * gap).astype(F32) > (F32(2.0 ** -20) * e_hi).astype(F32)
-    return qv > 0, np.abs(qv) > band, certain
+    return qv > 0, ~(np.abs(qv) <= band), certain
 
 
 def sample(rng, n, codebook):
