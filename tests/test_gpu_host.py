@@ -389,6 +389,52 @@ def test_unseeded_draws_follow_torch_generator(monkeypatch):
 
 
 # ---------------------------------------------------------------------------
+# torch.amp.GradScaler drives the optimizer unchanged
+# ---------------------------------------------------------------------------
+
+def test_grad_scaler_unscales_and_skips_steps():
+    """A trainer with loss scaling: ``scaler.unscale_(opt)`` divides the gradients in place and
+    records non-finite values, the fused clip reads the unscaled gradients, and
+    ``scaler.step(opt)`` skips the step of an overflowed iteration.  States and parameters equal
+    a twin optimizer stepped on the unscaled gradients of the iterations that were not skipped
+    (scaling by a power of two is exact)."""
+    log("GradScaler + fused clip")
+    gen = torch.Generator().manual_seed(41)
+    shapes = [(128, 256), (512,)]
+    init = [torch.randn(s, generator=gen) * 0.02 for s in shapes]
+    pa = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
+    pb = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
+    oa = aw.ZIPSRAdamW4Bit(pa, optimized=True, quant_rng_seed=2, **ARGS)
+    ob = aw.ZIPSRAdamW4Bit(pb, optimized=True, quant_rng_seed=2, **ARGS)
+    scaler = torch.amp.GradScaler("cuda", init_scale=2.0 ** 12, growth_interval=1000)
+    for k in range(4):
+        gs = grads_like(shapes, gen)
+        scaler.scale(torch.ones((), device=H.DEVICE))  # the loss a trainer would scale
+        scale = scaler.get_scale()
+        for a, g in zip(pa, gs):
+            a.grad = g * scale
+        if k == 2:  # an overflowed iteration
+            pa[0].grad.view(-1)[7] = float("inf")
+        scaler.unscale_(oa)
+        oa.clip_grad_norm_(1.0)
+        scaler.step(oa)
+        scaler.update()
+        if k == 2:
+            assert scaler.get_scale() == scale / 2  # the step was skipped
+            assert all(oa.state[a]["step"] == 2 for a in pa)
+            oa.zero_grad()  # drops the clip whose step was skipped
+            continue
+        for b, g in zip(pb, gs):
+            b.grad = g.clone()
+        ob.clip_grad_norm_(1.0)
+        ob.step()
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(pa, pb)):
+            same_state(oa, a, ob, b, (k, i))
+    assert all(oa.state[a]["step"] == 3 for a in pa)
+
+
+# ---------------------------------------------------------------------------
 # torch.compile: the launch is the custom operator
 # ---------------------------------------------------------------------------
 
