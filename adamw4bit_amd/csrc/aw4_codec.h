@@ -497,20 +497,61 @@ __device__ __forceinline__ double la_prob_lo(const aw4_moment& M, float z, float
 }
 
 // Float64 uniforms of this lane's 4 values of quarter q (see draws_quarter): the
-// generator's 24-bit fields times 2^-24, or a caller's doubles (AW4_MOMENT_EXT_DRAWS).
+// generator's 24-bit fields times 2^-24 (U: the fields themselves), or a caller's doubles
+// (AW4_MOMENT_EXT_DRAWS; U unused).
 __device__ __forceinline__ void la_draws_quarter(const aw4_moment& M, int64_t blk0, int grp, int j, int q, bool active,
-                                                 uint32_t (&rw)[12], double (&u)[4]) {
+                                                 uint32_t (&rw)[12], double (&u)[4], float (&U)[4]) {
     if (M.flags & AW4_MOMENT_EXT_DRAWS) {
         const gptr<const double> d = gaddr<const double>(M.draws) + (blk0 + grp) * kBlock + 32 * q + 4 * j;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) u[t] = active ? d[t] : 0.0;
+        for (int t = 0; t < 4; ++t) {
+            u[t] = active ? d[t] : 0.0;
+            U[t] = 0.0f;
+        }
     } else {
         if (q < 3) philox_lane_call(M.rng_seed, (M.rng_offset >> 7) + (uint64_t)(blk0 + grp), j, q, &rw[4 * q]);
-        float f[4];
-        lane_fields4(&rw[3 * q], f);
+        lane_fields4(&rw[3 * q], U);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) u[t] = (double)f[t] * 0x1p-24;
+        for (int t = 0; t < 4; ++t) u[t] = (double)U[t] * 0x1p-24;
     }
+}
+
+// Quick lookahead decision in fp32.  With r = sqrt(n), E = r / sqrt(bias) + eps, the rule's
+// P = (p(z) - p(q_hi)) / (p(q_lo) - p(q_hi)) is exactly
+//   (q_hi - z) (r_hi + r_lo) E_lo / ((q_hi - q_lo) (r_hi + r_z) E_z),
+// a quotient of positive factors without cancellation, which fp32 evaluates within about
+// 2^-18.5 of P.  The reference's float64 P itself is off by a few 2^-53 M, where
+// M = max(p_lo, 1) / (p_lo - p_hi) = (r_hi + r_lo) E_hi max(E_lo, 1) / (beta2 (q_hi - q_lo) / sqrt(bias)).
+// The decision u < P is sure outside the band 2^-16 max(P, 1) + 2^-46 M; values inside it, or
+// with M >= 2^36 (near the reference's switch to its value-linear form at 1e12), or with
+// n_lo below 2^-100 (where fp32 loses the small terms, and where p_lo = +inf makes the
+// reference's flat test true) take la_prob_lo.  rb = 1 / sqrt(bias) within 3 ulps; fresh within
+// 3 ulps of the reference's float64 term.
+struct LaQuick {
+    float beta2, rb, eps;
+};
+__device__ __forceinline__ void la_quick(const LaQuick& k, float z, float a, float b, float s, float fresh, float U,
+                                         bool& lower, bool& sure) {
+    const float q_lo = s * a, q_hi = s * b;
+    const float n_lo = __builtin_fmaf(k.beta2, q_lo, fresh);
+    const float n_hi = __builtin_fmaf(k.beta2, q_hi, fresh);
+    const float n_z = __builtin_fmaf(k.beta2, z, fresh);
+    const float r_lo = sqrt_faithful(n_lo), r_hi = sqrt_faithful(n_hi), r_z = sqrt_faithful(n_z);
+    const float e_lo = __builtin_fmaf(r_lo, k.rb, k.eps);
+    const float e_hi = __builtin_fmaf(r_hi, k.rb, k.eps);
+    const float e_z = __builtin_fmaf(r_z, k.rb, k.eps);
+    const float d_hi = __builtin_fmaf(s, b, -z);
+    const float w = s * (b - a);
+    const float s_lo = r_hi + r_lo;
+    const float num = (d_hi * s_lo) * e_lo;
+    const float den = (w * (r_hi + r_z)) * e_z;
+    const float p = num * rcp_faithful(den);
+    const float m = (s_lo * e_hi) * __builtin_fmaxf(e_lo, 1.0f) * rcp_faithful((k.beta2 * w) * k.rb);
+    const float band = __builtin_fmaf(0x1p-16f, __builtin_fmaxf(p, 1.0f), 0x1p-46f * m);
+    const float u = U * 0x1p-24f;
+    lower = u < p;
+    // comparisons with NaN are false: a NaN P or M is never sure
+    sure = (__builtin_fabsf(u - p) > band) & (m < 0x1p36f) & (n_lo >= 0x1p-100f);
 }
 
 // Lookahead update-SR of this lane's 16 values z of block blk0 + grp (clamped at 0 first).
@@ -533,13 +574,22 @@ __device__ __forceinline__ BlockScales encode_block_la(const aw4_moment& M, cons
     const bool wave_fast = __builtin_amdgcn_ballot_w64(!(s < 0x1p125f)) == 0;
     const float y = div_cr(1.0f, s);
     const bool proxy = (M.flags & AW4_MOMENT_FRESH_PROXY) != 0;
+    // the quick form needs the generator's 24-bit draws and finite, normal block scales
+    const bool quick = wave_fast & ((M.flags & AW4_MOMENT_EXT_DRAWS) == 0);
+    const LaQuick lq{(float)M.la_beta2, rcp_faithful(sqrt_faithful((float)M.la_bias)), (float)M.la_eps};
+    const float wf = (float)M.la_fresh_weight;
     uint32_t rw[12];
     wave_lds_sync();  // the stage's previous contents have been read
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         double u[4];
-        la_draws_quarter(M, blk0, grp, j, q, active, rw, u);
+        float U[4];
+        la_draws_quarter(M, blk0, grp, j, q, active, rw, u, U);
         uint32_t code[4];
+        int idx[4];
+        float a[4], b[4];
+        bool lower[4];
+        uint64_t unsure = quick ? 0 : ~0ull;  // lanes (bits) with a value the quick form leaves open
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const int i = 4 * q + t;
@@ -547,14 +597,33 @@ __device__ __forceinline__ BlockScales encode_block_la(const aw4_moment& M, cons
             const float x = clamp01_nan(xq);
             const LutEntry le = L.lut[lut_bucket_unsigned(x)];
             const bool up = x >= le.thr;
-            const int idx = (int)le.base + (up ? 1 : 0);
-            const float b = up ? le.lv_hi : le.lv_lo;   // cb[min(idx, 15)]
-            const float a = L.cb[idx > 0 ? idx - 1 : 0];
-            const double fresh = proxy ? (double)clamp_min_nan(w2f * z_in[i], 0.0f)
-                                       : M.la_fresh_weight * ((double)g[i] * (double)g[i]);
-            const bool lower = u[t] < la_prob_lo(M, z[i], a, b, s, fresh);
-            code[t] = (uint32_t)min(max(idx - (lower ? 1 : 0), 0), 15);
-            if (sampled) sampled[i] = s * (lower ? a : b);
+            idx[t] = (int)le.base + (up ? 1 : 0);
+            b[t] = up ? le.lv_hi : le.lv_lo;   // cb[min(idx, 15)]
+            a[t] = L.cb[idx[t] > 0 ? idx[t] - 1 : 0];
+            if (quick) {
+                const float fresh = proxy ? clamp_min_nan(w2f * z_in[i], 0.0f) : (wf * g[i]) * g[i];
+                bool sure;
+                la_quick(lq, z[i], a[t], b[t], s, fresh, U[t], lower[t], sure);
+                // idx == 0 (z = 0): a degenerate interval, P = 1, and lo == hi
+                unsure |= __builtin_amdgcn_ballot_w64(!(sure | (idx[t] == 0)));
+            }
+        }
+        // A quarter with any open value is decided again by the reference's float64 rule, every
+        // value of it (where the quick form was sure the two agree).  The branch is uniform.
+        if (unsure != 0) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int i = 4 * q + t;
+                const double fresh = proxy ? (double)clamp_min_nan(w2f * z_in[i], 0.0f)
+                                           : M.la_fresh_weight * ((double)g[i] * (double)g[i]);
+                lower[t] = u[t] < la_prob_lo(M, z[i], a[t], b[t], s, fresh);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int i = 4 * q + t;
+            code[t] = (uint32_t)min(max(idx[t] - (lower[t] ? 1 : 0), 0), 15);
+            if (sampled) sampled[i] = s * (lower[t] ? a[t] : b[t]);
         }
         if (store) sc.stage[8 * q + j] = (uint16_t)(code[0] | (code[1] << 4) | (code[2] << 8) | (code[3] << 12));
     }
