@@ -28,6 +28,7 @@ on a HIP device; there is no CPU implementation.
 
 from __future__ import annotations
 
+import bisect
 import functools
 import math
 import operator
@@ -122,6 +123,42 @@ def _byte_range(t: torch.Tensor) -> Tuple[str, int, int]:
 
 def _overlaps(a, b) -> bool:
     return a[0] == b[0] and a[1] < b[2] and b[1] < a[2]
+
+
+class _RangeSet:
+    """Byte ranges a launch writes in place, for the overlap test of ``_overlaps`` against all of
+    them in O(log n): per device, the union of the non-empty ranges as sorted disjoint intervals
+    (empty ranges, which overlap only what strictly contains their address, kept aside)."""
+
+    __slots__ = ("_starts", "_ends", "_points")
+
+    def __init__(self):
+        self._starts: Dict[str, List[int]] = {}
+        self._ends: Dict[str, List[int]] = {}
+        self._points: List[Tuple[str, int, int]] = []
+
+    def overlaps(self, r) -> bool:
+        key, a, b = r
+        ends = self._ends.get(key)
+        if ends:
+            i = bisect.bisect_right(ends, a)  # the first interval ending after a
+            if i < len(ends) and self._starts[key][i] < b:
+                return True
+        return any(_overlaps(r, q) for q in self._points)
+
+    def add(self, r) -> None:
+        key, a, b = r
+        if b <= a:
+            self._points.append(r)
+            return
+        starts = self._starts.setdefault(key, [])
+        ends = self._ends.setdefault(key, [])
+        i = bisect.bisect_left(ends, a)     # the first interval ending at or after a
+        j = bisect.bisect_right(starts, b)  # the first interval starting after b
+        if i < j:
+            a, b = min(a, starts[i]), max(b, ends[j - 1])
+        starts[i:j] = [a]
+        ends[i:j] = [b]
 
 
 class _StepConstants:
@@ -826,17 +863,20 @@ class QuantizedAdamW(Optimizer):
             if _overlaps(occupied[0], _byte_range(grad)):
                 grad = grad.clone()
             occupied.append(_byte_range(grad))
-            occupied.extend(batch.occupied)
+
+            def taken(r) -> bool:
+                return batch.occupied.overlaps(r) or any(_overlaps(r, q) for q in occupied)
+
             for key in ("m1", "m2", "m1_code", "m2_code", PENDING_KEY):
                 value = state.get(key)
                 if isinstance(value, torch.Tensor):
-                    if any(_overlaps(_byte_range(value), r) for r in occupied):
+                    if taken(_byte_range(value)):
                         state[key] = value = value.clone()
                     occupied.append(_byte_range(value))
             for key in ("m1_quant_state", "m2_quant_state"):
                 meta = state.get(key)
                 if isinstance(meta, QuantState) and isinstance(meta.absmax, torch.Tensor):
-                    if any(_overlaps(_byte_range(meta.absmax), r) for r in occupied):
+                    if taken(_byte_range(meta.absmax)):
                         meta.absmax = meta.absmax.clone()
                     occupied.append(_byte_range(meta.absmax))
         if not grad.is_contiguous():
@@ -894,8 +934,8 @@ class QuantizedAdamW(Optimizer):
                            c_.step_coef, c_.bc2_sqrt, c_.bc2_sqrt_rcp, c_.eps, m1, m2))
         batch.refs.append(refs)
         pre = state.get("m2_read_preconditioner")
-        batch.occupied.extend(_byte_range(t) for t in [target] + _moment_tensors(state)
-                              + ([pre] if isinstance(pre, torch.Tensor) else []))
+        for t in [target] + _moment_tensors(state) + ([pre] if isinstance(pre, torch.Tensor) else []):
+            batch.occupied.add(_byte_range(t))
 
     def _init_moment(self, p, state, moment, scheme, size, eden, chunk) -> None:
         """Zero state (``_moment_buffer.py:89-126`` / ``adamw.py:524-545``)."""
@@ -1027,7 +1067,7 @@ class _DeviceBatch:
     __slots__ = ("rows", "refs", "params", "written", "read", "copy_back", "occupied")
 
     def __init__(self):
-        self.occupied: list = []  # byte ranges the rows so far write in place
+        self.occupied = _RangeSet()  # byte ranges the rows so far write in place
         self.rows: List[Tuple] = []
         self.refs: List[Dict[int, Tuple[str, int]]] = []  # per row: column -> (list, index)
         self.params: List[torch.Tensor] = []   # updated in place
@@ -1081,8 +1121,8 @@ class _StepUndo:
 class _LaunchPlan:
     """Launch tables of the last full step, reused by the next steps while only per-step values
     change: gradient addresses, step counts, the fp32 step constants (one per group and step,
-    computed by the same code as the full path), random-stream positions and the update-SR
-    storage bias.  Any structural change -- other parameters with gradients, a parameter whose
+    computed by the same code as the full path), random-stream keys and positions, the update-SR
+    storage bias and the lookahead constants.  Any structural change -- other parameters with gradients, a parameter whose
     storage, dtype, size or layout changed (``p.data = ...``, ``module.to(dtype)``), new state
     objects, other schemes or chunking in a group, an m1 retarget, a checkpoint load, a draw
     provider, a gradient that is not contiguous or overlaps its parameter or state -- sends the
@@ -1110,8 +1150,8 @@ class _LaunchPlan:
 
     @classmethod
     def build(cls, opt: "QuantizedAdamW", batches: List[_DeviceBatch], checked: List[_Checked]):
-        if opt._draw_provider is not None or any(c.schemes[1] in LOOKAHEAD_SCHEMES or c.staged for c in checked):
-            return None  # lookahead rows carry per-step constants the plan does not refresh
+        if opt._draw_provider is not None or any(c.staged for c in checked):
+            return None  # caller draws and staged copies are per step
         plan = cls()
         meta = {id(c.param): c.schemes for c in checked}
         group_of = {}
@@ -1177,9 +1217,13 @@ class _LaunchPlan:
             pvec = np.array([p.data_ptr() % (4 * p.element_size()) == 0 for p in params], dtype=bool)
             gvec = np.array([4 * p.element_size() for p in params], dtype=np.int64)
             qrows = np.flatnonzero(table["m2"]["rounding"] != _lib.ROUND_FP32)
+            # lookahead m2 rows: their float64 beta2, 1 - beta2, bias correction and eps are per
+            # step too (the pending form's bias is bias_c2 of the step, the proxies' that of the next)
+            la_rows = np.flatnonzero(table["m2"]["rounding"] == _lib.ROUND_LOOKAHEAD_SR)
+            la_next = (table["m2"]["flags"][la_rows] & _lib.MOMENT_PENDING) == 0
             plan.devices.append((table, list(params), list(batch.written), entries, lo, hi, gbytes, pptr, pvec, gvec,
                                  table.view(_STEP_FIELDS), qrows, refs, torch.from_numpy(table.view(np.uint8)),
-                                 torch.from_numpy(refs)))
+                                 torch.from_numpy(refs), la_rows, la_next))
             plan.params.extend(params)
             plan.pdtypes.extend(p.dtype for p in params)
             plan.pnumel.extend(p.numel() for p in params)
@@ -1253,7 +1297,7 @@ class _LaunchPlan:
         consts: List[_StepConstants] = []
         launches = []
         for (table, params, written, entries, lo, hi, gbytes, pptr, pvec, gvec, fields, qrows, refs, table_t,
-             refs_t), g0 in zip(self.devices, grads):
+             refs_t, la_rows, la_next), g0 in zip(self.devices, grads):
             index = np.empty(len(entries), dtype=np.intp)
             offsets = {"m1": fields["m1_rng_offset"].copy(), "m2": fields["m2_rng_offset"].copy()}
             seeds = {"m1": fields["m1_rng_seed"].copy(), "m2": fields["m2_rng_seed"].copy()}
@@ -1280,6 +1324,18 @@ class _LaunchPlan:
                 sr_bias = [_f32(max(float(c.storage_bias), 1e-12)) for c in consts]
                 fields["m2_sr"][qrows] = np.array([(b, _rcp32(b), c.eps) for b, c in zip(sr_bias, consts)],
                                                   dtype=np.float32)[index[qrows]].view(np.uint32)
+            if len(la_rows):
+                # the lookahead fields, by the full path's arithmetic (Python floats)
+                la = []
+                for i, nxt in zip(la_rows.tolist(), la_next.tolist()):
+                    state, gi = entries[i][0], entries[i][1]
+                    group = self.groups[gi][0]
+                    beta2 = float(group["betas"][1])
+                    la.append((beta2, 1.0 - beta2, max(float(1 - beta2 ** (state["step"] + int(nxt))), 1e-12),
+                               float(group["eps"])))
+                m2 = table["m2"]
+                for k, name in enumerate(("la_beta2", "la_fresh_weight", "la_bias", "la_eps")):
+                    m2[name][la_rows] = [v[k] for v in la]
             fields["grad"] = g0
             fields["grad_scale"] = 0 if coef is None else coef.data_ptr()
             fields["m1_rng_seed"] = seeds["m1"]

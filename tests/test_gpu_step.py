@@ -623,14 +623,16 @@ def test_mixed_recipes_split_launches(dtype):
     compare_pair(*out, f"mixed recipes {dtype}", steps=4)
 
 
-@pytest.mark.parametrize("m2_scheme", [None, "dyn4_upd_sr_fp32read_nextbc"])
+@pytest.mark.parametrize("m2_scheme", [None, "dyn4_upd_sr_fp32read_nextbc", "dyn4_la_upd_sr", "dyn4_proxy_la_upd_sr",
+                                       "dyn4_vproxy_la_upd_sr"])
 def test_launch_plan_reuse_matches_full_path(m2_scheme):
     """Steps reusing the previous step's launch tables are bit-identical to steps that rebuild
     them, through a learning-rate change, a parameter without gradient, an m1 retarget, and
-    state tensors replaced by equal copies (a code tensor, a QuantState's absmax), which the
-    plan must not keep writing through its old addresses.  With the next-step storage bias
-    the group's first tensor is an fp32-state one, whose m2 scheme (fp32) has the other bias:
-    the step constants must not be shared across the two."""
+    state tensors replaced by equal copies (a code or pending-state tensor, a QuantState's
+    absmax), which the plan must not keep writing through its old addresses.  With the
+    next-step storage bias the group's first tensor is an fp32-state one, whose m2 scheme (fp32)
+    has the other bias: the step constants must not be shared across the two.  The lookahead
+    schemes' rows carry a bias correction of the step (or the next) that the plan rewrites."""
     log(f"launch plan reuse vs full path ({m2_scheme or 'ZIP-SR'})")
     shapes = [(256, 512), (768,), (64, 1024), (1000,), (128, 384)]
     q0 = 0
@@ -662,7 +664,8 @@ def test_launch_plan_reuse_matches_full_path(m2_scheme):
             ob.set_m1_quant_scheme_for_parameters([pb[q0]], "nf4_sr")
         if k == 6:
             for o, ps in ((oa, pa), (ob, pb)):
-                o.state[ps[q0]]["m2_code"] = o.state[ps[q0]]["m2_code"].clone()
+                key = "m2_code" if "m2_code" in o.state[ps[q0]] else "lookahead_pending_exp_avg_sq"
+                o.state[ps[q0]][key] = o.state[ps[q0]][key].clone()
                 q = o.state[ps[4]]["m1_quant_state"]
                 q.absmax = q.absmax.clone()
         before = oa._launch_plan

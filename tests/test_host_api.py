@@ -236,3 +236,24 @@ def test_aliased_state_load_marks_both_parameters_and_persists():
                                if isinstance(v, dict) else v) for k, v in sd2["state"][i].items()}
     o2.load_state_dict(sd2)
     assert [o2.state[p].get("_optimized_full_fallback", False) for p in ps] == [True, True, False]
+
+
+def test_range_set_answers_as_the_pairwise_overlap_test():
+    """The launch's record of written byte ranges (an interval union per device) answers every
+    query as testing ``_overlaps`` against each recorded range would, empty ranges included."""
+    import random
+
+    from adamw4bit_amd.adamw import _overlaps, _RangeSet
+
+    rng = random.Random(5)
+    for trial in range(200):
+        rs, kept = _RangeSet(), []
+        for _ in range(rng.randint(1, 40)):
+            key = rng.choice(["cuda:0", "cuda:1"])
+            a = rng.randint(0, 200)
+            r = (key, a, a + rng.choice([0, 1, 2, 5, 17, 40]))
+            expect = any(_overlaps(r, q) for q in kept)
+            assert rs.overlaps(r) == expect, (trial, r, kept)
+            if rng.random() < 0.7:
+                rs.add(r)
+                kept.append(r)
