@@ -216,8 +216,10 @@ def test_golden_trajectory(name):
 # ---------------------------------------------------------------------------
 
 def run_pair(make_opt, shapes, dtype, steps, *, seed=0, grad_seed=1, m1_override=None, oracle_kwargs=None,
-             zero_block_frac=0.0):
-    """Step the drop-in optimizer on the GPU and the oracle on the CPU with identical inputs/draws."""
+             zero_block_frac=0.0, grad_fn=None):
+    """Step the drop-in optimizer on the GPU and the oracle on the CPU with identical inputs/draws
+    (gradients: ``grad_fn(shape, generator)``, heavy-tailed by default)."""
+    grad_fn = grad_fn or H.heavy_tailed
     gen = torch.Generator().manual_seed(grad_seed)
     init = [(torch.randn(s, generator=gen) * 0.02).to(dtype) for s in shapes]
     params = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
@@ -242,7 +244,7 @@ def run_pair(make_opt, shapes, dtype, steps, *, seed=0, grad_seed=1, m1_override
     for _ in range(steps):
         grads = []
         for s in shapes:
-            g = H.heavy_tailed(s, gen)
+            g = grad_fn(s, gen)
             if zero_block_frac and g.numel() % 128 == 0:
                 nb = g.numel() // 128
                 g.view(nb, 128)[torch.rand(nb, generator=gen) < zero_block_frac] = 0.0
@@ -292,10 +294,15 @@ def compare_pair(opt, params, oracle, cpu_params, parted, what, steps=1):
     return total_parted
 
 
-def test_zeeden_1024x1024_matches_oracle():
-    log("zeeden 1024x1024 x 12 steps")
+@pytest.mark.parametrize("grads", ["normal", "heavy"])
+def test_zeeden_1024x1024_matches_oracle(grads):
+    """One fp32 1024x1024 parameter under ZE-EDEN for 12 steps: the benchmark's small case with
+    its seeded N(0, 1e-3) gradients (10 warmup steps and more), and with heavy-tailed ones."""
+    log(f"zeeden 1024x1024 x 12 steps, {grads} gradients")
     args = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True)
-    out = run_pair(lambda ps: aw.ZEEDENAdamW4Bit(ps, **args), [(1024, 1024)], torch.float32, 12, seed=None)
+    normal = lambda shape, gen: torch.randn(shape, generator=gen) * 1e-3  # noqa: E731
+    out = run_pair(lambda ps: aw.ZEEDENAdamW4Bit(ps, **args), [(1024, 1024)], torch.float32, 12, seed=None,
+                   grad_fn=normal if grads == "normal" else None)
     compare_pair(*out, "zeeden 1024^2")
 
 
@@ -556,10 +563,12 @@ def test_tensor_beyond_2_31_values():
 
 
 def test_zipsr_4096x4096_matches_oracle():
-    log("zipsr 4096x4096 x 2 steps (full size)")
+    """The benchmark's single-tensor ZIP-SR case at full size: one fp32 4096x4096 parameter,
+    heavy-tailed gradients, quant_rng_seed=0, past its 10 warmup steps."""
+    log("zipsr 4096x4096 x 11 steps (full size)")
     args = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True, quant_rng_seed=0)
-    out = run_pair(lambda ps: aw.ZIPSRAdamW4Bit(ps, **args), [(4096, 4096)], torch.float32, 2, seed=0)
-    compare_pair(*out, "zipsr 4096^2")
+    out = run_pair(lambda ps: aw.ZIPSRAdamW4Bit(ps, **args), [(4096, 4096)], torch.float32, 11, seed=0)
+    compare_pair(*out, "zipsr 4096^2", steps=11)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
