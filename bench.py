@@ -111,6 +111,7 @@ def make_grads(shapes, device, seed):
 
 
 CPU_SHAPE = (4096, 4096)
+SMALL_SHAPE, SMALL_WARMUP, SMALL_STEPS = (1024, 1024), 10, 100
 CPU_RECIPES = {"ZE-EDEN": ("nf4", "dyn4_nz", True), "ZIP-SR": ("nf4", "dyn4_upd_sr_fp32read", False)}
 
 
@@ -142,6 +143,18 @@ def cpu_leg(seconds_target: float) -> dict:
             times.append(time.perf_counter() - t0)
         out["ms_per_step"][name] = statistics.median(times) * 1e3
         out["steps"][name] = len(times)
+    # the single small tensor: ZE-EDEN on one fp32 1024x1024 parameter with fresh seeded
+    # N(0, 1e-3) gradients each step, 10 untimed steps, then the median of 100
+    p = torch.randn(SMALL_SHAPE, generator=gen) * 0.02
+    oracle = ref.Oracle([p], ref.Hyper(), ["nf4"], ["dyn4_nz"], [True])
+    grads = [torch.randn(SMALL_SHAPE, generator=gen) * 1e-3 for _ in range(SMALL_WARMUP + SMALL_STEPS)]
+    times = []
+    for k, g in enumerate(grads):
+        t0 = time.perf_counter()
+        oracle.step([g])
+        if k >= SMALL_WARMUP:
+            times.append(time.perf_counter() - t0)
+    out["small_ms_per_step"] = statistics.median(times) * 1e3
     return out
 
 
@@ -189,6 +202,7 @@ def cpu_baseline(seconds_target: float = 20.0):
                       f"os.cpu_count {os.cpu_count()}",
             "legs": [{"threads": leg["threads"], "omp_num_threads": leg["omp_num_threads"],
                       "ms_per_step": {k: round(v, 2) for k, v in leg["ms_per_step"].items()},
+                      "zeeden_1024x1024_ms_per_step": round(leg["small_ms_per_step"], 3),
                       "gelem_s": round(rate(leg), 5)} for leg in legs],
             "ci_threads_value": rate(ci_leg)}
 
@@ -304,6 +318,55 @@ def time_launches(recipes, steps: int, warmup: int, clip, stream):
     return {name: [a.elapsed_time(b) for a, b in ev] for name, ev in events.items()}, wall, norm_events
 
 
+def time_single_tensors(device, stream) -> dict:
+    """The two single-tensor workloads, each timed through ``step()`` after 10 untimed steps:
+    ZE-EDEN on one fp32 1024x1024 parameter with fresh seeded N(0, 1e-3) gradients each step
+    (100 timed steps), and ZIP-SR (quant_rng_seed=0) on one fp32 4096x4096 parameter with the
+    heavy-tailed gradients (20 timed steps).  Per step: HIP events around ``step()`` on the launch
+    stream (host time shows where it exceeds the kernel's) and the wall time."""
+    import torch
+
+    import adamw4bit_amd as aw
+
+    hyper = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True)
+    out = {}
+    gen = torch.Generator(device=device).manual_seed(7)
+    for name, shape, make, steps, fresh in (
+            ("zeeden_1024x1024", SMALL_SHAPE, lambda ps: aw.ZEEDENAdamW4Bit(ps, **hyper), SMALL_STEPS, True),
+            ("zipsr_4096x4096", (4096, 4096), lambda ps: aw.ZIPSRAdamW4Bit(ps, quant_rng_seed=0, **hyper), 20,
+             False)):
+        p = torch.nn.Parameter(torch.randn(shape, generator=gen, device=device) * 0.02)
+        opt = make([p])
+        if fresh:
+            grads = [torch.randn(shape, generator=gen, device=device) * 1e-3 for _ in range(SMALL_WARMUP + steps)]
+        else:
+            grads = make_grads([shape], device, seed=11) * (SMALL_WARMUP + steps)
+        events = []
+        torch.cuda.synchronize()
+        for k, g in enumerate(grads):
+            if k == SMALL_WARMUP:
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+            p.grad = g
+            if k >= SMALL_WARMUP:
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record(stream)
+                opt.step()
+                b.record(stream)
+                events.append((a, b))
+            else:
+                opt.step()
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) / steps
+        ms = [a.elapsed_time(b) for a, b in events]
+        algo = math.prod(shape) * bytes_per_value(math.prod(shape))
+        out[name] = {"steps": steps, "warmup": SMALL_WARMUP, "event_ms_per_step": round(statistics.mean(ms), 4),
+                     "wall_ms_per_step": round(wall * 1e3, 4),
+                     "hbm_frac": round(algo / (statistics.mean(ms) * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del opt, p, grads
+    return out
+
+
 def time_unfused(recipes, params, steps: int, warmup: int, clip, stream):
     """The unfused path a trainer runs: torch's clip (norm pass + in-place multiply), then the
     step; mean ms per recipe."""
@@ -338,7 +401,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-bf16-mixed", action="store_true",
-                    help="with the default fp32 set, skip the bf16 mixed-scheme set measured after it")
+                    help="with the default fp32 set, skip the bf16 mixed-scheme set and the single-tensor "
+                         "cases measured after it")
     ap.add_argument("--cpu-leg", action="store_true", help=argparse.SUPPRESS)  # child process of the CPU baseline
     ap.add_argument("--clip-grad-norm", type=float, default=None, metavar="MAX_NORM",
                     help="clip the gradients to this global 2-norm before every step, fused into the step "
@@ -431,6 +495,12 @@ def main():
         print(f"[bench] bf16 mixed set: {bf16_mixed}", file=sys.stderr, flush=True)
         mrecipes = mparams = None
 
+    single = None
+    if args.config == "llama3-8b" and clip is None and not args.no_bf16_mixed:
+        torch.cuda.empty_cache()
+        single = time_single_tensors(device, stream)
+        print(f"[bench] single tensors: {single}", file=sys.stderr, flush=True)
+
     baseline = None
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
@@ -465,6 +535,7 @@ def main():
             "algorithmic_gb_per_launch": {k: round(v / 1e9, 4) for k, v in algo_bytes.items()},
             **({"prologue": prologue} if prologue else {}),
             **({"bf16_mixed": bf16_mixed} if bf16_mixed else {}),
+            **({"single_tensors": single} if single else {}),
         },
         "roofline": {
             "bound": "hbm",
