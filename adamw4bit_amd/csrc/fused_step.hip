@@ -168,6 +168,16 @@ step_kernel_4w(const StepHeader* __restrict__ hdr, const Tables* __restrict__ ta
     step_body<M1K, M2K, D>(hdr, tables);
 }
 
+// The same kernel held to 256 VGPRs, two waves per SIMD: the generic research instance (every
+// m2 kind, read back or lookahead, with run-time dtypes) needs 270 otherwise, one wave per SIMD;
+// the few registers it spills cost less than the second wave gains (pending lookahead 108 ->
+// 66 ms on the Llama-3-8B set).
+template <int M1K, int M2K, int D>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+step_kernel_2w(const StepHeader* __restrict__ hdr, const Tables* __restrict__ tables) {
+    step_body<M1K, M2K, D>(hdr, tables);
+}
+
 // The instantiated kernels; the host groups a step's tensors by the variant whose moment
 // specs and dtype they match (optimized-path flags).  ZE-EDEN: NF4 round-to-nearest m1,
 // Dyn4 round-to-nearest m2 with EDEN.  ZIP-SR: NF4 round-to-nearest m1, Dyn4 update-SR m2
@@ -191,6 +201,7 @@ struct KernelVariant {
 };
 #define AW4_VARIANT(M1, M2, D) {M1, M2, D, (const void*)&step_kernel<M1, M2, D>}
 #define AW4_VARIANT_4W(M1, M2, D) {M1, M2, D, (const void*)&step_kernel_4w<M1, M2, D>}
+#define AW4_VARIANT_2W(M1, M2, D) {M1, M2, D, (const void*)&step_kernel_2w<M1, M2, D>}
 const KernelVariant kVariants[] = {
     AW4_VARIANT_4W(kRtn, kRtnEden, D_F32),        AW4_VARIANT_4W(kRtn, kUsrGuarded, D_F32),
     AW4_VARIANT(kRtn, kRtnEden, D_BF16),          AW4_VARIANT(kRtn, kUsrGuarded, D_BF16),
@@ -199,11 +210,12 @@ const KernelVariant kVariants[] = {
     AW4_VARIANT(kRtn, kUsrGuardedEden, D_F32),    AW4_VARIANT(kRtn, kUsrGuardedEden, D_BF16),
     AW4_VARIANT(kRtn, kUsrRead, D_F32),           AW4_VARIANT(kRtn, kUsrReadEden, D_F32),
     AW4_VARIANT(kRtn, kLaStore, D_F32),
-    AW4_VARIANT(K_ANY, kAnyResearch, D_ANY),
+    AW4_VARIANT_2W(K_ANY, kAnyResearch, D_ANY),
     AW4_VARIANT(K_ANY, K_ANY, D_ANY),
 };
 #undef AW4_VARIANT
 #undef AW4_VARIANT_4W
+#undef AW4_VARIANT_2W
 constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 constexpr int kGenericVariant = kNumVariants - 1;
 constexpr int kResearchVariant = kNumVariants - 2;  // generic, for read-back and lookahead m2

@@ -25,8 +25,11 @@ from adamw4bit_amd import build
 MIN_WAVES = {
     (1, 33, 0): 4, (1, 67, 0): 4, (1, 33, 1): 4, (1, 67, 1): 4, (66, 67, 0): 3, (66, 67, 1): 4,
     (1, 0, 0): 4, (1, 0, 1): 4, (1, 99, 0): 3, (1, 99, 1): 3, (1, 259, 0): 3, (1, 803, 0): 2,
-    (1, 4, 0): 2,
+    (1, 4, 0): 3,
 }
+# The generic research instance (any m1, any read-back or lookahead m2, run-time dtypes) is held to
+# two waves per SIMD and may spill a few registers for it.
+RESEARCH_GENERIC, RESEARCH_SPILL_LIMIT = (7, 263, 7), 16
 
 
 def waves_per_simd(vgprs: int) -> int:
@@ -51,7 +54,7 @@ def kernel_vgprs():
         name = re.search(r"\.name:\s+(\S+)", block)
         if not name or "step_kernel" not in name.group(1):
             continue
-        args = re.search(r"step_kernel(?:_4w)?ILi(\d+)ELi(\d+)ELi(\d+)E", name.group(1))
+        args = re.search(r"step_kernel(?:_[24]w)?ILi(\d+)ELi(\d+)ELi(\d+)E", name.group(1))
         vgpr = re.search(r"\.vgpr_count:\s+(\d+)", block)
         spill = re.search(r"\.vgpr_spill_count:\s+(\d+)", block)
         found[tuple(int(x) for x in args.groups())] = (int(vgpr.group(1)), int(spill.group(1)))
@@ -68,6 +71,10 @@ def test_specialised_kernels_keep_their_occupancy(kernel_vgprs):
 
 def test_generic_kernels_do_not_spill(kernel_vgprs):
     generic = [k for k in kernel_vgprs if k not in MIN_WAVES]
-    assert generic, "generic kernels not found"
+    assert generic and RESEARCH_GENERIC in generic, "generic kernels not found"
     for key in generic:
-        assert kernel_vgprs[key][1] == 0, f"kernel {key} spills"
+        vgprs, spills = kernel_vgprs[key]
+        if key == RESEARCH_GENERIC:
+            assert waves_per_simd(vgprs) >= 2 and spills <= RESEARCH_SPILL_LIMIT, (key, vgprs, spills)
+        else:
+            assert spills == 0, f"kernel {key} spills"
