@@ -48,6 +48,9 @@ constexpr int spec_flags_mask(int kind) {
                          : (AW4_MOMENT_EDEN | AW4_MOMENT_GUARDS | AW4_MOMENT_ZERO_FLOOR);
 }
 
+// A lookahead m2 spec marked pending: fp32 values, sampled before the update, no codes.
+constexpr bool pending_spec(int spec) { return kind_of(spec) == K_LA && (flags_of(spec) & AW4_MOMENT_PENDING) != 0; }
+
 // Lookup-table ids (aw4_encode_tables): round-to-nearest tables, then level-count tables.
 constexpr int kLutRtn[AW4_NUM_CODEBOOKS] = {0, 1, 2, 3, 4};
 constexpr int kLutRtnDyn4Floor = 5;

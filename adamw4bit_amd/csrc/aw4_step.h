@@ -173,8 +173,9 @@ template <int M1K, int M2K, int D>
 struct TileInputs {
     static constexpr int kW = (D == D_F32 || D == D_ANY) ? 4 : 2;  // words per 4 values
     static constexpr int K1 = kind_of(M1K), K2 = kind_of(M2K);
+    // a pending lookahead m2 (AW4_MOMENT_PENDING in its spec) keeps fp32 values, no codes
     static constexpr bool kQ1 = K1 != K_FP32, kV1 = K1 == K_FP32 || K1 == K_ANY;
-    static constexpr bool kQ2 = K2 != K_FP32, kV2 = K2 == K_FP32 || K2 == K_ANY;
+    static constexpr bool kQ2 = K2 != K_FP32 && !pending_spec(M2K), kV2 = K2 == K_FP32 || K2 == K_ANY || pending_spec(M2K);
     uint32_t g[4 * kW];
     uint32_t p[4 * kW];
     uint32_t c1[kQ1 ? 2 : 1], c2[kQ2 ? 2 : 1];  // code words of quarters 2h (low half) and 2h + 1 (high half)
@@ -189,7 +190,7 @@ __device__ __forceinline__ bool is_quantized(const aw4_moment& m) { return has_c
 template <int MK>
 __device__ __forceinline__ bool moment_quantized(const aw4_moment& m) {
     if constexpr (kind_of(MK) == K_ANY) return is_quantized(m);
-    else return kind_of(MK) != K_FP32;
+    else return kind_of(MK) != K_FP32 && !pending_spec(MK);
 }
 
 // Addressing of one lane within a wave tile: the tile's base pointers are wave-uniform
@@ -648,14 +649,16 @@ __device__ __forceinline__ void run_tiles(const StepHeader* hdr, const LdsT& lds
                 if constexpr (kind_of(M2K) == K_ANY || kind_of(M2K) == K_LA) {
                   if (!sampled) {
                     // lookahead update-SR: sample the pending state before the update (the
-                    // generic instance; the K_LA instance takes the code-storing proxies only),
-                    // or encode the new m2 after it
+                    // generic instance, or the K_LA instance specialised on AW4_MOMENT_PENDING),
+                    // or encode the new m2 after it (the code-storing proxies)
+                    constexpr bool kMaybePending = kind_of(M2K) == K_ANY || pending_spec(M2K);
                     float g[16];
                     tile_grads(T, in, g);
-                    const bool pending = kind_of(M2K) == K_ANY && (T.m2.flags & AW4_MOMENT_PENDING) != 0;
+                    const bool pending = pending_spec(M2K) ||
+                                         (kind_of(M2K) == K_ANY && (T.m2.flags & AW4_MOMENT_PENDING) != 0);
                     const float w2f = (float)T.m2.la_fresh_weight;
                     float prior[16];
-                    if constexpr (kind_of(M2K) == K_ANY) {
+                    if constexpr (kMaybePending) {
                         if (pending) {
                             float z[16];
 #pragma unroll
@@ -668,15 +671,17 @@ __device__ __forceinline__ void run_tiles(const StepHeader* hdr, const LdsT& lds
                     finish_moment<M1K, false>(T.m1, L1, tl, RegValues{m1}, ws);
                     prefetch();
                     bool stored = false;
-                    if constexpr (kind_of(M2K) == K_ANY) {
+                    if constexpr (kMaybePending) {
                         if (pending) {
                             finish_moment<M2K, true>(T.m2, L2, tl, m2.values(), ws);
                             stored = true;
                         }
                     }
-                    if (!stored)
-                        encode_block_la(T.m2, L2, tl.blk0, tl.grp, tl.j, tl.active, m2v, g, w2f, true, nullptr,
-                                        ws.block(tl.grp));
+                    if constexpr (!pending_spec(M2K)) {
+                        if (!stored)
+                            encode_block_la(T.m2, L2, tl.blk0, tl.grp, tl.j, tl.active, m2v, g, w2f, true, nullptr,
+                                            ws.block(tl.grp));
+                    }
                   }
                 }
             } else if constexpr (stage_m2(M1K, M2K, D)) {

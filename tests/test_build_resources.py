@@ -20,13 +20,15 @@ from adamw4bit_amd import build
 # m1: 1 = NF4 round-to-nearest, 66 = value-space SR with guards;
 # m2: 33 = round-to-nearest + EDEN, 67 = update-SR with guards, 99 = update-SR + EDEN, 0 = fp32,
 # 259 = update-SR read back after its encode, 803 = the same with the store-EDEN flags,
-# 4 = lookahead update-SR stored as codes;
+# 4 = lookahead update-SR stored as codes, 2052 = the pending lookahead form (fp32 state);
 # dtype: 0 = fp32, 1 = bf16.
 MIN_WAVES = {
     (1, 33, 0): 4, (1, 67, 0): 4, (1, 33, 1): 4, (1, 67, 1): 4, (66, 67, 0): 3, (66, 67, 1): 4,
     (1, 0, 0): 4, (1, 0, 1): 4, (1, 99, 0): 3, (1, 99, 1): 3, (1, 259, 0): 3, (1, 803, 0): 2,
-    (1, 4, 0): 3,
+    (1, 4, 0): 3, (1, 2052, 0): 3,
 }
+# Kernels held to an occupancy with a few spilled registers (the occupancy pays for them).
+SPILL_LIMIT = {(1, 2052, 0): 8}
 # The generic research instance (any m1, any read-back or lookahead m2, run-time dtypes) is held to
 # two waves per SIMD and may spill a few registers for it.
 RESEARCH_GENERIC, RESEARCH_SPILL_LIMIT = (7, 263, 7), 16
@@ -54,7 +56,7 @@ def kernel_vgprs():
         name = re.search(r"\.name:\s+(\S+)", block)
         if not name or "step_kernel" not in name.group(1):
             continue
-        args = re.search(r"step_kernel(?:_[24]w)?ILi(\d+)ELi(\d+)ELi(\d+)E", name.group(1))
+        args = re.search(r"step_kernel(?:_[234]w)?ILi(\d+)ELi(\d+)ELi(\d+)E", name.group(1))
         vgpr = re.search(r"\.vgpr_count:\s+(\d+)", block)
         spill = re.search(r"\.vgpr_spill_count:\s+(\d+)", block)
         found[tuple(int(x) for x in args.groups())] = (int(vgpr.group(1)), int(spill.group(1)))
@@ -65,7 +67,7 @@ def test_specialised_kernels_keep_their_occupancy(kernel_vgprs):
     for key, waves in MIN_WAVES.items():
         assert key in kernel_vgprs, f"kernel {key} not instantiated"
         vgprs, spills = kernel_vgprs[key]
-        assert spills == 0, f"kernel {key} spills {spills} VGPRs"
+        assert spills <= SPILL_LIMIT.get(key, 0), f"kernel {key} spills {spills} VGPRs"
         assert waves_per_simd(vgprs) >= waves, f"kernel {key}: {vgprs} VGPRs -> {waves_per_simd(vgprs)} waves < {waves}"
 
 
