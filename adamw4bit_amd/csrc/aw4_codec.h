@@ -253,15 +253,15 @@ __device__ __forceinline__ void usr_exact(const aw4_moment& M, float s, float x,
     lower = U * 0x1p-24f < (fx - fb) / clamp_min_nan(den, 1e-30f);
 }
 
-// The quick decision (see update_sr_tables): Q > 0 means lower; `sure` is false inside the band.
-// U = u * 2^24.
-__device__ __forceinline__ void usr_quick(const UpdEntry& ue, const UsrBlock& ub, float eps, float x, float U,
-                                          bool& lower, bool& sure) {
+// The quick decision (see update_sr_tables): returns Q, where Q > 0 means lower; `sure` is false
+// inside the band.  U = u * 2^24.
+__device__ __forceinline__ float usr_quick(const UpdEntry& ue, const UsrBlock& ub, float eps, float x, float U,
+                                           bool& sure) {
     const float w = sqrt_faithful(x);
     const float ex = __builtin_fmaf(ub.c, w, eps);
     const float q = __builtin_fmaf(-U, ue.g * ex, ue.sqrt_hi - w);
-    lower = q > 0.0f;
     sure = !(__builtin_fabsf(q) <= ub.band);  // NaN: sure (entry 0, or a zero draw with g = +inf)
+    return q;
 }
 
 // NaN-propagating max(acc, |v|): v_maximum3_f32 with |.| operands.
@@ -365,15 +365,11 @@ __device__ __forceinline__ BlockScales encode_block(const aw4_moment& M, const M
             // below x.  Since u is in [0, 1), u < clamp(P, 0, 1) == u < P for every P (NaN included),
             // so the clamps of the reference never change a code and the guards become masks.
             int idx[4];
-            float b[4];  // upper neighbour cb[min(idx, 15)]
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const LutEntry le = L.lut[kNonNeg ? lut_bucket_unsigned(x[t]) : lut_bucket_signed(x[t])];
-                const bool up = x[t] >= le.thr;
-                idx[t] = (int)le.base + (up ? 1 : 0);
-                b[t] = up ? le.lv_hi : le.lv_lo;
+                idx[t] = (int)le.base + (x[t] >= le.thr ? 1 : 0);
             }
-            bool lower[4];
             if constexpr (KIND == K_SSR) {
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
@@ -384,7 +380,7 @@ __device__ __forceinline__ BlockScales encode_block(const aw4_moment& M, const M
                     const float p = div_by_rcp(x[t] - pe.a, width < 1e-12f ? 1e-12f : width, pe.width_rcp);
                     bool upper = u[t] < p * 0x1p24f;
                     if (guards) upper = (upper | (x[t] >= pe.b)) & !(x[t] <= pe.a);
-                    lower[t] = !upper;
+                    code[t] = (uint32_t)min(max(idx[t] - (upper ? 0 : 1), 0), 15);
                 }
             } else {
                 // P(lo) = (f(x) - f(b)) / max(f(a) - f(b), 1e-30), 1 on invalid intervals
@@ -393,7 +389,9 @@ __device__ __forceinline__ BlockScales encode_block(const aw4_moment& M, const M
                 // invalid interval, and add x <= a -> lo, which holds exactly when no level is
                 // below x (idx == 0), where lo and hi are both code 0: that guard changes no code
                 // (nor the level EDEN reads) and is not evaluated.
-                bool dl[4], valid[4];
+                // the decision as a float whose sign is the outcome (> 0: lower), so that the two
+                // paths below meet in plain registers
+                float dq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
                 uint64_t unsure = 1;  // lanes (bits) with a value the quick test leaves open
                 if (__builtin_expect(wave_fast, 1)) {
                     unsure = 0;
@@ -401,33 +399,41 @@ __device__ __forceinline__ BlockScales encode_block(const aw4_moment& M, const M
                     for (int t = 0; t < 4; ++t) {
                         const UpdEntry ue = sc.upd[idx[t]];
                         bool sure;
-                        usr_quick(ue, ub, M.sr_eps, x[t], u[t], dl[t], sure);
-                        valid[t] = true;  // (idx > 0 below: levels increase, so x > cb[0] has an interval)
+                        dq[t] = usr_quick(ue, ub, M.sr_eps, x[t], u[t], sure);
                         unsure |= __builtin_amdgcn_ballot_w64(!sure);
                     }
                 }
                 // A quarter with any open value (a few in a hundred) is decided again by the
                 // reference's operations, every value of it: where the quick test was sure the two
-                // agree, so nothing needs to be selected.  The branch is uniform.
+                // agree, so nothing needs to be selected.  The branch is uniform.  It leaves
+                // code = idx - lower with idx in [0, 15], the clamps folded into lower and idx.
                 if (unsure != 0) {
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
                         const PairEntry pe = L.pairs[idx[t]];
-                        usr_exact(M, s, x[t], pe.a, pe.b, u[t], valid[t], dl[t]);
+                        bool valid, dl;
+                        usr_exact(M, s, x[t], pe.a, pe.b, u[t], valid, dl);
+                        // bitwise operators: the operands are all computed, and short-circuit
+                        // forms become per-value branches
+                        const bool at_b = x[t] >= pe.b;
+                        const bool ok = valid & (idx[t] > 0);
+                        const bool lower = guards ? ((!ok) | dl) & !at_b : (!ok) | (dl & !at_b);
+                        // idx 0: code 0; idx 16: code 15
+                        dq[t] = (lower & ((uint32_t)(idx[t] - 1) < 15u)) ? 1.0f : -1.0f;
+                        idx[t] = min(idx[t], 15);
                     }
                 }
-                // Bitwise operators: the operands are all computed, and short-circuit forms
-                // become per-value branches.
+                // Where the quick test decided every value of the quarter: code = idx - lower,
+                // without guards or clamps.  The block is certain, so every interval is valid.  No
+                // level below x (idx = 0): Q is NaN and lower false, code 0.  x at its upper level
+                // b (where both forms of the rule pick hi): Q = (sqrt(b) - w) - u * g * E(b) with w
+                // within an ulp of sqrt(b), so a sure Q is negative and lower false.  idx <= 15,
+                // as x <= 1, the top level of the update-SR codebooks, on the quick path.
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const bool at_b = x[t] >= b[t];
-                    const bool ok = valid[t] & (idx[t] > 0);
-                    lower[t] = guards ? ((!ok) | dl[t]) & !at_b : (!ok) | (dl[t] & !at_b);
-                }
+                for (int t = 0; t < 4; ++t) code[t] = (uint32_t)(idx[t] - (dq[t] > 0.0f ? 1 : 0));
             }
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                code[t] = (uint32_t)min(max(idx[t] - (lower[t] ? 1 : 0), 0), 15);
                 if (floor0) code[t] = max(code[t], 1u);
                 lv[t] = eden ? L.cb[code[t]] : 0.0f;
             }

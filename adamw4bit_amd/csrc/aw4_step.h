@@ -154,14 +154,34 @@ __device__ __forceinline__ void moments_update(const aw4_tensor& T, float g, flo
 // p = p * (1 - lr*wd) [rounded to storage]; p = p + (-lr/bc1 * m1) / (sqrt(m2) / sqrt(bc2) + eps).
 // The denominator and the quotient are faithful: hardware square root and reciprocal
 // (<= 1 ulp each), so the update term is within 3 ulps of ATen's, whose square root is
-// itself only faithful.  The decayed parameter is exact; the update term is usually
-// far below its ulp.  Zero, infinite and NaN denominators give ATen's results
-// (x * rcp(0) = x / 0, x * rcp(inf) = 0 for finite x).
+// itself only faithful; the sum is one fused operation.  The decayed parameter is exact; the
+// update term is usually far below its ulp.  Zero, infinite and NaN denominators give ATen's
+// results (x * rcp(0) = x / 0, x * rcp(inf) = 0 for finite x).
+__device__ __forceinline__ float param_apply(const aw4_tensor& T, float p1, float m1, float m2) {
+    const float d = __builtin_fmaf(sqrt_faithful(m2), T.bc2_sqrt_rcp, T.eps);
+    return __builtin_fmaf(T.step_coef * m1, __builtin_amdgcn_rcpf(d), p1);
+}
+
 template <int D>
 __device__ __forceinline__ float param_update(const aw4_tensor& T, float p, float m1, float m2) {
-    const float d = __builtin_fmaf(sqrt_faithful(m2), T.bc2_sqrt_rcp, T.eps);
-    const float p1 = round_to_storage<D>(p * T.decay);
-    return p1 + (T.step_coef * m1) * __builtin_amdgcn_rcpf(d);
+    return param_apply(T, round_to_storage<D>(p * T.decay), m1, m2);
+}
+
+// The decayed parameters p * (1 - lr*wd) of 4 values, rounded to storage (bf16: one conversion
+// for two values).
+template <int D>
+__device__ __forceinline__ void decay4(const aw4_tensor& T, const float (&p)[4], float (&p1)[4]) {
+    if constexpr (D == D_BF16) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t w = f32x2_to_bf16x2(p[2 * h] * T.decay, p[2 * h + 1] * T.decay);
+            p1[2 * h] = u2f(w << 16);
+            p1[2 * h + 1] = u2f(w & 0xffff0000u);
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) p1[t] = round_to_storage<D>(p[t] * T.decay);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -336,6 +356,8 @@ __device__ __forceinline__ void update_quarter(const aw4_tensor& T, int q, const
         }
     }
     const bool large1 = (T.flags & AW4_TENSOR_LERP1_LARGE) != 0, large2 = (T.flags & AW4_TENSOR_LERP2_LARGE) != 0;
+    float pd[4];
+    decay4<DP>(T, p, pd);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
         if constexpr (kGenericLerp) {
@@ -347,8 +369,8 @@ __device__ __forceinline__ void update_quarter(const aw4_tensor& T, int q, const
         }
         if (la_prior)
             b[t] = __builtin_fmaf((float)T.m2.la_fresh_weight * g[t], g[t], la_prior[4 * q + t] * (float)T.m2.la_beta2);
-        if constexpr (kDefer) p1[4 * q + t] = round_to_storage<DP>(p[t] * T.decay);
-        else p[t] = param_update<DP>(T, p[t], a[t], b[t]);
+        if constexpr (kDefer) p1[4 * q + t] = pd[t];
+        else p[t] = param_apply(T, pd[t], a[t], b[t]);
         m1[4 * q + t] = a[t];
     }
     m2.put(q, b);

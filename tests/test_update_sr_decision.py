@@ -145,3 +145,18 @@ def test_a_narrower_band_would_be_wrong():
             valid, ref_lower = reference_lower(s, bias, eps, a, b, x, u, True)
         bad_total += int((sure & certain & valid & (lower != ref_lower)).sum())
     assert bad_total > 0
+
+
+@pytest.mark.parametrize("codebook", ["dyn4", "lin4"])
+def test_a_value_at_its_upper_level_is_never_decided_lower(codebook):
+    """Where every value of a quarter is sure, the kernel forms code = idx - lower without the
+    guards: x at its upper level b must then come out upper (the guard x >= b, and P = 0 there),
+    whatever the draw and the one-ulp errors of the faithful operations."""
+    rng = np.random.default_rng(14 if codebook == "dyn4" else 15)
+    cb_values = q.CODEBOOK_VALUES[q.CB_DYN4 if codebook == "dyn4" else q.CB_LIN4]
+    for _ in range(4):
+        with np.errstate(all="ignore"):
+            cb, a_idx, b_idx, a, b, x, s, bias, eps, U, uniform = sample(rng, 400_000, cb_values)
+            U = np.where(rng.random(len(x)) < 0.1, F32(0), U).astype(F32)  # zero draws too
+            lower, sure, certain = quick(s, bias, eps, a_idx, b_idx, b.copy(), U, cb, rng)
+        assert not (sure & certain & lower).any(), codebook
