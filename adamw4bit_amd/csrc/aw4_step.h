@@ -171,6 +171,20 @@ __device__ __forceinline__ float param_update(const aw4_tensor& T, float p, floa
 // for two values).
 template <int D>
 __device__ __forceinline__ void decay4(const aw4_tensor& T, const float (&p)[4], float (&p1)[4]) {
+    if constexpr (D == D_BF16 || D == D_F16) {
+        // 1 - 2^-9 < decay <= 1 (bf16; 1 - 2^-12 for fp16): p * decay is within half a storage ulp of
+        // every 16-bit p (the spacing below a power of two, the closest case, is 2^-8 of it for
+        // bf16, 2^-11 for fp16; subnormals have a wider relative spacing), so it rounds back to p.
+        // The branch is uniform, and the test compares bit patterns (scalar integer compares:
+        // positive floats order as their bits, and a negative or NaN decay fails it).
+        constexpr uint32_t kIdentity = D == D_BF16 ? 0x3F7F8000u : 0x3F7FF000u;  // 1 - 2^-9, 1 - 2^-12
+        const uint32_t db = f2u(T.decay);
+        if (db > kIdentity && db <= 0x3F800000u) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) p1[t] = p[t];
+            return;
+        }
+    }
     if constexpr (D == D_BF16) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
