@@ -28,10 +28,12 @@ on a HIP device; there is no CPU implementation.
 
 from __future__ import annotations
 
+import array
 import bisect
 import functools
 import math
 import operator
+import struct
 from collections.abc import Mapping
 from typing import Any, Dict, Iterable, Iterator, List, Optional, Tuple
 
@@ -80,8 +82,12 @@ def _f32(x: float) -> float:
 
 
 def _rcp32(x: float) -> float:
-    """Correctly rounded fp32 reciprocal of the fp32 value ``x``."""
-    return float(np.float32(1.0) / np.float32(x))
+    """Correctly rounded fp32 reciprocal of the fp32 value ``x``: the float64 quotient rounded to
+    fp32 (a double rounding that cannot differ from one rounding, 53 >= 2 * 24 + 2 bits); 1/0 is
+    inf with the sign of the zero."""
+    if x == 0.0:
+        return math.copysign(math.inf, x)
+    return array.array("f", (1.0 / x,)).tolist()[0]
 
 
 def _step_fields() -> np.dtype:
@@ -161,32 +167,51 @@ class _RangeSet:
         ends[i:j] = [b]
 
 
+def _f32s(*values: float) -> list:
+    """Each value rounded to fp32 (to nearest, as numpy's float32 conversion; out of range: inf)."""
+    return array.array("f", values).tolist()
+
+
 class _StepConstants:
     """The fp32 step constants of one (group, step), computed in float64 and rounded once to
-    fp32 as the reference does (``_optimized.py:168-173``)."""
+    fp32 as the reference does (``_optimized.py:168-173``).  ``words`` and ``m2_sr`` are their
+    bit patterns as the launch table holds them (the flags word and the seven fp32 constants;
+    the m2 update-SR bias, its reciprocal and eps)."""
 
-    __slots__ = ("lerp_flags", "w1", "w2", "decay", "step_coef", "bc2_sqrt", "bc2_sqrt_rcp", "eps", "storage_bias")
+    __slots__ = ("lerp_flags", "w1", "w2", "decay", "step_coef", "bc2_sqrt", "bc2_sqrt_rcp", "eps", "storage_bias",
+                 "_words", "_m2_sr")
 
     def __init__(self, group, step: int, m2_scheme: str):
         beta1, beta2 = group["betas"]
         lr, wd, eps = group["lr"], group["weight_decay"], group["eps"]
         bias1, bias2 = 1 - beta1 ** step, 1 - beta2 ** step
         self.storage_bias = 1 - beta2 ** (step + 1) if m2_scheme in NEXT_BIAS_SCHEMES else bias2
+        w1, w2, self.decay, self.step_coef, self.bc2_sqrt, self.eps = _f32s(
+            1 - beta1, 1 - beta2, 1 - lr * wd, -lr / bias1, math.sqrt(bias2), eps)
         flags = 0
-        w1, w2 = np.float32(1 - beta1), np.float32(1 - beta2)
         if not abs(w1) < 0.5:  # ATen lerp switches formulas at |weight| >= 0.5
             flags |= _lib.TENSOR_LERP1_LARGE
-            w1 = w1 - np.float32(1.0)
+            w1 = w1 - 1.0  # exact for w1 in [0.5, 1] (and NaN stays NaN), as in fp32
         if not abs(w2) < 0.5:
             flags |= _lib.TENSOR_LERP2_LARGE
-            w2 = w2 - np.float32(1.0)
+            w2 = w2 - 1.0
         self.lerp_flags = flags
-        self.w1, self.w2 = float(w1), float(w2)
-        self.decay = _f32(1 - lr * wd)
-        self.step_coef = _f32(-lr / bias1)
-        self.bc2_sqrt = _f32(math.sqrt(bias2))
+        self.w1, self.w2 = w1, w2
         self.bc2_sqrt_rcp = _rcp32(self.bc2_sqrt)
-        self.eps = _f32(eps)
+        self._words = self._m2_sr = None
+
+    def words(self) -> np.ndarray:
+        if self._words is None:
+            self._words = np.frombuffer(struct.pack("<i7f", self.lerp_flags, self.w1, self.w2, self.decay,
+                                                    self.step_coef, self.bc2_sqrt, self.bc2_sqrt_rcp, self.eps),
+                                        dtype=np.uint32)
+        return self._words
+
+    def m2_sr(self) -> np.ndarray:
+        if self._m2_sr is None:
+            bias = _f32(max(float(self.storage_bias), 1e-12))
+            self._m2_sr = np.frombuffer(struct.pack("<3f", bias, _rcp32(bias), self.eps), dtype=np.uint32)
+        return self._m2_sr
 
 
 def _step_constants(group, step: int, m2_scheme: str) -> _StepConstants:
@@ -198,6 +223,21 @@ def _vec_aligned(p: torch.Tensor, grad: torch.Tensor) -> bool:
     psize = 4 * p.element_size()
     gsize = 4 * grad.element_size()
     return p.data_ptr() % psize == 0 and grad.data_ptr() % gsize == 0
+
+
+def _table_tensor(table: np.ndarray) -> torch.Tensor:
+    """The rows of a launch table as the CPU uint8 tensor a launch record carries; the tensor also
+    keeps the rows for the eager launch (``_aw4_rows``)."""
+    t = torch.from_numpy(table.view(np.uint8))
+    t._aw4_rows = table
+    return t
+
+
+try:
+    from torch._C import _cuda_getCurrentRawStream as _raw_stream  # torch's own (inductor's get_raw_stream)
+except ImportError:  # pragma: no cover - other torch builds
+    def _raw_stream(index: int) -> int:
+        return torch.cuda.current_stream(index).cuda_stream
 
 
 def _launch(params: List[torch.Tensor], written: List[torch.Tensor], read: List[torch.Tensor],
@@ -218,12 +258,14 @@ def _launch(params: List[torch.Tensor], written: List[torch.Tensor], read: List[
         device = params[0].device
         if device.type != "cuda":
             raise ValueError("the fused 4-bit step runs on HIP devices only")
-        rows = table.numpy().view(_lib.TENSOR)
+        rows = getattr(table, "_aw4_rows", None)
+        if rows is None:
+            rows = table.numpy().view(_lib.TENSOR)
         if torch.cuda.current_device() != device.index:
             with torch.cuda.device(device):
-                _lib.fused_step(rows, torch.cuda.current_stream(device).cuda_stream)
+                _lib.fused_step(rows, _raw_stream(device.index))
         else:
-            _lib.fused_step(rows, torch.cuda.current_stream(device).cuda_stream)
+            _lib.fused_step(rows, _raw_stream(device.index))
         torch.autograd.graph.increment_version(params + written)
     for p, staged in copy_back:
         p.copy_(staged)
@@ -1095,8 +1137,7 @@ class _DeviceBatch:
             for col, (kind, index) in row.items():
                 refs[i, col] = base[kind] + index
         _ops.resolve_addresses(table, refs, self.params + self.written + self.read)
-        return (self.params, self.written, self.read, torch.from_numpy(table.view(np.uint8)),
-                torch.from_numpy(refs), self.copy_back)
+        return (self.params, self.written, self.read, _table_tensor(table), torch.from_numpy(refs), self.copy_back)
 
 
 class _StepUndo:
@@ -1118,6 +1159,58 @@ class _StepUndo:
             s.offset = offset
 
 
+# Plans of at most this many rows per device check and refresh their rows in Python loops,
+# larger ones with numpy (whose fixed cost per operation is about a microsecond).
+_SMALL_PLAN = 16
+
+
+class _PlanDevice:
+    """One device's part of a launch plan: its table (rows with every address filled in) and
+    the views and per-row facts its per-step refresh needs."""
+
+    __slots__ = ("table", "params", "written", "entries", "states", "device", "small", "lo", "hi", "ranges",
+                 "pptr", "gbytes", "gbytes_list", "pvec", "pvec_list", "gvec", "gvec_list", "fields", "words",
+                 "m2_sr", "seed_cols", "offset_cols", "grad_col", "qrows", "qsel", "qrows_any", "la_rows", "la_next",
+                 "refs", "table_t", "refs_t", "scale_ptr", "scale_ref")
+
+    def __init__(self, table: np.ndarray, params, written, entries, lo, hi, ranges, refs: np.ndarray):
+        n = len(params)
+        self.table = table
+        self.params = list(params)
+        self.written = list(written)
+        self.entries = entries
+        self.states = [e[0] for e in entries]
+        self.device = params[0].device
+        self.small = n <= _SMALL_PLAN
+        self.lo, self.hi = lo, hi
+        self.ranges = ranges  # per row: the (start, end) byte ranges a gradient may not overlap
+        self.pptr = [p.data_ptr() for p in params]
+        self.gbytes_list = [p.numel() * p.element_size() for p in params]
+        self.gbytes = np.array(self.gbytes_list, dtype=np.int64)
+        self.pvec_list = [p.data_ptr() % (4 * p.element_size()) == 0 for p in params]
+        self.pvec = np.array(self.pvec_list, dtype=bool)
+        self.gvec_list = [4 * p.element_size() for p in params]
+        self.gvec = np.array(self.gvec_list, dtype=np.int64)
+        # views into the table
+        self.fields = table.view(_STEP_FIELDS)
+        self.words = self.fields["words"]
+        self.m2_sr = self.fields["m2_sr"]
+        self.seed_cols = {"m1": self.fields["m1_rng_seed"], "m2": self.fields["m2_rng_seed"]}
+        self.offset_cols = {"m1": self.fields["m1_rng_offset"], "m2": self.fields["m2_rng_offset"]}
+        self.grad_col = self.fields["grad"]
+        self.qrows = np.flatnonzero(table["m2"]["rounding"] != _lib.ROUND_FP32)
+        self.qrows_any = len(self.qrows) > 0
+        self.qsel = slice(None) if len(self.qrows) == n else self.qrows
+        # lookahead m2 rows: their float64 beta2, 1 - beta2, bias correction and eps are per
+        # step too (the pending form's bias is bias_c2 of the step, the proxies' that of the next)
+        self.la_rows = np.flatnonzero(table["m2"]["rounding"] == _lib.ROUND_LOOKAHEAD_SR)
+        self.la_next = (table["m2"]["flags"][self.la_rows] & _lib.MOMENT_PENDING) == 0
+        self.refs = refs
+        self.table_t = _table_tensor(table)
+        self.refs_t = torch.from_numpy(refs)
+        self.scale_ptr = self.scale_ref = None  # what the grad_scale fields hold (unknown: rewrite)
+
+
 class _LaunchPlan:
     """Launch tables of the last full step, reused by the next steps while only per-step values
     change: gradient addresses, step counts, the fp32 step constants (one per group and step,
@@ -1137,6 +1230,7 @@ class _LaunchPlan:
 
     def __init__(self):
         self.groups: list = []     # (group, structure, parameter count)
+        self.streams: list = []    # the random streams the planned rows draw from
         self.params: List[torch.Tensor] = []
         self.pdtypes: list = []    # each parameter's dtype, numel at build time
         self.pnumel: list = []
@@ -1164,6 +1258,7 @@ class _LaunchPlan:
             n = len(params)
             lo = np.zeros((n, cls._MAX_RANGES), dtype=np.int64)
             hi = np.zeros((n, cls._MAX_RANGES), dtype=np.int64)
+            row_ranges = []
             entries = []
             for i, p in enumerate(params):
                 state = opt.state[p]
@@ -1182,6 +1277,7 @@ class _LaunchPlan:
                     return None
                 for k, (a, b) in enumerate(ranges):
                     lo[i, k], hi[i, k] = a, b
+                row_ranges.append(ranges)
                 sr = tuple((moment, opt._stream(moment, p.device))
                            for moment, scheme in (("m1", schemes[0]), ("m2", schemes[1]))
                            if scheme != "fp32" and SCHEMES[scheme][1] in _SR_ROUNDINGS)
@@ -1212,18 +1308,11 @@ class _LaunchPlan:
                     else:
                         refs[i, col] = base[kind] + index
             _ops.resolve_addresses(table, refs, list(params) + list(batch.written) + [p.grad for p in params])
-            gbytes = np.array([p.numel() * p.element_size() for p in params], dtype=np.int64)
-            pptr = np.array([p.data_ptr() for p in params], dtype=np.int64)
-            pvec = np.array([p.data_ptr() % (4 * p.element_size()) == 0 for p in params], dtype=bool)
-            gvec = np.array([4 * p.element_size() for p in params], dtype=np.int64)
-            qrows = np.flatnonzero(table["m2"]["rounding"] != _lib.ROUND_FP32)
-            # lookahead m2 rows: their float64 beta2, 1 - beta2, bias correction and eps are per
-            # step too (the pending form's bias is bias_c2 of the step, the proxies' that of the next)
-            la_rows = np.flatnonzero(table["m2"]["rounding"] == _lib.ROUND_LOOKAHEAD_SR)
-            la_next = (table["m2"]["flags"][la_rows] & _lib.MOMENT_PENDING) == 0
-            plan.devices.append((table, list(params), list(batch.written), entries, lo, hi, gbytes, pptr, pvec, gvec,
-                                 table.view(_STEP_FIELDS), qrows, refs, torch.from_numpy(table.view(np.uint8)),
-                                 torch.from_numpy(refs), la_rows, la_next))
+            plan.devices.append(_PlanDevice(table, params, batch.written, entries, lo, hi, row_ranges, refs))
+            for _, _, _, sr, _ in entries:
+                for _, stream in sr:
+                    if not any(stream is s for s in plan.streams):
+                        plan.streams.append(stream)
             plan.params.extend(params)
             plan.pdtypes.extend(p.dtype for p in params)
             plan.pnumel.extend(p.numel() for p in params)
@@ -1270,16 +1359,23 @@ class _LaunchPlan:
             return None
         out = []
         for dev in self.devices:
-            dparams, lo, hi, gbytes, pptr = dev[1], dev[4], dev[5], dev[6], dev[7]
+            dparams = dev.params
             # the parameters' storage is still where the tables point (p.data can be swapped
             # without changing the Parameter object)
-            if not np.array_equal(np.fromiter(map(torch.Tensor.data_ptr, dparams), dtype=np.int64,
-                                              count=len(dparams)), pptr):
+            if list(map(torch.Tensor.data_ptr, dparams)) != dev.pptr:
                 return None
-            g0 = np.fromiter((p.grad.data_ptr() for p in dparams), dtype=np.int64, count=len(dparams))
-            g1 = g0 + gbytes
-            if bool(((lo < g1[:, None]) & (g0[:, None] < hi)).any()):
-                return None
+            g0 = [p.grad.data_ptr() for p in dparams]
+            if dev.small:
+                for g, nbytes, ranges in zip(g0, dev.gbytes_list, dev.ranges):
+                    g1 = g + nbytes
+                    for a, b in ranges:
+                        if a < g1 and g < b:
+                            return None
+            else:
+                g0 = np.array(g0, dtype=np.int64)
+                g1 = g0 + dev.gbytes
+                if bool(((dev.lo < g1[:, None]) & (g0[:, None] < dev.hi)).any()):
+                    return None
             out.append(g0)
         return out
 
@@ -1289,18 +1385,17 @@ class _LaunchPlan:
         grads = self._valid(opt)
         if grads is None:
             return None
-        saved_steps = [(state, state["step"]) for dev in self.devices for state, *_ in dev[3]]
-        saved_streams = [(s, s.offset) for s in opt._all_streams()]
+        saved_steps = [(state, state["step"]) for dev in self.devices for state in dev.states]
+        saved_streams = [(s, s.offset) for s in self.streams]
         # one _StepConstants per (group, step, m2 scheme): the update-SR storage bias depends on
         # the tensor's m2 scheme (an fp32-state tensor of a group has the fp32 scheme)
         constants: Dict[Tuple[int, int, str], int] = {}
         consts: List[_StepConstants] = []
         launches = []
-        for (table, params, written, entries, lo, hi, gbytes, pptr, pvec, gvec, fields, qrows, refs, table_t,
-             refs_t, la_rows, la_next), g0 in zip(self.devices, grads):
-            index = np.empty(len(entries), dtype=np.intp)
-            offsets = {"m1": fields["m1_rng_offset"].copy(), "m2": fields["m2_rng_offset"].copy()}
-            seeds = {"m1": fields["m1_rng_seed"].copy(), "m2": fields["m2_rng_seed"].copy()}
+        for dev, g0 in zip(self.devices, grads):
+            entries = dev.entries
+            ks = []  # constants index of each row
+            seeds, offsets = dev.seed_cols, dev.offset_cols
             for i, (state, gi, m2_scheme, sr, numel) in enumerate(entries):
                 step = state["step"] + 1
                 state["step"] = step
@@ -1308,45 +1403,61 @@ class _LaunchPlan:
                 if k is None:
                     k = constants[(gi, step, m2_scheme)] = len(consts)
                     consts.append(_StepConstants(self.groups[gi][0], step, m2_scheme))
-                index[i] = k
+                ks.append(k)
                 for moment, stream in sr:
                     seeds[moment][i] = stream.seed
                     offsets[moment][i] = stream.take(numel)
             # the flags word and the seven fp32 step constants (bit patterns), and the m2
             # update-SR constants of the rows whose m2 is quantized
-            words = np.array([(c.lerp_flags, c.w1, c.w2, c.decay, c.step_coef, c.bc2_sqrt, c.bc2_sqrt_rcp, c.eps)
-                              for c in consts], dtype=_STEP_WORDS)[index]
-            coef = opt._take_grad_clip(params[0].device)
-            words["flags"] |= np.where(pvec & (g0 % gvec == 0), _lib.TENSOR_VEC_ALIGNED, 0) | (
-                0 if coef is None else _lib.TENSOR_GRAD_SCALE)
-            fields["words"] = words.view(np.uint32).reshape(-1, 8)
-            if len(qrows):
-                sr_bias = [_f32(max(float(c.storage_bias), 1e-12)) for c in consts]
-                fields["m2_sr"][qrows] = np.array([(b, _rcp32(b), c.eps) for b, c in zip(sr_bias, consts)],
-                                                  dtype=np.float32)[index[qrows]].view(np.uint32)
-            if len(la_rows):
+            one = ks.count(ks[0]) == len(ks)
+            if one:
+                dev.words[:] = consts[ks[0]].words()
+            else:
+                index = np.array(ks, dtype=np.intp)
+                dev.words[:] = np.stack([c.words() for c in consts])[index]
+            coef = opt._take_grad_clip(dev.device)
+            extra = 0 if coef is None else _lib.TENSOR_GRAD_SCALE
+            if dev.small:
+                flags = dev.words[:, 0]
+                for i, (g, pvec, gvec) in enumerate(zip(g0, dev.pvec_list, dev.gvec_list)):
+                    f = extra | (_lib.TENSOR_VEC_ALIGNED if pvec and g % gvec == 0 else 0)
+                    if f:
+                        flags[i] |= f
+            else:
+                dev.words[:, 0] |= (np.where(dev.pvec & (g0 % dev.gvec == 0), _lib.TENSOR_VEC_ALIGNED, 0)
+                                    | extra).astype(np.uint32)
+            if dev.qrows_any:
+                if one:
+                    dev.m2_sr[dev.qsel] = consts[ks[0]].m2_sr()
+                else:
+                    dev.m2_sr[dev.qrows] = np.stack([c.m2_sr() for c in consts])[index[dev.qrows]]
+            if len(dev.la_rows):
                 # the lookahead fields, by the full path's arithmetic (Python floats)
                 la = []
-                for i, nxt in zip(la_rows.tolist(), la_next.tolist()):
+                for i, nxt in zip(dev.la_rows.tolist(), dev.la_next.tolist()):
                     state, gi = entries[i][0], entries[i][1]
                     group = self.groups[gi][0]
                     beta2 = float(group["betas"][1])
                     la.append((beta2, 1.0 - beta2, max(float(1 - beta2 ** (state["step"] + int(nxt))), 1e-12),
                                float(group["eps"])))
-                m2 = table["m2"]
+                m2 = dev.table["m2"]
                 for k, name in enumerate(("la_beta2", "la_fresh_weight", "la_bias", "la_eps")):
-                    m2[name][la_rows] = [v[k] for v in la]
-            fields["grad"] = g0
-            fields["grad_scale"] = 0 if coef is None else coef.data_ptr()
-            fields["m1_rng_seed"] = seeds["m1"]
-            fields["m2_rng_seed"] = seeds["m2"]
-            fields["m1_rng_offset"] = offsets["m1"]
-            fields["m2_rng_offset"] = offsets["m2"]
+                    m2[name][dev.la_rows] = [v[k] for v in la]
+            dev.grad_col[:] = g0
+            params, written = dev.params, dev.written
             read = [p.grad for p in params]
+            scale_ref = -1
             if coef is not None:
                 read.append(coef)
-            refs[:, _COL["grad_scale"]] = -1 if coef is None else len(params) + len(written) + len(params)
-            launches.append((params, written, read, table_t, refs_t, []))
+                scale_ref = len(params) + len(written) + len(params)
+            scale_ptr = 0 if coef is None else coef.data_ptr()
+            if scale_ptr != dev.scale_ptr:
+                dev.fields["grad_scale"] = scale_ptr
+                dev.scale_ptr = scale_ptr
+            if scale_ref != dev.scale_ref:
+                dev.refs[:, _COL["grad_scale"]] = scale_ref
+                dev.scale_ref = scale_ref
+            launches.append((params, written, read, dev.table_t, dev.refs_t, []))
 
         def finish(done: int, total: int) -> None:
             if done == total:
