@@ -187,6 +187,36 @@ step_kernel_3w(const StepHeader* __restrict__ hdr, const Tables* __restrict__ ta
     step_body<M1K, M2K, D>(hdr, tables);
 }
 
+// Small steps: the launch table travels in the kernel arguments, so that the step is one launch
+// with no staging copy before it and no staging buffer to recycle after it (the launch packet
+// holds its own copy of the arguments).  The kernel reads the table where the arguments are, so
+// its fields still come through scalar loads.  Instances exist for the two recipes' kernels.
+constexpr int kInlineTableBytes = 3584;
+
+struct __align__(16) InlineArgs {
+    const Tables* tables;
+    uint64_t reserved;
+    unsigned char table[kInlineTableBytes];
+};
+
+template <int M1K, int M2K, int D>
+__device__ __forceinline__ void step_body_inline(const InlineArgs& a) {
+    const StepHeader* hdr =
+        (const StepHeader*)((const char*)__builtin_amdgcn_kernarg_segment_ptr() + offsetof(InlineArgs, table));
+    step_body<M1K, M2K, D>(hdr, a.tables);
+}
+
+template <int M1K, int M2K, int D>
+__global__ void __launch_bounds__(kThreads) step_kernel_inline(const InlineArgs a) {
+    step_body_inline<M1K, M2K, D>(a);
+}
+
+template <int M1K, int M2K, int D>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4)))
+step_kernel_inline_4w(const InlineArgs a) {
+    step_body_inline<M1K, M2K, D>(a);
+}
+
 // The instantiated kernels; the host groups a step's tensors by the variant whose moment
 // specs and dtype they match (optimized-path flags).  ZE-EDEN: NF4 round-to-nearest m1,
 // Dyn4 round-to-nearest m2 with EDEN.  ZIP-SR: NF4 round-to-nearest m1, Dyn4 update-SR m2
@@ -209,14 +239,19 @@ constexpr int kAnyResearch = mspec(K_ANY, AW4_MOMENT_SAMPLED_READ);
 struct KernelVariant {
     int m1, m2, dtype;
     const void* fn;
+    const void* fn_inline;  // the instance taking its table in the arguments, or null
 };
-#define AW4_VARIANT(M1, M2, D) {M1, M2, D, (const void*)&step_kernel<M1, M2, D>}
-#define AW4_VARIANT_4W(M1, M2, D) {M1, M2, D, (const void*)&step_kernel_4w<M1, M2, D>}
-#define AW4_VARIANT_2W(M1, M2, D) {M1, M2, D, (const void*)&step_kernel_2w<M1, M2, D>}
-#define AW4_VARIANT_3W(M1, M2, D) {M1, M2, D, (const void*)&step_kernel_3w<M1, M2, D>}
+#define AW4_VARIANT(M1, M2, D) {M1, M2, D, (const void*)&step_kernel<M1, M2, D>, nullptr}
+#define AW4_VARIANT_4W(M1, M2, D) {M1, M2, D, (const void*)&step_kernel_4w<M1, M2, D>, nullptr}
+#define AW4_VARIANT_2W(M1, M2, D) {M1, M2, D, (const void*)&step_kernel_2w<M1, M2, D>, nullptr}
+#define AW4_VARIANT_3W(M1, M2, D) {M1, M2, D, (const void*)&step_kernel_3w<M1, M2, D>, nullptr}
+#define AW4_VARIANT_I(M1, M2, D) \
+    {M1, M2, D, (const void*)&step_kernel<M1, M2, D>, (const void*)&step_kernel_inline<M1, M2, D>}
+#define AW4_VARIANT_I4W(M1, M2, D) \
+    {M1, M2, D, (const void*)&step_kernel_4w<M1, M2, D>, (const void*)&step_kernel_inline_4w<M1, M2, D>}
 const KernelVariant kVariants[] = {
-    AW4_VARIANT_4W(kRtn, kRtnEden, D_F32),        AW4_VARIANT_4W(kRtn, kUsrGuarded, D_F32),
-    AW4_VARIANT(kRtn, kRtnEden, D_BF16),          AW4_VARIANT(kRtn, kUsrGuarded, D_BF16),
+    AW4_VARIANT_I4W(kRtn, kRtnEden, D_F32),       AW4_VARIANT_I4W(kRtn, kUsrGuarded, D_F32),
+    AW4_VARIANT_I(kRtn, kRtnEden, D_BF16),        AW4_VARIANT_I(kRtn, kUsrGuarded, D_BF16),
     AW4_VARIANT(kSsrGuarded, kUsrGuarded, D_F32), AW4_VARIANT(kSsrGuarded, kUsrGuarded, D_BF16),
     AW4_VARIANT(kRtn, kFp32, D_F32),              AW4_VARIANT(kRtn, kFp32, D_BF16),
     AW4_VARIANT(kRtn, kUsrGuardedEden, D_F32),    AW4_VARIANT(kRtn, kUsrGuardedEden, D_BF16),
@@ -229,6 +264,8 @@ const KernelVariant kVariants[] = {
 #undef AW4_VARIANT_4W
 #undef AW4_VARIANT_2W
 #undef AW4_VARIANT_3W
+#undef AW4_VARIANT_I
+#undef AW4_VARIANT_I4W
 constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 constexpr int kGenericVariant = kNumVariants - 1;
 constexpr int kResearchVariant = kNumVariants - 2;  // generic, for read-back and lookahead m2
@@ -473,6 +510,7 @@ struct DeviceState {
     // until the process ends rather than freed and their pages handed out again.
     std::vector<void*> retired_host;
     std::vector<uint8_t> noalloc_host;  // host image of the tables aw4_fused_step_noalloc stages
+    std::vector<uint8_t> inline_host;   // host image of the tables of small steps (launch arguments)
 };
 
 std::mutex g_mutex;
@@ -802,6 +840,35 @@ int launch_step(const StepLaunch& sl, const char* dev_base, const Tables* tables
     return AW4_OK;
 }
 
+// Bytes of group g's launch table (header, rows, tile starts; without the 256-byte padding).
+size_t group_table_bytes(const StepLaunch& sl, size_t g) {
+    const size_t n = sl.plan[g].members.size();
+    return sizeof(StepHeader) + sizeof(aw4_tensor) * n + sizeof(int64_t) * (n + 1);
+}
+
+// Whether every group can take its table in its launch's arguments.
+bool fits_inline(const StepLaunch& sl) {
+    for (size_t g = 0; g < sl.plan.size(); ++g)
+        if (!kVariants[sl.plan[g].variant].fn_inline || group_table_bytes(sl, g) > (size_t)kInlineTableBytes)
+            return false;
+    return true;
+}
+
+// Launch every group with its table (at host + offset) in the launch's arguments.
+int launch_step_inline(const StepLaunch& sl, const uint8_t* host, const Tables* tables, hipStream_t s) {
+    InlineArgs a;
+    a.tables = tables;
+    a.reserved = 0;
+    for (size_t g = 0; g < sl.plan.size(); ++g) {
+        if (sl.grid[g] == 0) continue;
+        memcpy(a.table, host + sl.offset[g], group_table_bytes(sl, g));
+        void* args[] = {(void*)&a};
+        AW4_HIP_CHECK(hipLaunchKernel(kVariants[sl.plan[g].variant].fn_inline, dim3((unsigned)sl.grid[g]),
+                                      dim3(kThreads), args, 0, s));
+    }
+    return AW4_OK;
+}
+
 // Staging through kernel arguments: each launch carries up to kArgBytes of the table by value
 // and copies them to their place in device memory, so the bytes need no device buffer of the
 // host's and no copy engine, and the host's buffer is free again when the call returns (the
@@ -861,13 +928,20 @@ int aw4_fused_step(const aw4_tensor* tensors, int32_t count, void* stream) {
     DeviceState* ds = nullptr;
     rc = device_state(&ds);
     if (rc) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    if (fits_inline(sl)) {
+        std::vector<uint8_t>& host = ds->inline_host;
+        host.resize(sl.bytes);
+        rc = fill_step_tables(tensors, sl, ds->num_cus, host.data());
+        if (rc) return rc;
+        return launch_step_inline(sl, host.data(), ds->tables, s);
+    }
     StagingSlot* sp = nullptr;
     rc = acquire_slot(ds, sl.bytes, &sp);
     if (rc) return rc;
     StagingSlot& slot = *sp;
     rc = fill_step_tables(tensors, sl, ds->num_cus, slot.host);
     if (rc) return rc;
-    hipStream_t s = (hipStream_t)stream;
     rc = upload_slot(slot, sl.bytes, s);
     if (rc) return rc;
     rc = launch_step(sl, (const char*)slot.dev, ds->tables, s);
