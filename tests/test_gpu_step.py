@@ -632,18 +632,22 @@ def test_mixed_recipes_split_launches(dtype):
     compare_pair(*out, f"mixed recipes {dtype}", steps=4)
 
 
-@pytest.mark.parametrize("m2_scheme", [None, "dyn4_upd_sr_fp32read_nextbc", "dyn4_la_upd_sr", "dyn4_proxy_la_upd_sr",
-                                       "dyn4_vproxy_la_upd_sr"])
-def test_launch_plan_reuse_matches_full_path(m2_scheme):
+@pytest.mark.parametrize("m2_scheme,many", [(None, False), (None, True), ("dyn4_upd_sr_fp32read_nextbc", False),
+                                            ("dyn4_la_upd_sr", False), ("dyn4_proxy_la_upd_sr", False),
+                                            ("dyn4_vproxy_la_upd_sr", False)])
+def test_launch_plan_reuse_matches_full_path(m2_scheme, many):
     """Steps reusing the previous step's launch tables are bit-identical to steps that rebuild
     them, through a learning-rate change, a parameter without gradient, an m1 retarget, and
     state tensors replaced by equal copies (a code or pending-state tensor, a QuantState's
     absmax), which the plan must not keep writing through its old addresses.  With the
     next-step storage bias the group's first tensor is an fp32-state one, whose m2 scheme (fp32)
     has the other bias: the step constants must not be shared across the two.  The lookahead
-    schemes' rows carry a bias correction of the step (or the next) that the plan rewrites."""
-    log(f"launch plan reuse vs full path ({m2_scheme or 'ZIP-SR'})")
-    shapes = [(256, 512), (768,), (64, 1024), (1000,), (128, 384)]
+    schemes' rows carry a bias correction of the step (or the next) that the plan rewrites.
+    `many`: 21 tensors, past the plan's small-plan limit (16 rows, checked and refreshed in
+    Python) and past the launch-argument table (12 rows), so the plan's numpy path and the staged
+    table run."""
+    log(f"launch plan reuse vs full path ({m2_scheme or 'ZIP-SR'}{', 21 tensors' if many else ''})")
+    shapes = [(256, 512), (768,), (64, 1024), (1000,), (128, 384)] + ([(128, 64)] * 16 if many else [])
     q0 = 0
     if m2_scheme is not None:
         shapes[0], shapes[1] = shapes[1], shapes[0]
