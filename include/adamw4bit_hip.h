@@ -157,10 +157,13 @@ int aw4_abi_version(void);
 const char* aw4_last_error(void);
 
 /*
- * One fused AdamW step over `count` parameters in ONE kernel launch on
- * `stream` (a hipStream_t; 0 = legacy default stream).  `tensors` is a host
- * array; it is staged to device memory by the library (the call returns
- * before the step completes, stream-ordered like any HIP launch).
+ * One fused AdamW step over `count` parameters on `stream` (a hipStream_t;
+ * 0 = legacy default stream): one kernel launch per group of parameters that
+ * share a kernel (one launch for a recipe's parameters).  `tensors` is a host
+ * array: a group of up to 12 parameters on the ZE-EDEN or ZIP-SR kernels
+ * receives its rows in its launch's arguments, any other step's rows are
+ * staged to device memory by the library (the call returns before the step
+ * completes, stream-ordered like any HIP launch).
  * Replaces the per-parameter chunk loop of _optimized.py:145-203 and the
  * chunk update _optimized.py:206-234.
  */
