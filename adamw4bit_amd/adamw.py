@@ -17,13 +17,14 @@ the backend's preflight would reject, and every parameter when
 differs only in those two points.
 
 The reference-step m2 variants that read the stored m2 back for the current update
-(``dyn4_upd_sr``, ``lin4_upd_sr``, ``*_upd_sr_store_eden``, ``adamw.py:615-656``) run
-in the same launch, in the generic kernel's read-back instance.
+(``dyn4_upd_sr``, ``lin4_upd_sr``, ``*_upd_sr_store_eden``, ``adamw.py:615-656``) and
+the lookahead update-SR variants (``dyn4_la_upd_sr`` and its proxies, ``adamw.py:566-614``)
+run in the same launch, in kernels of their own.
 
-Outside this build (raise ``NotImplementedError`` on construction): 8-bit state
-(``linear``/``dynamic``, ``AdamW8bit``), the lookahead m2 variants, update
-clipping, diagnostics recording and telemetry callbacks.  Parameters must live
-on a HIP device; there is no CPU implementation.
+Not provided (``NotImplementedError`` on construction): 8-bit state
+(``linear``/``dynamic``, ``AdamW8bit``), update clipping, diagnostics recording and
+telemetry callbacks.  Parameters must live on a HIP device; there is no CPU
+implementation.
 """
 
 from __future__ import annotations

@@ -415,7 +415,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the optimizer step is replica-local "
-              "and this build runs no multi-GPU configuration", file=sys.stderr)
+              "and no multi-GPU configuration is measured here", file=sys.stderr)
         sys.exit(2)
 
     import torch
