@@ -495,11 +495,24 @@ def main():
         print(f"[bench] bf16 mixed set: {bf16_mixed}", file=sys.stderr, flush=True)
         mrecipes = mparams = None
 
-    single = None
+    single = gpt2 = None
     if args.config == "llama3-8b" and clip is None and not args.no_bf16_mixed:
         torch.cuda.empty_cache()
         single = time_single_tensors(device, stream)
         print(f"[bench] single tensors: {single}", file=sys.stderr, flush=True)
+        # The GPT-2-small parameter list (148 tensors, 124M values; its vectors stay fp32 in the
+        # same launch), both recipes, through the same timing as the headline.
+        gshapes, gparams, grecipes, galgo, _ = build_workload("gpt2-small", "zeeden,zipsr", None, device)
+        glaunch, _, _ = time_launches(grecipes, 20, 5, None, stream)
+        gms = {k: statistics.mean(v) for k, v in glaunch.items()}
+        gpt2 = {
+            "workload": "gpt2-small: 148 tensors, 124,439,808 fp32 values, ZE-EDEN and ZIP-SR",
+            "steps": 20, "warmup": 5,
+            "launch_ms": {k: round(v, 4) for k, v in gms.items()},
+            "hbm_frac": {k: round(galgo[k] / (v * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) for k, v in gms.items()},
+        }
+        print(f"[bench] gpt2-small: {gpt2}", file=sys.stderr, flush=True)
+        grecipes = gparams = None
 
     baseline = None
     if not args.no_cpu_baseline:
@@ -536,6 +549,7 @@ def main():
             **({"prologue": prologue} if prologue else {}),
             **({"bf16_mixed": bf16_mixed} if bf16_mixed else {}),
             **({"single_tensors": single} if single else {}),
+            **({"gpt2_small": gpt2} if gpt2 else {}),
         },
         "roofline": {
             "bound": "hbm",
