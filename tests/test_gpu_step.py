@@ -632,6 +632,18 @@ def test_mixed_recipes_split_launches(dtype):
     compare_pair(*out, f"mixed recipes {dtype}", steps=4)
 
 
+@pytest.mark.parametrize("n", [12, 13])
+def test_inline_table_limit(n):
+    """A launch of twelve tensors takes its table in the kernel's arguments (3,504 of 3,584
+    bytes: a 40-byte header, 280 bytes per tensor, 8 per tile start); thirteen (3,792 bytes)
+    stage it through device memory.  Both match the oracle, ZIP-SR over two steps."""
+    log(f"inline table limit: {n} tensors")
+    shapes = [(64, 128 * (1 + k % 3)) for k in range(n)]
+    args = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True, quant_rng_seed=11)
+    out = run_pair(lambda ps: aw.ZIPSRAdamW4Bit(ps, **args), shapes, torch.float32, 2, seed=11)
+    compare_pair(*out, f"{n} tensors", steps=2)
+
+
 @pytest.mark.parametrize("m2_scheme,many", [(None, False), (None, True), ("dyn4_upd_sr_fp32read_nextbc", False),
                                             ("dyn4_la_upd_sr", False), ("dyn4_proxy_la_upd_sr", False),
                                             ("dyn4_vproxy_la_upd_sr", False)])
