@@ -20,6 +20,7 @@ import pytest
 import torch
 
 import adamw4bit_amd as aw
+from tests import gpu_helpers as H
 from tests.test_gpu_step import compare_pair, log, run_pair
 
 pytestmark = pytest.mark.gpu
@@ -95,3 +96,87 @@ def test_random_configuration_matches_oracle(seed):
     out = run_pair(make, shapes, case["dtype"], 3, seed=case["quant_rng_seed"], grad_seed=1000 + seed,
                    m1_override=retarget, zero_block_frac=case["zero_blocks"], grad_fn=GRADS[case["grads"]])
     compare_pair(*out, f"random case {seed}", steps=3)
+
+
+def _flat_state(opt, p) -> dict:
+    """Every entry of a parameter's optimizer state, tensors as bit patterns on the host."""
+    from adamw4bit_amd.quantization import QuantState
+    out = {}
+    for key, value in opt.state[p].items():
+        if isinstance(value, torch.Tensor):
+            out[key] = H.bits(value)
+        elif isinstance(value, QuantState):
+            out[key] = (H.bits(value.absmax), tuple(value.shape) if value.shape is not None else None,
+                        value.dtype, value.blocksize, value.packed)
+        else:
+            out[key] = value
+    return out
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_configuration_resumes_exactly(seed, tmp_path):
+    """Seeded random configurations (other draws than the oracle cases): two steps, a checkpoint
+    written and read back with ``weights_only=True``, three more steps on fresh parameter objects
+    is bit-identical to five uninterrupted steps: parameters and every state entry (codes, block
+    scales, fp32 and pending lookahead state, the store-EDEN denominators, step counts), which
+    also pins the random streams' positions across the checkpoint."""
+    case = draw_case(1000 + seed)
+    log(f"resume case {seed}: {case}")
+    shapes, pairs = [], []
+    for g in case["groups"]:
+        for s in g["shapes"]:
+            shapes.append(s)
+            pairs.append((g["m1"], g["m2"], g["eden"]))
+    dtype = case["dtype"]
+    gen = torch.Generator().manual_seed(2000 + seed)
+    grad_fn = GRADS[case["grads"]] or H.heavy_tailed
+    init = [(torch.randn(s, generator=gen) * 0.02).to(dtype) for s in shapes]
+    grads = [[grad_fn(s, gen).to(dtype) for s in shapes] for _ in range(5)]
+    cand = [i for i, (m1, m2, _) in enumerate(pairs) if m1 in ("nf4", "nf4_sr") and m2 not in LOOKAHEAD]
+    retarget = cand[:1] if case["retarget"] else []
+
+    def make(ps):
+        groups = [dict(params=[p], m1_quant_scheme=a, m2_quant_scheme=b, use_eden_m2=e) for p, (a, b, e) in zip(ps, pairs)]
+        opt = aw.QuantizedAdamW(groups, lr=case["lr"], betas=case["betas"], eps=case["eps"],
+                                weight_decay=case["weight_decay"], m1_quant_scheme="nf4", m2_quant_scheme="dyn4_nz",
+                                quant_rng_seed=case["quant_rng_seed"], optimized=case["optimized"])
+        if case["optimized"] and case["chunk"]:
+            for group in opt.param_groups:
+                group["max_chunk_numel"] = case["chunk"]
+        if retarget:
+            opt.set_m1_quant_scheme_for_parameters([ps[i] for i in retarget],
+                                                   "nf4_sr" if pairs[retarget[0]][0] == "nf4" else "nf4")
+        return opt
+
+    def run(opt, ps, steps):
+        for k in steps:
+            for p, g in zip(ps, grads[k]):
+                p.grad = g.to(H.DEVICE)
+            opt.step()
+
+    a = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
+    oa = make(a)
+    run(oa, a, range(5))
+    b = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
+    ob = make(b)
+    run(ob, b, range(2))
+    torch.save(ob.state_dict(), tmp_path / "ckpt.pt")
+    sd = torch.load(tmp_path / "ckpt.pt", weights_only=True)
+    c = [torch.nn.Parameter(p.detach().clone()) for p in b]
+    oc = make(c)
+    oc.load_state_dict(sd)
+    run(oc, c, range(2, 5))
+    torch.cuda.synchronize()
+    for i, (pa, pc) in enumerate(zip(a, c)):
+        assert torch.equal(H.bits(pa), H.bits(pc)), (seed, i, "parameter")
+        sa, sc = _flat_state(oa, pa), _flat_state(oc, pc)
+        assert set(sa) == set(sc), (seed, i, sorted(sa), sorted(sc))
+        for key in sa:
+            va, vc = sa[key], sc[key]
+            if isinstance(va, torch.Tensor):
+                assert torch.equal(va, vc), (seed, i, key)
+            elif isinstance(va, tuple):
+                assert torch.equal(va[0], vc[0]) and va[1:] == vc[1:], (seed, i, key)
+            else:
+                assert va == vc, (seed, i, key)
+    log(f"  {len(a)} parameters bit-identical after resume")
