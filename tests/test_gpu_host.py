@@ -475,3 +475,64 @@ def test_compiled_step_goes_through_the_operator_and_matches_eager():
     targets = {str(node.target) for gm in counter.graphs for node in gm.graph.nodes if node.op == "call_function"}
     log(f"  {counter.frame_count} frames compiled; call targets {sorted(targets)}")
     assert any("adamw4bit_hip.fused_step_" in t for t in targets), targets
+
+
+def test_concurrent_steps_on_two_streams_match_sequential():
+    """Two host threads, each stepping its own optimizer on its own stream (16 tensors per step,
+    so the tables go through the library's shared staging slots, and one single-tensor optimizer
+    whose table travels in the launch arguments), interleave their library calls; every result
+    is bit-identical to the same steps run one optimizer after the other."""
+    import threading
+
+    log("two threads, two streams")
+    gen = torch.Generator().manual_seed(17)
+    shapes_a = [(128, 64)] * 15 + [(768,)]
+    shapes_b = [(256, 128)]
+    init = {k: [torch.randn(s, generator=gen) * 0.02 for s in sh] for k, sh in (("a", shapes_a), ("b", shapes_b))}
+    grads = {k: [[H.heavy_tailed(s, gen) for s in sh] for _ in range(12)] for k, sh in (("a", shapes_a), ("b", shapes_b))}
+    make = {"a": lambda ps: aw.ZIPSRAdamW4Bit(ps, quant_rng_seed=5, optimized=True, **ARGS),
+            "b": lambda ps: aw.ZEEDENAdamW4Bit(ps, optimized=True, **ARGS)}
+
+    def build(k):
+        ps = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init[k]]
+        gs = [[g.to(H.DEVICE) for g in step] for step in grads[k]]
+        return ps, make[k](ps), gs
+
+    def run(ps, opt, gs, stream):
+        with torch.cuda.stream(stream):
+            for step in gs:
+                for p, g in zip(ps, step):
+                    p.grad = g
+                opt.step()
+        stream.synchronize()
+
+    # sequential reference, each on the default stream
+    seq = {k: build(k) for k in ("a", "b")}
+    torch.cuda.synchronize()
+    for k in ("a", "b"):
+        run(*seq[k], torch.cuda.current_stream())
+    # concurrent: one thread and one stream each (default priority)
+    con = {k: build(k) for k in ("a", "b")}
+    torch.cuda.synchronize()
+    streams = {k: torch.cuda.Stream() for k in ("a", "b")}
+    errors = []
+
+    def worker(k):
+        try:
+            run(*con[k], streams[k])
+        except BaseException as e:  # surfaced in the main thread
+            errors.append((k, e))
+
+    threads = [threading.Thread(target=worker, args=(k,)) for k in ("a", "b")]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not any(t.is_alive() for t in threads), "a stepping thread did not finish"
+    assert not errors, errors
+    torch.cuda.synchronize()
+    for k in ("a", "b"):
+        (pa, oa, _), (pb, ob, _) = seq[k], con[k]
+        for i, (x, y) in enumerate(zip(pa, pb)):
+            same_state(oa, x, ob, y, f"{k} tensor {i}")
+    log("  both threads bit-identical to the sequential runs")
