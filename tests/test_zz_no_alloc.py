@@ -56,3 +56,67 @@ def test_noalloc_step_matches_fused_step(monkeypatch, recipe):
         for i in with_grad:
             _same(oa, pa[i], ob, pb[i], (k, i))
     assert calls == [5, 3]
+
+
+def test_noalloc_step_replays_from_a_hip_graph():
+    """The no-allocation step captured in a graph (torch.cuda.graph over the library call on the
+    capturing stream) and replayed three times, with other eager work and synchronizations
+    between the replays: each replay leaves the parameters and moment state bit-identical to
+    the same launch table called eagerly the same number of times from the same start."""
+    print("noalloc step under graph capture", flush=True)
+    gen = torch.Generator().manual_seed(31)
+    shapes = [(128, 64), (256, 128), (768,)]
+    params = [torch.nn.Parameter((torch.randn(s, generator=gen) * 0.02).to(H.DEVICE)) for s in shapes]
+    opt = aw.ZIPSRAdamW4Bit(params, quant_rng_seed=8, optimized=True)
+    captured = []
+    regular = _lib.fused_step
+    for k in range(2):
+        for p, s in zip(params, shapes):
+            p.grad = H.heavy_tailed(s, gen).to(H.DEVICE)
+        if k == 1:
+            _lib.fused_step = lambda t, st: (captured.append(t.copy()), regular(t, st))
+        try:
+            opt.step()
+        finally:
+            _lib.fused_step = regular
+    table = captured[-1]
+    # everything the table's launch writes, to restore between the eager and the graph runs
+    written = []
+    for p in params:
+        written.append(p.data)
+        for key in ("m1_code", "m2_code", "m1", "m2"):
+            if isinstance(opt.state[p].get(key), torch.Tensor):
+                written.append(opt.state[p][key])
+        for key in ("m1_quant_state", "m2_quant_state"):
+            if opt.state[p].get(key) is not None:
+                written.append(opt.state[p][key].absmax)
+    torch.cuda.synchronize()
+    start = [t.clone() for t in written]
+
+    def snapshot():
+        torch.cuda.synchronize()
+        return [H.bits(t) for t in written]
+
+    stream = torch.cuda.current_stream()
+    eager = []
+    for _ in range(3):
+        _lib.fused_step_noalloc(table, stream.cuda_stream)
+        eager.append(snapshot())
+    for t, s in zip(written, start):
+        t.copy_(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _lib.fused_step_noalloc(table, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    for t, s in zip(written, start):  # capture runs nothing; restore anyway
+        t.copy_(s)
+    other = torch.randn(1 << 20, device=H.DEVICE)
+    for k in range(3):
+        graph.replay()
+        got = snapshot()
+        for i, (a, b) in enumerate(zip(got, eager[k])):
+            assert torch.equal(a, b), (k, i)
+        other.mul_(1.0001)
+        torch.cuda.synchronize()
+    print("  3 replays bit-identical to the eager calls", flush=True)
