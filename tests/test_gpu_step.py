@@ -632,6 +632,18 @@ def test_mixed_recipes_split_launches(dtype):
     compare_pair(*out, f"mixed recipes {dtype}", steps=4)
 
 
+def test_thousands_of_tensors_in_one_launch():
+    """1,536 tensors in one step (a 442 KB launch table staged through a grown slot): 4-bit ones
+    of one to eight tiles and fp32-state ones in between, so that a wave's tiles are found by
+    the binary search over a long tile-start list.  ZIP-SR, two steps, against the oracle."""
+    log("1536 tensors, one launch")
+    cycle = [(32, 128), (100,), (4096,), (7,), (64, 1024), (300,), (8192,), (129,)]
+    shapes = [cycle[k % len(cycle)] for k in range(1536)]
+    args = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True, quant_rng_seed=13)
+    out = run_pair(lambda ps: aw.ZIPSRAdamW4Bit(ps, **args), shapes, torch.float32, 2, seed=13)
+    compare_pair(*out, "1536 tensors", steps=2)
+
+
 @pytest.mark.parametrize("n", [12, 13])
 def test_inline_table_limit(n):
     """A launch of twelve tensors takes its table in the kernel's arguments (3,504 of 3,584
