@@ -218,10 +218,12 @@ def test_golden_trajectory(name):
 def run_pair(make_opt, shapes, dtype, steps, *, seed=0, grad_seed=1, m1_override=None, oracle_kwargs=None,
              zero_block_frac=0.0, grad_fn=None):
     """Step the drop-in optimizer on the GPU and the oracle on the CPU with identical inputs/draws
-    (gradients: ``grad_fn(shape, generator)``, heavy-tailed by default)."""
+    (gradients: ``grad_fn(shape, generator)``, heavy-tailed by default; ``dtype``: one for every
+    tensor, or a list of one per tensor)."""
     grad_fn = grad_fn or H.heavy_tailed
     gen = torch.Generator().manual_seed(grad_seed)
-    init = [(torch.randn(s, generator=gen) * 0.02).to(dtype) for s in shapes]
+    dtypes = list(dtype) if isinstance(dtype, (list, tuple)) else [dtype] * len(shapes)  # one per tensor
+    init = [(torch.randn(s, generator=gen) * 0.02).to(dt) for s, dt in zip(shapes, dtypes)]
     params = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
     opt = make_opt(params)
     if m1_override:
@@ -243,12 +245,12 @@ def run_pair(make_opt, shapes, dtype, steps, *, seed=0, grad_seed=1, m1_override
     parted = [torch.zeros(p.numel(), dtype=torch.bool) for p in params]
     for _ in range(steps):
         grads = []
-        for s in shapes:
+        for s, dt in zip(shapes, dtypes):
             g = grad_fn(s, gen)
             if zero_block_frac and g.numel() % 128 == 0:
                 nb = g.numel() // 128
                 g.view(nb, 128)[torch.rand(nb, generator=gen) < zero_block_frac] = 0.0
-            grads.append(g.to(dtype))
+            grads.append(g.to(dt))
         for p, g in zip(params, grads):
             p.grad = g.to(H.DEVICE)
         opt.step()
@@ -630,6 +632,19 @@ def test_mixed_recipes_split_launches(dtype):
                                  m1_quant_scheme="nf4", m2_quant_scheme="dyn4_nz", quant_rng_seed=5, optimized=True)
     out = run_pair(make, shapes, dtype, 4, seed=5, m1_override=([6], "nf4_sr"), zero_block_frac=0.02)
     compare_pair(*out, f"mixed recipes {dtype}", steps=4)
+
+
+def test_mixed_parameter_dtypes_in_one_step():
+    """fp32, bf16 and fp16 parameters in one optimizer step (one launch per dtype's specialised
+    kernel, the fp32-state vectors with their dtype's launch), ZIP-SR with an nf4_sr retarget,
+    three steps against the oracle."""
+    log("mixed parameter dtypes")
+    shapes = [(256, 128), (256, 128), (256, 128), (768,), (768,), (768,), (64, 512), (4096,), (1000,)]
+    dtypes = [torch.float32, torch.bfloat16, torch.float16] * 3
+    args = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True, quant_rng_seed=29)
+    out = run_pair(lambda ps: aw.ZIPSRAdamW4Bit(ps, **args), shapes, dtypes, 3, seed=29, m1_override=([1, 6], "nf4_sr"),
+                   zero_block_frac=0.03)
+    compare_pair(*out, "mixed dtypes", steps=3)
 
 
 def test_thousands_of_tensors_in_one_launch():
