@@ -787,6 +787,18 @@ int prepare_step(const aw4_tensor* tensors, int32_t count, StepLaunch& sl) {
     return AW4_OK;
 }
 
+// Tiles per wave of a large launch: three for the kernels that take their tiles in grid order
+// (round to nearest, bound by memory), four for the others.  Measured on the Llama-3-8B fp32
+// set, in-process A/B on two boxes: three took ZE-EDEN from 20.33 to 20.15 ms and from 20.44
+// to 20.26 ms, and ZIP-SR from 21.11 to 21.19 ms (so it keeps four); five cost ZE-EDEN 2%.
+int large_tiles_per_wave(int variant) {
+    if (variant < kNumSpecialised) {
+        const KernelVariant& kv = kVariants[variant];
+        if (tile_order_grid(kv.m1, kv.m2, kv.dtype)) return 3;
+    }
+    return kTilesPerWave;
+}
+
 // Write each group's launch table into `dst` (host memory of sl.bytes) and set its grid.
 //
 // A few tiles per wave and a grid covering all of them: the hardware dispatcher hands each free
@@ -812,10 +824,10 @@ int fill_step_tables(const aw4_tensor* tensors, StepLaunch& sl, int num_cus, voi
         }
         starts[n] = acc;
         // Small launches take fewer tiles per wave so that their waves still spread over every
-        // CU: 4 tiles per wave from 128 tiles per CU, 2 from 8, else 1 (measured on one 4096^2
-        // and one 1024^2 tensor, and the GPT-2-small list).
+        // CU: 3 or 4 tiles per wave from 128 tiles per CU, 2 from 8, else 1 (measured on one
+        // 4096^2 and one 1024^2 tensor, and the GPT-2-small list).
         const int64_t per_cu = acc / (int64_t)num_cus;
-        const int tiles_per_wave = per_cu >= 128 ? kTilesPerWave : per_cu >= 8 ? 2 : 1;
+        const int tiles_per_wave = per_cu >= 128 ? large_tiles_per_wave(lg.variant) : per_cu >= 8 ? 2 : 1;
         const int64_t waves = (acc + tiles_per_wave - 1) / tiles_per_wave;
         sl.grid[g] = (waves + kWavesPerGroup - 1) / kWavesPerGroup;
         if (sl.grid[g] > 0x7fffffff)
