@@ -10,7 +10,9 @@ one, fp32 / bf16 / fp16 parameters, tensors on the 4-bit path and on the fp32-st
 (fewer than 4,096 values or not a multiple of 128), betas on both sides of ATen's lerp switch,
 weight decay on and off, the optimized step's chunk size (its draw accounting), and gradients
 from heavy-tailed to tiny, with and without all-zero blocks.  Three steps each, so the second and
-third reuse the first step's launch plan.  The configuration is printed before the case runs."""
+third reuse the first step's launch plan.  Eight more cases draw tensors of up to 33.6M values,
+whose launches take 2, 3 or 4 tiles per wave.  The configuration is printed before the case
+runs."""
 
 from __future__ import annotations
 
@@ -44,7 +46,11 @@ GRADS = {
 }
 
 
-def draw_case(seed: int) -> dict:
+# Larger tensors, whose launches take 2, 3 or 4 tiles per wave (the pool above stays at one)
+LARGE_SHAPES = [(4096, 4096), (8192, 4096), (2048, 2048), (1024, 1024), (768,), (4097,), (128, 64)]
+
+
+def draw_case(seed: int, shapes=SHAPES) -> dict:
     rng = random.Random(seed)
     dtype = rng.choice([torch.float32, torch.float32, torch.bfloat16, torch.float16])
     groups = []
@@ -52,7 +58,7 @@ def draw_case(seed: int) -> dict:
         m2, eden_ok = rng.choice(M2)
         m1 = rng.choice(["fp32", "nf4"] if m2 in LOOKAHEAD else M1)
         eden = eden_ok and rng.random() < 0.5
-        groups.append(dict(m1=m1, m2=m2, eden=eden, shapes=[rng.choice(SHAPES) for _ in range(rng.randint(1, 2))]))
+        groups.append(dict(m1=m1, m2=m2, eden=eden, shapes=[rng.choice(shapes) for _ in range(rng.randint(1, 2))]))
     grads = rng.choice(list(GRADS))
     return dict(
         seed=seed, dtype=dtype, groups=groups, grads=grads,
@@ -70,7 +76,16 @@ def draw_case(seed: int) -> dict:
 
 @pytest.mark.parametrize("seed", range(96))
 def test_random_configuration_matches_oracle(seed):
-    case = draw_case(seed)
+    _check_against_oracle(seed, draw_case(seed))
+
+
+@pytest.mark.parametrize("seed", range(5005, 5013))
+def test_large_random_configuration_matches_oracle(seed):
+    """The same with tensors of up to 33.6M values (launches of 2-4 tiles per wave)."""
+    _check_against_oracle(seed, draw_case(seed, LARGE_SHAPES))
+
+
+def _check_against_oracle(seed: int, case: dict) -> None:
     log(f"random case {seed}: {case}")
     shapes, pairs = [], []
     for g in case["groups"]:
