@@ -539,8 +539,11 @@ __device__ __forceinline__ void step_values_one(const aw4_tensor& T, int64_t k) 
     v2[k] = b;
 }
 
+// Out of line (a cold path); the row is read through a global pointer, so that its fields are
+// global loads here too (a generic one would give flat instructions).
 template <int D>
-__device__ void step_tile_values(const aw4_tensor& T, int64_t e_tile, int lane) {
+__device__ void step_tile_values(gptr<const aw4_tensor> row, int64_t e_tile, int lane) {
+    const aw4_tensor& T = *(const aw4_tensor*)row;
     const int j = lane & 7;
     const int grp = lane >> 3;
 #pragma unroll
@@ -644,7 +647,7 @@ __device__ __forceinline__ void run_tiles(const StepHeader* hdr, const LdsT& lds
         const bool more = ++k < per_wave && next < total;
         int tn = -1;  // tensor of `next`, once searched
         if (values_only(T)) {
-            step_tile_values<D>(T, local * kWaveTile, lane);
+            step_tile_values<D>((gptr<const aw4_tensor>)&T, local * kWaveTile, lane);
             loaded = false;
         } else {
             const TileLane tl = tile_lane(T, local * kBlocksPerWave, lane);

@@ -123,7 +123,7 @@ struct LdsAll {
     Tables t;
     WaveScratch scratch[kWavesPerGroup];
 
-    __device__ MomentTables moment(const aw4_moment& m, int) const {
+    __device__ __forceinline__ MomentTables moment(const aw4_moment& m, int) const {
         const int cbid = m.rounding == AW4_ROUND_FP32 ? 0 : m.codebook;
         return MomentTables{t.codebook[cbid], t.pairs[cbid], t.dec[cbid],
                             t.lut[m.rounding == AW4_ROUND_FP32 ? 0 : lut_id_of(m.rounding, cbid, m.flags)],
@@ -425,7 +425,9 @@ bool build_lut(LutEntry* out, F f, const float* cb, std::string& err) {
             LutEntry e;
             e.base = (uint32_t)base;
             if (top == base) {
-                e.thr = host_f(0x7f800000u);  // +inf: never increments
+                // NaN: x >= thr is false for every x (an infinite threshold would still
+                // increment at x = +inf, one past the bucket's count)
+                e.thr = host_f(0x7fc00000u);
             } else if (top == base + 1) {
                 // smallest x (in value order) with f(x) == base + 1
                 uint32_t good = amax, bad = amin;
@@ -896,7 +898,7 @@ struct __align__(16) ArgChunk {
 
 __global__ void __launch_bounds__(256) stage_args_kernel(const ArgChunk chunk) {
     const uint4* src = (const uint4*)((const char*)__builtin_amdgcn_kernarg_segment_ptr() + offsetof(ArgChunk, data));
-    for (uint32_t i = threadIdx.x; i < chunk.n16; i += 256) ((uint4*)chunk.dst)[i] = src[i];
+    for (uint32_t i = threadIdx.x; i < chunk.n16; i += 256) gaddr<u32x4>(chunk.dst)[i] = ((const u32x4*)src)[i];
 }
 
 int upload_by_arguments(const void* src, size_t bytes, uint8_t* dst, hipStream_t s) {

@@ -237,6 +237,19 @@ def test_encode_tables_reproduce_rounding_rules(mode, cb_id):
         assert np.array_equal(lut_level(tables, 5, x), cb[floored])
 
 
+@pytest.mark.parametrize("mode,cb_id", LUT_CODEBOOKS)
+def test_encode_tables_on_infinite_and_nan_values(mode, cb_id):
+    """+-inf and NaN take searchsorted's count and round-to-nearest code too: no table entry
+    increments past its bucket's count (a bucket without a change has a NaN threshold).  A NaN x
+    reaches the table as the positive quiet NaN (the encode makes it so)."""
+    tables = _lib.encode_tables()
+    cb = np.array(q.CODEBOOK_VALUES[cb_id], dtype=np.float32)
+    x = np.array([np.inf, -np.inf, np.nan, 3e38, -3e38], dtype=np.float32)
+    count, rtn = reference_rules(cb, x)
+    assert np.array_equal(lut_eval(tables, 6 + cb_id, x), count)
+    assert np.array_equal(lut_eval(tables, cb_id, x), rtn)
+
+
 def test_aten_row_sum_order():
     """The per-block sum order the kernel reproduces (8 lanes x 4 accumulators) is ATen's."""
     gen = torch.Generator().manual_seed(0)
