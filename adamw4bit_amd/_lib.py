@@ -17,11 +17,11 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIBRARY = os.path.join(HERE, "libadamw4bit_hip.so")
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 BLOCK = 128
 
 # Error codes
-OK, EINVAL, EHIP, EALIGN = 0, -1, -2, -3
+OK, EINVAL, EHIP, EALIGN, ELAUNCHED = 0, -1, -2, -3, -4
 
 # Codebooks / rounding / flags (AW4_* in the header)
 CB_NF4, CB_SDYN4, CB_DYN4, CB_LIN4, CB_LIN4_NZ = 0, 1, 2, 3, 4
@@ -64,11 +64,18 @@ SIGNATURES = {
     "aw4_encode_tables": (ctypes.c_int64, [ctypes.c_void_p, ctypes.c_int64]),
     "aw4_clip_coefficient": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_float, ctypes.c_void_p,
                                             ctypes.c_void_p, ctypes.c_void_p]),
+    "aw4_inject_launch_failure": (None, [ctypes.c_int32]),
 }
 
 
 class HipLibraryError(RuntimeError):
-    """A call into the HIP library failed (the message is aw4_last_error())."""
+    """A call into the HIP library failed (the message is aw4_last_error()).  Unless it is a
+    HipLaunchIncomplete, the call enqueued no step kernel."""
+
+
+class HipLaunchIncomplete(HipLibraryError):
+    """A step failed after some of its kernels were enqueued (AW4_ELAUNCHED): the parameters and
+    moment state it covers may be partly updated."""
 
 
 _lib: Optional[ctypes.CDLL] = None
@@ -98,7 +105,7 @@ def library() -> ctypes.CDLL:
 def check(rc: int, what: str) -> int:
     if rc < 0:
         message = library().aw4_last_error().decode(errors="replace")
-        raise HipLibraryError(f"{what} failed ({rc}): {message}")
+        raise (HipLaunchIncomplete if rc == ELAUNCHED else HipLibraryError)(f"{what} failed ({rc}): {message}")
     return rc
 
 
@@ -131,6 +138,12 @@ def clip_coefficient(table: np.ndarray, max_norm: float, norm_ptr: int, coef_ptr
     assert table.dtype == TENSOR and table.flags.c_contiguous
     check(library().aw4_clip_coefficient(table.ctypes.data, len(table), max_norm, norm_ptr, coef_ptr, stream),
           "aw4_clip_coefficient")
+
+
+def inject_launch_failure(after: int) -> None:
+    """Make the next fused step on this thread fail after `after` step kernel launches (tests of
+    error handling; no launch is attempted at that point).  Negative: clear."""
+    library().aw4_inject_launch_failure(after)
 
 
 def uniforms(seed: int, offset: int, n: int, out_ptr: int, stream: int) -> None:

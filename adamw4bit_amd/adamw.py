@@ -443,6 +443,7 @@ class QuantizedAdamW(Optimizer):
         self._draw_provider = None
         self._launch_plan: Optional[_LaunchPlan] = None
         self._pending_finish = None  # commit / undo of the step being launched
+        self._inconsistent: Optional[str] = None  # why step() refuses to run (a partly enqueued step)
         # Gradient clipping computed by clip_grad_norm_ and applied by the next step:
         # (device, fp32 coefficient on that device) or None.
         self._grad_clip: Optional[Tuple[torch.device, torch.Tensor]] = None
@@ -596,6 +597,7 @@ class QuantizedAdamW(Optimizer):
         self._quant_generators = {"m1": {}, "m2": {}}
         self._pending_quant_rng_states = {"m1": {}, "m2": {}}
         self._launch_plan = None
+        self._inconsistent = None  # the loaded state replaces whatever a failed step left
         if rng_payload is not None:
             if not isinstance(rng_payload, Mapping):
                 raise ValueError("Invalid quantization RNG checkpoint payload")
@@ -750,26 +752,44 @@ class QuantizedAdamW(Optimizer):
         otherwise.  A step changes nothing unless it launches: every parameter is checked before
         any state changes, and a failed launch restores step counts, moment state and random
         stream positions."""
+        if self._inconsistent is not None:
+            raise RuntimeError(self._inconsistent)
         loss = None
         if closure is not None:
             with torch.enable_grad():
                 loss = closure()
         launches = self._prepare_launches()
         done = 0
+        incomplete = False
         try:
             for launch in launches:
-                _launch(*launch)
+                try:
+                    _launch(*launch)
+                except _lib.HipLaunchIncomplete:
+                    incomplete = True
+                    raise
                 done += 1
         finally:
-            self._finish_step(done, len(launches))
+            self._finish_step(done, len(launches), incomplete)
         return loss
 
     @torch.compiler.disable
-    def _finish_step(self, done: int, total: int) -> None:
-        """Commit the prepared step after its launches (``done == total``), or undo it if none ran."""
+    def _finish_step(self, done: int, total: int, incomplete: bool = False) -> None:
+        """Commit the prepared step after its launches (``done == total``), or undo it if no step
+        kernel was enqueued.  A step that failed after enqueuing some of its kernels (a launch that
+        failed part way, or one device's launch after another's) cannot be undone: the tensors may
+        be partly updated, so the optimizer refuses further steps until a checkpoint is loaded."""
         finish, self._pending_finish = self._pending_finish, None
-        if finish is not None:
+        if finish is None:
+            return
+        if done == total or (done == 0 and not incomplete):
             finish(done, total)
+            return
+        self._launch_plan = None
+        self._inconsistent = (
+            f"a step failed after {'some of its kernels' if incomplete else f'{done} of its {total} launches'} "
+            "were enqueued: parameters and moment state may be partly updated; load a checkpoint with "
+            "load_state_dict() before stepping again")
 
     @torch.compiler.disable
     def _prepare_launches(self):

@@ -229,7 +229,7 @@ __device__ __forceinline__ void draws_quarter(const aw4_moment& M, int64_t blk0,
             v = *(gptr<const f32x4>)(gaddr<const float>(M.draws) + (blk0 + grp) * kBlock + 32 * q + 4 * j);
         u[0] = v.x * 0x1p24f; u[1] = v.y * 0x1p24f; u[2] = v.z * 0x1p24f; u[3] = v.w * 0x1p24f;
     } else {
-        if (q < 3) philox_lane_call(M.rng_seed, (M.rng_offset >> 7) + (uint64_t)(blk0 + grp), j, q, &rw[4 * q]);
+        if (q < 3) philox_tile_call(M.rng_seed, (M.rng_offset >> 7) + (uint64_t)blk0, grp, j, q, &rw[4 * q]);
         lane_fields4(&rw[3 * q], u);
     }
 }
@@ -244,13 +244,26 @@ __device__ __forceinline__ float usr_precond(const aw4_moment& M, float s, float
 
 // Update-SR decision by the reference's operations (_compiled_quantization.py:74-109):
 // valid = (b > a) & (f(a) - f(b) > 0); lower = u < (f(x) - f(b)) / max(f(a) - f(b), 1e-30),
-// u = U * 2^-24.  The clamp of P to [0, 1] never changes u < P for u in [0, 1).
-__device__ __forceinline__ void usr_exact(const aw4_moment& M, float s, float x, float a, float b, float U, bool& valid,
-                                       bool& lower) {
-    const float fa = usr_precond(M, s, a), fb = usr_precond(M, s, b), fx = usr_precond(M, s, x);
+// u = U * 2^-24.  The clamp of P to [0, 1] never changes u < P for u in [0, 1).  fa and fb are
+// the preconditioners of the levels a and b (usr_precond of the block's scale and the level,
+// from the block's table: usr_level_preconds).
+__device__ __forceinline__ void usr_exact(const aw4_moment& M, float s, float x, float a, float b, float fa, float fb,
+                                          float U, bool& valid, bool& lower) {
+    const float fx = usr_precond(M, s, x);
     const float den = fa - fb;
     valid = (b > a) & (den > 0.0f);
     lower = U * 0x1p-24f < (fx - fb) / clamp_min_nan(den, 1e-30f);
+}
+
+// The reference's preconditioners of the block's 16 levels, f(l) = usr_precond(s, l), into the
+// block's 16-entry table (two per lane), for usr_exact: the same function of the same inputs as
+// an evaluation per value, so the same bits.  The table reuses the slots of the quick form's
+// E(l), which update_sr_tables has finished reading.
+__device__ __forceinline__ void usr_level_preconds(const MomentTables& L, int j, float s, const aw4_moment& M,
+                                                   float* pre) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) pre[j + 8 * h] = usr_precond(M, s, L.cb[j + 8 * h]);
+    wave_lds_sync();
 }
 
 // The quick decision (see update_sr_tables): returns Q, where Q > 0 means lower; `sure` is false
@@ -330,6 +343,7 @@ __device__ __forceinline__ BlockScales encode_block(const aw4_moment& M, const M
 
     float acc_xx[4] = {0.0f, 0.0f, 0.0f, 0.0f}, acc_xl[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     uint32_t rw[12];  // Philox words of this lane's position group (stochastic kinds)
+    bool level_preconds = false;  // the block's table of level preconditioners is built (update-SR)
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         float x[4], mq[4];
@@ -393,6 +407,7 @@ __device__ __forceinline__ BlockScales encode_block(const aw4_moment& M, const M
                 // paths below meet in plain registers
                 float dq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
                 uint64_t unsure = 1;  // lanes (bits) with a value the quick test leaves open
+                bool open[4] = {true, true, true, true};  // per value: left open (every value off the quick path)
                 if (__builtin_expect(wave_fast, 1)) {
                     unsure = 0;
 #pragma unroll
@@ -400,19 +415,28 @@ __device__ __forceinline__ BlockScales encode_block(const aw4_moment& M, const M
                         const UpdEntry ue = sc.upd[idx[t]];
                         bool sure;
                         dq[t] = usr_quick(ue, ub, M.sr_eps, x[t], u[t], sure);
+                        open[t] = !sure;
                         unsure |= __builtin_amdgcn_ballot_w64(!sure);
                     }
                 }
-                // A quarter with any open value (a few in a hundred) is decided again by the
-                // reference's operations, every value of it: where the quick test was sure the two
-                // agree, so nothing needs to be selected.  The branch is uniform.  It leaves
-                // code = idx - lower with idx in [0, 15], the clamps folded into lower and idx.
+                // A quarter with any open value (a few in a hundred) decides its open values again
+                // by the reference's operations (a branch per value slot, taken where any lane has
+                // that slot open; the quarter's branch is uniform).  Where the quick test was sure
+                // the two agree.  It leaves code = idx - lower with idx in [0, 15], the clamps folded
+                // into lower and idx.
                 if (unsure != 0) {
+                    // the levels' preconditioners once per block encode, when a quarter first needs them
+                    if (!level_preconds) {
+                        usr_level_preconds(L, j, s, M, sc.pre);
+                        level_preconds = true;
+                    }
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
+                        if (!open[t]) continue;
                         const PairEntry pe = L.pairs[idx[t]];
                         bool valid, dl;
-                        usr_exact(M, s, x[t], pe.a, pe.b, u[t], valid, dl);
+                        usr_exact(M, s, x[t], pe.a, pe.b, sc.pre[pe.lohi & 0xffu], sc.pre[pe.lohi >> 8], u[t], valid,
+                                  dl);
                         // bitwise operators: the operands are all computed, and short-circuit
                         // forms become per-value branches
                         const bool at_b = x[t] >= pe.b;
@@ -518,7 +542,7 @@ __device__ __forceinline__ void la_draws_quarter(const aw4_moment& M, int64_t bl
             U[t] = 0.0f;
         }
     } else {
-        if (q < 3) philox_lane_call(M.rng_seed, (M.rng_offset >> 7) + (uint64_t)(blk0 + grp), j, q, &rw[4 * q]);
+        if (q < 3) philox_tile_call(M.rng_seed, (M.rng_offset >> 7) + (uint64_t)blk0, grp, j, q, &rw[4 * q]);
         lane_fields4(&rw[3 * q], U);
 #pragma unroll
         for (int t = 0; t < 4; ++t) u[t] = (double)U[t] * 0x1p-24;

@@ -188,10 +188,28 @@ __device__ __forceinline__ void philox4x32_10(uint32_t c0, uint32_t c1, uint32_t
     out[3] = c3;
 }
 
+// Philox(counter = ctr, key = seed): four output words.
+__device__ __forceinline__ void philox_call(uint64_t seed, uint64_t ctr, uint32_t* w) {
+    philox4x32_10((uint32_t)ctr, (uint32_t)(ctr >> 32), (uint32_t)seed, (uint32_t)(seed >> 32), w);
+}
+
 // Call r (0..2) of lane j in position group B: words 4r .. 4r+3 of the lane's 384-bit string.
 __device__ __forceinline__ void philox_lane_call(uint64_t seed, uint64_t group, int j, int r, uint32_t* w) {
-    const uint64_t ctr = group * 24u + (uint64_t)(3 * j + r);
-    philox4x32_10((uint32_t)ctr, (uint32_t)(ctr >> 32), (uint32_t)seed, (uint32_t)(seed >> 32), w);
+    philox_call(seed, group * 24u + (uint64_t)(3 * j + r), w);
+}
+
+// The same call for block grp of a wave tile whose first block is position group g0 (wave-uniform):
+// counter 24 (g0 + grp) + 3 j + r = 24 g0 + 3 (8 grp + j) + r, so the 64-bit product is the
+// wave's (a scalar one) and each lane adds its small constant.
+__device__ __forceinline__ void philox_tile_call(uint64_t seed, uint64_t g0, int grp, int j, int r, uint32_t* w) {
+    // The product in scalar registers: read as the first lane's (g0 is the wave tile's, the same in
+    // every lane), and held there by an empty asm statement, so that each lane's counter is one
+    // 64-bit add rather than two 64-bit vector multiply-adds.
+    const uint64_t prod = g0 * 24u;
+    uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)prod);
+    uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(prod >> 32));
+    asm("" : "+s"(lo), "+s"(hi));
+    philox_call(seed, ((uint64_t)hi << 32 | lo) + (uint32_t)(24 * grp + 3 * j + r), w);
 }
 
 // Fields 4q .. 4q+3 of a lane's string (words 3q .. 3q+2), as exact floats in [0, 2^24):

@@ -355,6 +355,7 @@ __global__ void __launch_bounds__(kThreads) uniforms_kernel(uint64_t seed, uint6
 // ---------------------------------------------------------------------------
 
 thread_local std::string g_error;
+thread_local int g_fail_after = -1;  // aw4_inject_launch_failure
 
 int set_error(int code, const char* fmt, ...) {
     char buf[512];
@@ -842,14 +843,31 @@ int fill_step_tables(const aw4_tensor* tensors, StepLaunch& sl, int num_cus, voi
     return AW4_OK;
 }
 
+// One step kernel launch of a call that has made `launched` of them: a failure after the first
+// is AW4_ELAUNCHED (the step's tensors may be partly updated).  aw4_inject_launch_failure makes
+// the launch fail here without attempting it.
+int launch_one(const void* fn, unsigned grid, void** args, hipStream_t s, int& launched) {
+    const int code = launched > 0 ? AW4_ELAUNCHED : AW4_EHIP;
+    if (g_fail_after >= 0 && launched >= g_fail_after) {
+        g_fail_after = -1;
+        return set_error(code, "step kernel launch %d: failure injected by aw4_inject_launch_failure", launched + 1);
+    }
+    const hipError_t err = hipLaunchKernel(fn, dim3(grid), dim3(kThreads), args, 0, s);
+    if (err != hipSuccess)
+        return set_error(code, "step kernel launch %d: %s%s", launched + 1, hipGetErrorString(err),
+                         launched > 0 ? " (earlier launches of this step were enqueued)" : "");
+    ++launched;
+    return AW4_OK;
+}
+
 // Launch every group whose table is at dev_base + offset.
-int launch_step(const StepLaunch& sl, const char* dev_base, const Tables* tables, hipStream_t s) {
+int launch_step(const StepLaunch& sl, const char* dev_base, const Tables* tables, hipStream_t s, int& launched) {
     for (size_t g = 0; g < sl.plan.size(); ++g) {
         if (sl.grid[g] == 0) continue;
         const StepHeader* dh = (const StepHeader*)(dev_base + sl.offset[g]);
         void* args[] = {(void*)&dh, (void*)&tables};
-        AW4_HIP_CHECK(hipLaunchKernel(kVariants[sl.plan[g].variant].fn, dim3((unsigned)sl.grid[g]), dim3(kThreads),
-                                      args, 0, s));
+        const int rc = launch_one(kVariants[sl.plan[g].variant].fn, (unsigned)sl.grid[g], args, s, launched);
+        if (rc) return rc;
     }
     return AW4_OK;
 }
@@ -873,12 +891,13 @@ int launch_step_inline(const StepLaunch& sl, const uint8_t* host, const Tables* 
     InlineArgs a;
     a.tables = tables;
     a.reserved = 0;
+    int launched = 0;
     for (size_t g = 0; g < sl.plan.size(); ++g) {
         if (sl.grid[g] == 0) continue;
         memcpy(a.table, host + sl.offset[g], group_table_bytes(sl, g));
         void* args[] = {(void*)&a};
-        AW4_HIP_CHECK(hipLaunchKernel(kVariants[sl.plan[g].variant].fn_inline, dim3((unsigned)sl.grid[g]),
-                                      dim3(kThreads), args, 0, s));
+        const int rc = launch_one(kVariants[sl.plan[g].variant].fn_inline, (unsigned)sl.grid[g], args, s, launched);
+        if (rc) return rc;
     }
     return AW4_OK;
 }
@@ -958,10 +977,14 @@ int aw4_fused_step(const aw4_tensor* tensors, int32_t count, void* stream) {
     if (rc) return rc;
     rc = upload_slot(slot, sl.bytes, s);
     if (rc) return rc;
-    rc = launch_step(sl, (const char*)slot.dev, ds->tables, s);
+    int launched = 0;
+    rc = launch_step(sl, (const char*)slot.dev, ds->tables, s, launched);
+    // the slot is in use by whatever was enqueued: it is not reused before that completes
+    const hipError_t err = hipEventRecord(slot.done, s);
+    slot.pending = err == hipSuccess;
     if (rc) return rc;
-    AW4_HIP_CHECK(hipEventRecord(slot.done, s));
-    slot.pending = true;
+    if (err != hipSuccess)
+        return set_error(AW4_ELAUNCHED, "hipEventRecord after the step's launches: %s", hipGetErrorString(err));
     return AW4_OK;
 }
 
@@ -986,8 +1009,11 @@ int aw4_fused_step_noalloc(const aw4_tensor* tensors, int32_t count, void* strea
     hipStream_t s = (hipStream_t)stream;
     rc = upload_by_arguments(host.data(), sl.bytes, ds->scratch, s);
     if (rc) return rc;
-    return launch_step(sl, (const char*)ds->scratch, ds->tables, s);
+    int launched = 0;
+    return launch_step(sl, (const char*)ds->scratch, ds->tables, s, launched);
 }
+
+void aw4_inject_launch_failure(int32_t after) { g_fail_after = after < 0 ? -1 : after; }
 
 int aw4_quantize(const float* values, int64_t numel, const aw4_moment* m, void* stream) {
     g_error.clear();

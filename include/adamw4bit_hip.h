@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define AW4_ABI_VERSION 5
+#define AW4_ABI_VERSION 6
 #define AW4_BLOCK 128 /* values per block scale (quantization.py:694-703, 4-bit default) */
 
 /* Error codes. */
@@ -40,6 +40,10 @@ extern "C" {
 #define AW4_EINVAL -1  /* malformed descriptor (null pointer, bad enum, bad size) */
 #define AW4_EHIP -2    /* a HIP runtime call failed */
 #define AW4_EALIGN -3  /* a buffer violates the alignment its descriptor promises */
+/* A step failed after some of its step kernels were enqueued: parameters and
+ * moment state may be partly updated (every other error enqueues no step
+ * kernel, so the caller's tensors are unchanged). */
+#define AW4_ELAUNCHED -4
 
 /* 16-level codebooks (quantization.py:201-237, 401-422, 457-497). */
 #define AW4_CB_NF4 0     /* nf4, nf4_sr */
@@ -184,6 +188,15 @@ int aw4_fused_step(const aw4_tensor* tensors, int32_t count, void* stream);
  */
 #define AW4_NOALLOC_TABLE_BYTES (1 << 20)
 int aw4_fused_step_noalloc(const aw4_tensor* tensors, int32_t count, void* stream);
+
+/*
+ * For tests of a caller's error handling; no counterpart in the reference.  The
+ * next aw4_fused_step or aw4_fused_step_noalloc call on this thread makes
+ * `after` step kernel launches and then fails as a failed launch would
+ * (AW4_ELAUNCHED if `after` > 0, else AW4_EHIP): the launch is not made, so no
+ * device fault is involved.  A negative `after` clears it.
+ */
+void aw4_inject_launch_failure(int32_t after);
 
 /*
  * Encode `numel` fp32 values (numel a multiple of 128) into the quantized

@@ -277,6 +277,54 @@ def test_rejected_parameter_leaves_every_state_untouched():
     same_state(opt, good, ot, twin, "after the rejected step")
 
 
+def test_step_failing_after_enqueued_kernels_refuses_further_steps():
+    """A step whose launches fail after some of its step kernels were enqueued cannot be undone
+    (its tensors may be partly updated).  Injected in the library: the step of an fp32 and a bf16
+    parameter is two launches; the first is made, the second fails without being attempted
+    (AW4_ELAUNCHED).  The step raises HipLaunchIncomplete, the optimizer refuses further steps, and
+    after the parameters and a checkpoint from before the failure are loaded it continues bit for bit
+    like an optimizer that never failed.  With the failure at the first launch nothing was enqueued
+    and the step is undone as before."""
+    log("failure after enqueued kernels: refused until a checkpoint is loaded")
+    gen = torch.Generator().manual_seed(23)
+    shapes = [(128, 256), (64, 256)]
+    dtypes = [torch.float32, torch.bfloat16]
+    init = [(torch.randn(s, generator=gen) * 0.02).to(dt) for s, dt in zip(shapes, dtypes)]
+    pa = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
+    pb = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
+    oa = aw.ZIPSRAdamW4Bit(pa, optimized=True, quant_rng_seed=5, **ARGS)
+    ob = aw.ZIPSRAdamW4Bit(pb, optimized=True, quant_rng_seed=5, **ARGS)
+    for k in range(5):
+        gs = [H.heavy_tailed(s, gen).to(dt).to(H.DEVICE) for s, dt in zip(shapes, dtypes)]
+        for a, b, g in zip(pa, pb, gs):
+            a.grad, b.grad = g.clone(), g.clone()
+        if k in (1, 3):  # k == 1: the full path; k == 3: the cached plan
+            saved_params = [a.detach().clone() for a in pa]
+            saved_state = _deep_clone(oa.state_dict())
+            # nothing enqueued: an ordinary failure, undone
+            _lib.inject_launch_failure(0)
+            with pytest.raises(_lib.HipLibraryError, match="injected") as info:
+                oa.step()
+            assert not isinstance(info.value, _lib.HipLaunchIncomplete)
+            # one launch enqueued, then the failure
+            _lib.inject_launch_failure(1)
+            with pytest.raises(_lib.HipLaunchIncomplete, match="injected"):
+                oa.step()
+            with pytest.raises(RuntimeError, match="partly updated"):
+                oa.step()
+            torch.cuda.synchronize()
+            with torch.no_grad():
+                for a, saved in zip(pa, saved_params):
+                    a.copy_(saved)
+            oa.load_state_dict(saved_state)
+        oa.step()
+        ob.step()
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(pa, pb)):
+            same_state(oa, a, ob, b, (k, i))
+    _lib.inject_launch_failure(-1)
+
+
 def test_failed_launch_is_undone(monkeypatch):
     """A launch that fails leaves step counts, moment state and stream positions as they were,
     through the full path and through the cached plan."""

@@ -120,3 +120,43 @@ def test_noalloc_step_replays_from_a_hip_graph():
         other.mul_(1.0001)
         torch.cuda.synchronize()
     print("  3 replays bit-identical to the eager calls", flush=True)
+
+
+def test_noalloc_step_allocates_no_device_memory():
+    """The entry point's contract itself: after the first call on the device, calls with a launch
+    table near the 1 MiB limit (3,000 tensors) leave the device's free memory unchanged, and one is
+    captured in a graph under torch's global capture mode, which refuses calls that are unsafe
+    during capture, then replayed."""
+    print("noalloc step: no device allocation", flush=True)
+    gen = torch.Generator().manual_seed(41)
+    count = 3000
+    params = [torch.nn.Parameter((torch.randn(4096, generator=gen) * 0.02).to(H.DEVICE)) for _ in range(count)]
+    opt = aw.ZIPSRAdamW4Bit(params, quant_rng_seed=3, optimized=True)
+    for p in params:
+        p.grad = (torch.randn(4096, generator=gen) * 1e-3).to(H.DEVICE)
+    captured = []
+    regular = _lib.fused_step
+    _lib.fused_step = lambda t, st: (captured.append(t.copy()), regular(t, st))
+    try:
+        opt.step()
+    finally:
+        _lib.fused_step = regular
+    (table,) = captured
+    assert len(table) == count
+    nbytes = 64 + count * _lib.TENSOR.itemsize + (count + 1) * 8
+    assert 0.8 * _lib.NOALLOC_TABLE_BYTES < nbytes < _lib.NOALLOC_TABLE_BYTES
+    stream = torch.cuda.current_stream()
+    _lib.fused_step_noalloc(table, stream.cuda_stream)  # warm-up: the device's first call
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info()
+    for _ in range(5):
+        _lib.fused_step_noalloc(table, stream.cuda_stream)
+    torch.cuda.synchronize()
+    free1, _ = torch.cuda.mem_get_info()
+    assert free1 == free0, (free0, free1)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, capture_error_mode="global"):
+        _lib.fused_step_noalloc(table, torch.cuda.current_stream().cuda_stream)
+    graph.replay()
+    torch.cuda.synchronize()
+    print(f"  free device memory {free0} -> {free1} over 5 calls; graph captured and replayed", flush=True)
