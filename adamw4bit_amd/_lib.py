@@ -30,6 +30,7 @@ MOMENT_ZERO_FLOOR, MOMENT_EDEN, MOMENT_GUARDS, MOMENT_EXT_DRAWS = 0x1, 0x2, 0x4,
 MOMENT_SAMPLED_READ, MOMENT_READ_RAW_SCALE, MOMENT_FRESH_PROXY, MOMENT_PENDING = 0x10, 0x20, 0x40, 0x80
 F32, BF16, F16 = 0, 1, 2
 TENSOR_LERP1_LARGE, TENSOR_LERP2_LARGE, TENSOR_VEC_ALIGNED, TENSOR_GRAD_SCALE = 0x1, 0x2, 0x4, 0x8
+TENSOR_GRAD_UNSCALE = 0x10
 
 NUM_LUTS, LUT_HALF, LUT_EXP0 = 11, 89, 936
 NOALLOC_TABLE_BYTES = 1 << 20
@@ -64,6 +65,8 @@ SIGNATURES = {
     "aw4_encode_tables": (ctypes.c_int64, [ctypes.c_void_p, ctypes.c_int64]),
     "aw4_clip_coefficient": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_float, ctypes.c_void_p,
                                             ctypes.c_void_p, ctypes.c_void_p]),
+    "aw4_unscale_clip_coefficient": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p, ctypes.c_float,
+                                                    ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
     "aw4_inject_launch_failure": (None, [ctypes.c_int32]),
 }
 
@@ -138,6 +141,16 @@ def clip_coefficient(table: np.ndarray, max_norm: float, norm_ptr: int, coef_ptr
     assert table.dtype == TENSOR and table.flags.c_contiguous
     check(library().aw4_clip_coefficient(table.ctypes.data, len(table), max_norm, norm_ptr, coef_ptr, stream),
           "aw4_clip_coefficient")
+
+
+def unscale_clip_coefficient(table: np.ndarray, inv_scale_ptr: int, max_norm: float, norm_ptr: int, coef_ptr: int,
+                             found_inf_ptr: int, stream: int) -> None:
+    """``clip_coefficient`` over gradients scaled by a loss scale: each value is unscaled by the
+    device float at ``inv_scale_ptr`` as it is read, and ``found_inf_ptr`` receives 1.0 if any
+    scaled value is not finite."""
+    assert table.dtype == TENSOR and table.flags.c_contiguous
+    check(library().aw4_unscale_clip_coefficient(table.ctypes.data, len(table), inv_scale_ptr, max_norm, norm_ptr,
+                                                 coef_ptr, found_inf_ptr, stream), "aw4_unscale_clip_coefficient")
 
 
 def inject_launch_failure(after: int) -> None:

@@ -79,24 +79,47 @@ def _fused_step_fake(params, states, inputs, table, refs) -> None:
     return None
 
 
-@torch.library.custom_op("adamw4bit_hip::clip_coefficient_", mutates_args=("out",))
-def clip_coefficient_(grads: List[torch.Tensor], out: torch.Tensor, table: torch.Tensor, max_norm: float) -> None:
-    """Total gradient 2-norm and clipping coefficient of ``grads`` (row i of ``table`` describes
-    ``grads[i]``; its address is taken from the tensor), written to ``out[0]`` and ``out[1]``
-    (fp32, on the gradients' device)."""
+def _norm_rows(grads: List[torch.Tensor], out: torch.Tensor, table: torch.Tensor) -> np.ndarray:
     if table.dtype != torch.uint8 or table.device.type != "cpu" or table.numel() % _lib.TENSOR.itemsize:
         raise ValueError("table must be a CPU uint8 tensor of aw4_tensor rows")
-    if out.dtype != torch.float32 or out.numel() < 2 or out.device.type != "cuda" or not out.is_contiguous():
-        raise ValueError("out must be 2 contiguous float32 values on a HIP device")
+    if out.dtype != torch.float32 or out.numel() < 4 or out.device.type != "cuda" or not out.is_contiguous():
+        raise ValueError("out must be 4 contiguous float32 values on a HIP device")
     rows = table.contiguous().numpy().view(_lib.TENSOR).copy()
     if len(rows) != len(grads) or not all(g.is_contiguous() for g in grads):
         raise ValueError("one contiguous gradient per table row")
     rows["grad"] = [g.data_ptr() for g in grads]
+    return rows
+
+
+@torch.library.custom_op("adamw4bit_hip::clip_coefficient_", mutates_args=("out",))
+def clip_coefficient_(grads: List[torch.Tensor], out: torch.Tensor, table: torch.Tensor, max_norm: float) -> None:
+    """Total gradient 2-norm and clipping coefficient of ``grads`` (row i of ``table`` describes
+    ``grads[i]``; its address is taken from the tensor), written to ``out[0]`` and ``out[3]``
+    (fp32, on the gradients' device; ``out[2:4]`` is the pair the step reads)."""
+    rows = _norm_rows(grads, out, table)
     with torch.cuda.device(out.device):
-        _lib.clip_coefficient(rows, max_norm, out.data_ptr(), out.data_ptr() + 4,
-                              torch.cuda.current_stream(out.device).cuda_stream)
+        p = out.data_ptr()
+        _lib.clip_coefficient(rows, max_norm, p, p + 12, torch.cuda.current_stream(out.device).cuda_stream)
 
 
 @clip_coefficient_.register_fake
 def _clip_coefficient_fake(grads, out, table, max_norm) -> None:
+    return None
+
+
+@torch.library.custom_op("adamw4bit_hip::unscale_clip_coefficient_", mutates_args=("out",))
+def unscale_clip_coefficient_(grads: List[torch.Tensor], out: torch.Tensor, table: torch.Tensor,
+                              max_norm: float) -> None:
+    """``clip_coefficient_`` of the gradients unscaled by the inverse loss scale in ``out[2]``:
+    total norm to ``out[0]``, found_inf (1.0 if any scaled value is not finite) to ``out[1]`` and
+    the coefficient to ``out[3]``."""
+    rows = _norm_rows(grads, out, table)
+    with torch.cuda.device(out.device):
+        p = out.data_ptr()
+        _lib.unscale_clip_coefficient(rows, p + 8, max_norm, p, p + 12, p + 4,
+                                      torch.cuda.current_stream(out.device).cuda_stream)
+
+
+@unscale_clip_coefficient_.register_fake
+def _unscale_clip_coefficient_fake(grads, out, table, max_norm) -> None:
     return None

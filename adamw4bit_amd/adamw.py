@@ -64,6 +64,18 @@ from .quantization import (
 )
 
 _TORCHAO_MIN_QUANT_NUMEL = 4096           # adamw.py:19
+# Classes whose instances hold a quantized moment's block scales: this package's QuantState, and
+# those of optimizers driven through HipOptimizedBackend (the reference's own, same fields).
+_QUANT_STATE_TYPES: Tuple[type, ...] = (QuantState,)
+
+
+def register_quant_state_type(cls: type) -> None:
+    """Accept instances of `cls` (fields absmax, shape, dtype, blocksize, packed) as moment state."""
+    global _QUANT_STATE_TYPES
+    if cls not in _QUANT_STATE_TYPES:
+        _QUANT_STATE_TYPES = _QUANT_STATE_TYPES + (cls,)
+
+
 _CHUNK_NUMEL = 1 << 19                    # _optimized.py:33
 _CHUNK_KEY = "max_chunk_numel"            # _optimized.py:34
 _FALLBACK_KEY = "_optimized_full_fallback"  # _optimized.py:35
@@ -306,7 +318,7 @@ def _moment_tensors(state: Dict[str, Any]) -> List[torch.Tensor]:
             if isinstance(value, torch.Tensor) and value.layout == torch.strided and value.numel():
                 out.append(value)
         meta = state.get(f"{key}_quant_state")
-        if (isinstance(meta, QuantState) and isinstance(meta.absmax, torch.Tensor)
+        if (isinstance(meta, _QUANT_STATE_TYPES) and isinstance(meta.absmax, torch.Tensor)
                 and meta.absmax.layout == torch.strided and meta.absmax.numel()):
             out.append(meta.absmax)
     return out
@@ -336,6 +348,7 @@ class QuantizedAdamW(Optimizer):
     _VPROXY_LOOKAHEAD_UPDATE_SR_SCHEMES = {"dyn4_vproxy_la_upd_sr"}
     _QUANT_RNG_STATE_KEY = "_quant_rng_state"
     _QUANT_RNG_OFFSETS = {"m1": 0x1A2B3C4D, "m2": 0x5E6F7789}  # adamw.py:122-125
+    _quant_state_type: type = QuantState  # the class new quantized moment state is created as
 
     def __init__(self,
                  params: Iterator[torch.nn.Parameter],
@@ -445,8 +458,9 @@ class QuantizedAdamW(Optimizer):
         self._pending_finish = None  # commit / undo of the step being launched
         self._inconsistent: Optional[str] = None  # why step() refuses to run (a partly enqueued step)
         # Gradient clipping computed by clip_grad_norm_ and applied by the next step:
-        # (device, fp32 coefficient on that device) or None.
-        self._grad_clip: Optional[Tuple[torch.device, torch.Tensor]] = None
+        # (device, the float pair {inverse loss scale, clip coefficient} on that device, the row
+        # flags that apply them) or None.
+        self._grad_clip: Optional[Tuple[torch.device, torch.Tensor, int]] = None
         if optimized:
             for group in self.param_groups:
                 group.setdefault(_CHUNK_KEY, _CHUNK_NUMEL)
@@ -540,7 +554,7 @@ class QuantizedAdamW(Optimizer):
     def state_dict(self):
         result = super().state_dict()
         result["state"] = {
-            index: {key: vars(value).copy() if isinstance(value, QuantState) else value
+            index: {key: vars(value).copy() if isinstance(value, _QUANT_STATE_TYPES) else value
                     for key, value in parameter_state.items()}
             for index, parameter_state in result["state"].items()
         }
@@ -655,7 +669,7 @@ class QuantizedAdamW(Optimizer):
     # ------------------------------------------------------------------
     @torch.no_grad()
     def clip_grad_norm_(self, max_norm: float, norm_type: float = 2.0, error_if_nonfinite: bool = False,
-                        foreach: Optional[bool] = None) -> torch.Tensor:
+                        foreach: Optional[bool] = None, *, grad_scaler=None) -> torch.Tensor:
         """``torch.nn.utils.clip_grad_norm_`` over this optimizer's parameters, fused into the next
         ``step()``.
 
@@ -669,26 +683,90 @@ class QuantizedAdamW(Optimizer):
         parameters' device, in the promoted gradient dtype), like torch.  Only the 2-norm of
         parameters on one HIP device; one pending clip per step (``zero_grad()`` drops a pending
         clip whose step was skipped).
+
+        With ``grad_scaler`` (an enabled ``torch.amp.GradScaler`` whose scaled loss produced the
+        gradients), this is ``grad_scaler.unscale_(self)`` followed by the clip, in the same single
+        read of the gradients (``aw4_unscale_clip_coefficient``): each value is unscaled as torch's
+        ``_amp_foreach_non_finite_check_and_unscale_`` would leave it, the norm is that of the
+        unscaled gradients, and the scaler records this optimizer's ``found_inf`` (any scaled value
+        not finite) and its stage as unscaled, so ``grad_scaler.step(self)`` skips an overflowed
+        step as usual.  The gradients in memory stay scaled; the next ``step()`` reads them
+        unscaled and clipped.
         """
         if float(norm_type) != 2.0:
             raise NotImplementedError("the fused clip computes the 2-norm only")
+        return self._fused_prologue(float(max_norm), grad_scaler, error_if_nonfinite, clip=True)
+
+    @torch.no_grad()
+    def unscale_grads_(self, grad_scaler) -> None:
+        """``grad_scaler.unscale_(self)`` fused into the next ``step()``: one read of the gradients
+        checks them for non-finite values (the scaler's ``found_inf`` for this optimizer, as
+        ``_amp_foreach_non_finite_check_and_unscale_`` computes it, and its stage set to unscaled),
+        and ``step()`` reads every gradient value as ``grad_dtype(g * inv_scale)`` instead of torch
+        writing the unscaled gradients back.  Call it where ``grad_scaler.unscale_(optimizer)``
+        would be called (or let ``grad_scaler.step`` call torch's own)."""
+        self._fused_prologue(math.inf, grad_scaler, False, clip=False)
+
+    def _scaler_begin(self, grad_scaler):
+        """The scaler's per-optimizer state for a fused unscale (GradScaler.unscale_'s checks), or
+        None without an enabled scaler."""
+        if grad_scaler is None or not grad_scaler.is_enabled():
+            return None
+        from torch.amp.grad_scaler import OptState
+
+        grad_scaler._check_scale_growth_tracker("unscale_")
+        state = grad_scaler._per_optimizer_states[id(self)]
+        if state["stage"] is OptState.UNSCALED:
+            raise RuntimeError("unscale_() has already been called on this optimizer since the last update().")
+        if state["stage"] is OptState.STEPPED:
+            raise RuntimeError("unscale_() is being called after step().")
+        return state
+
+    def _fused_prologue(self, max_norm: float, grad_scaler, error_if_nonfinite: bool, clip: bool):
+        scaler_state = self._scaler_begin(grad_scaler)
         prepared = self._prepare_clip()
         if prepared is None:
+            if scaler_state is not None:
+                from torch.amp.grad_scaler import OptState
+
+                scaler_state["found_inf_per_device"] = {}
+                scaler_state["stage"] = OptState.UNSCALED
             return torch.tensor(0.0)
         grads, table, out, result_dtype = prepared
-        if torch.compiler.is_compiling():
-            _ops.clip_coefficient_(grads, out, table, float(max_norm))
+        flags = _lib.TENSOR_GRAD_SCALE if clip else 0
+        if scaler_state is not None and any(g.dtype == torch.float16 for g in grads):
+            self._grad_clip = None
+            raise ValueError("Attempting to unscale FP16 gradients.")  # GradScaler.unscale_ (allow_fp16=False)
+        if scaler_state is not None:
+            # torch carries out the reciprocal of the scale in float64 (GradScaler.unscale_)
+            out[2:3].copy_(grad_scaler._scale.double().reciprocal().float().reshape(1).to(out.device))
+            flags |= _lib.TENSOR_GRAD_UNSCALE
+            if torch.compiler.is_compiling():
+                _ops.unscale_clip_coefficient_(grads, out, table, max_norm)
+            else:
+                with torch.cuda.device(out.device):
+                    p = out.data_ptr()
+                    _lib.unscale_clip_coefficient(table.numpy().view(_lib.TENSOR), p + 8, max_norm, p, p + 12, p + 4,
+                                                  torch.cuda.current_stream(out.device).cuda_stream)
+        elif torch.compiler.is_compiling():
+            _ops.clip_coefficient_(grads, out, table, max_norm)
         else:  # the operator's dispatch over every gradient costs more than the call (see _launch)
             with torch.cuda.device(out.device):
-                _lib.clip_coefficient(table.numpy().view(_lib.TENSOR), float(max_norm), out.data_ptr(),
-                                      out.data_ptr() + 4, torch.cuda.current_stream(out.device).cuda_stream)
+                p = out.data_ptr()
+                _lib.clip_coefficient(table.numpy().view(_lib.TENSOR), max_norm, p, p + 12,
+                                      torch.cuda.current_stream(out.device).cuda_stream)
         total = out[0].to(result_dtype)
         if error_if_nonfinite and bool(torch.logical_or(total.isnan(), total.isinf())):
             raise RuntimeError(
-                f"The total norm of order {float(norm_type)} for gradients from `parameters` is non-finite, so it "
+                f"The total norm of order 2.0 for gradients from `parameters` is non-finite, so it "
                 "cannot be clipped. To disable this error and scale the gradients by the non-finite norm anyway, "
                 "set `error_if_nonfinite=False`")
-        self._set_grad_clip(out)
+        if scaler_state is not None:
+            from torch.amp.grad_scaler import OptState
+
+            scaler_state["found_inf_per_device"] = {out.device: out[1]}
+            scaler_state["stage"] = OptState.UNSCALED
+        self._set_grad_clip(out, flags)
         return total
 
     @torch.compiler.disable
@@ -715,7 +793,8 @@ class QuantizedAdamW(Optimizer):
         table["numel"] = [g.numel() for g in grads]
         table["grad_dtype"] = [_DTYPES[g.dtype] for g in grads]
         table["flags"] = [_lib.TENSOR_VEC_ALIGNED if g.data_ptr() % (4 * g.element_size()) == 0 else 0 for g in grads]
-        out = torch.empty(2, dtype=torch.float32, device=device)  # [total norm, coefficient]
+        # [total norm, found_inf, then the pair the step reads: inverse loss scale, clip coefficient]
+        out = torch.empty(4, dtype=torch.float32, device=device)
         result_dtype = grads[0].dtype
         for g in grads[1:]:
             if g.dtype != result_dtype:
@@ -723,8 +802,8 @@ class QuantizedAdamW(Optimizer):
         return grads, torch.from_numpy(table.view(np.uint8)), out, result_dtype
 
     @torch.compiler.disable
-    def _set_grad_clip(self, out: torch.Tensor) -> None:
-        self._grad_clip = (out.device, out[1:])
+    def _set_grad_clip(self, out: torch.Tensor, flags: int) -> None:
+        self._grad_clip = (out.device, out[2:4], flags)
 
     def zero_grad(self, set_to_none: bool = True) -> None:
         """``Optimizer.zero_grad``; also drops a pending gradient clip, whose gradients are gone
@@ -732,11 +811,12 @@ class QuantizedAdamW(Optimizer):
         self._grad_clip = None
         super().zero_grad(set_to_none=set_to_none)
 
-    def _take_grad_clip(self, device: torch.device) -> Optional[torch.Tensor]:
+    def _take_grad_clip(self, device: torch.device) -> Optional[Tuple[torch.Tensor, int]]:
+        """The pending (unscale, clip) pair on `device` and its row flags, or None."""
         clip = self._grad_clip
         if clip is None or clip[0] != device:
             return None
-        return clip[1]
+        return clip[1], clip[2]
 
     # ------------------------------------------------------------------
     # The step
@@ -838,7 +918,7 @@ class QuantizedAdamW(Optimizer):
                     and value.shape == p.shape and value.device == p.device and value.dtype == torch.float32)
         codes = state.get(f"{key}_code")
         meta = state.get(f"{key}_quant_state")
-        if not isinstance(codes, torch.Tensor) or not isinstance(meta, QuantState):
+        if not isinstance(codes, torch.Tensor) or not isinstance(meta, _QUANT_STATE_TYPES):
             return False
         n = p.numel()
         absmax = meta.absmax
@@ -938,7 +1018,7 @@ class QuantizedAdamW(Optimizer):
                     occupied.append(_byte_range(value))
             for key in ("m1_quant_state", "m2_quant_state"):
                 meta = state.get(key)
-                if isinstance(meta, QuantState) and isinstance(meta.absmax, torch.Tensor):
+                if isinstance(meta, _QUANT_STATE_TYPES) and isinstance(meta.absmax, torch.Tensor):
                     if taken(_byte_range(meta.absmax)):
                         meta.absmax = meta.absmax.clone()
                     occupied.append(_byte_range(meta.absmax))
@@ -1014,7 +1094,7 @@ class QuantizedAdamW(Optimizer):
         code, scale = initial_code_and_scale(scheme, eden)
         state[f"{moment}_code"] = torch.full(((n + 1) // 2,), code | (code << 4), dtype=torch.uint8, device=p.device)
         absmax = torch.full((n // size,), scale, dtype=torch.float32, device=p.device)
-        state[f"{moment}_quant_state"] = QuantState(absmax=absmax, shape=p.shape, dtype=torch.float32,
+        state[f"{moment}_quant_state"] = self._quant_state_type(absmax=absmax, shape=p.shape, dtype=torch.float32,
                                                     blocksize=size, packed=True)
         state.pop(moment, None)
         if SCHEMES[scheme][1] in (ROUND_STATE_SR, ROUND_UPDATE_SR):
@@ -1037,7 +1117,7 @@ class QuantizedAdamW(Optimizer):
             return
         codes = state.get(f"{moment}_code")
         meta = state.get(f"{moment}_quant_state")
-        if not isinstance(codes, torch.Tensor) or not isinstance(meta, QuantState):
+        if not isinstance(codes, torch.Tensor) or not isinstance(meta, _QUANT_STATE_TYPES):
             raise NotImplementedError(f"{moment}: fp32 state found where the scheme is quantized")
         if not isinstance(meta.absmax, torch.Tensor):
             raise ValueError(f"{moment}: quantization scales must be a tensor")
@@ -1143,15 +1223,17 @@ class _DeviceBatch:
         target.append(tensor)
         return kind, len(target) - 1
 
-    def launch(self, coef: Optional[torch.Tensor]) -> Tuple:
+    def launch(self, clip: Optional[Tuple[torch.Tensor, int]]) -> Tuple:
         """The launch record: (params, written, read, table, refs, copy_back), the table a CPU uint8
-        tensor of rows with every address filled in, refs its (rows, fields) int64 references."""
+        tensor of rows with every address filled in, refs its (rows, fields) int64 references.
+        `clip`: the pending (unscale, clip) pair and its row flags."""
         table = np.array(self.rows, dtype=_lib.TENSOR)
-        if coef is not None:
-            k = self.ref("r", coef)
+        if clip is not None:
+            pair, flags = clip
+            k = self.ref("r", pair)
             for r in self.refs:
                 r[_COL["grad_scale"]] = k
-            table["flags"] |= _lib.TENSOR_GRAD_SCALE
+            table["flags"] |= flags
         base = {"p": 0, "w": len(self.params), "r": len(self.params) + len(self.written)}
         refs = np.full((len(self.rows), len(_ops.ADDRESS_FIELDS)), -1, dtype=np.int64)
         for i, row in enumerate(self.refs):
@@ -1166,7 +1248,8 @@ class _StepUndo:
     (and the scales and packing flag of their QuantStates), and every random stream's position."""
 
     def __init__(self, opt: "QuantizedAdamW", states: List[Dict[str, Any]]):
-        self.states = [(st, dict(st), [(q, q.absmax, q.packed) for q in st.values() if isinstance(q, QuantState)])
+        self.states = [(st, dict(st), [(q, q.absmax, q.packed) for q in st.values()
+                                       if isinstance(q, _QUANT_STATE_TYPES)])
                        for st in states]
         self.streams = [(s, s.offset) for s in opt._all_streams()]
 
@@ -1310,7 +1393,7 @@ class _LaunchPlan:
                     plan.state_refs[1].append(k)
                     plan.state_refs[2].append(state.get(k))
                 for q in (state.get("m1_quant_state"), state.get("m2_quant_state")):
-                    if isinstance(q, QuantState):
+                    if isinstance(q, _QUANT_STATE_TYPES):
                         plan.quant_refs[0].append(q)
                         plan.quant_refs[1].append(q.absmax)
             table = np.array(batch.rows, dtype=_lib.TENSOR)
@@ -1436,8 +1519,8 @@ class _LaunchPlan:
             else:
                 index = np.array(ks, dtype=np.intp)
                 dev.words[:] = np.stack([c.words() for c in consts])[index]
-            coef = opt._take_grad_clip(dev.device)
-            extra = 0 if coef is None else _lib.TENSOR_GRAD_SCALE
+            clip = opt._take_grad_clip(dev.device)
+            coef, extra = clip if clip is not None else (None, 0)
             if dev.small:
                 flags = dev.words[:, 0]
                 for i, (g, pvec, gvec) in enumerate(zip(g0, dev.pvec_list, dev.gvec_list)):

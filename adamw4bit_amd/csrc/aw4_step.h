@@ -103,18 +103,29 @@ __device__ __forceinline__ float round_to_storage(float v) {
     else return v;
 }
 
-// Gradient clipping (AW4_TENSOR_GRAD_SCALE): g -> grad_dtype(fp32(g * c)), the value the
-// in-place _foreach_mul_ of torch.nn.utils.clip_grad_norm_ leaves in a gradient of that dtype
-// (the fp32 product of two 16-bit values is exact, so one rounding to the dtype).  G is the
-// gradient's storage dtype, D_ANY for a run-time one.  The branch is uniform per tensor.
+__device__ __forceinline__ float round_to_dtype(float v, int dt) {
+    return dt == D_BF16 ? round_to_storage<D_BF16>(v) : dt == D_F16 ? round_to_storage<D_F16>(v) : v;
+}
+
+// Loss-scale unscaling and gradient clipping applied as the step reads the gradients
+// (grad_scale -> {u, c}): with AW4_TENSOR_GRAD_UNSCALE g -> grad_dtype(fp32(g * u)), the value
+// GradScaler.unscale_'s _amp_foreach_non_finite_check_and_unscale_ leaves in a gradient of
+// that dtype (u = its fp32 inverse scale); then with AW4_TENSOR_GRAD_SCALE g ->
+// grad_dtype(fp32(g * c)), what the in-place _foreach_mul_ of torch.nn.utils.clip_grad_norm_
+// leaves (the fp32 product of two 16-bit values is exact, so one rounding to the dtype each).
+// G is the gradient's storage dtype, D_ANY for a run-time one.  The branch is uniform per tensor.
 template <int G>
 __device__ __forceinline__ void clip_grads(const aw4_tensor& T, float* g, int n) {
-    if (__builtin_expect((T.flags & AW4_TENSOR_GRAD_SCALE) == 0, 1)) return;
-    const float c = *gaddr<const float>(T.grad_scale);
+    if (__builtin_expect((T.flags & (AW4_TENSOR_GRAD_SCALE | AW4_TENSOR_GRAD_UNSCALE)) == 0, 1)) return;
+    const gptr<const float> f = gaddr<const float>(T.grad_scale);
+    const float u = f[0], c = f[1];
+    const bool unscale = (T.flags & AW4_TENSOR_GRAD_UNSCALE) != 0, clip = (T.flags & AW4_TENSOR_GRAD_SCALE) != 0;
     const int dt = G == D_ANY ? T.grad_dtype : G;
     for (int t = 0; t < n; ++t) {
-        const float v = g[t] * c;
-        g[t] = dt == D_BF16 ? round_to_storage<D_BF16>(v) : dt == D_F16 ? round_to_storage<D_F16>(v) : v;
+        float v = g[t];
+        if (unscale) v = round_to_dtype(v * u, dt);
+        if (clip) v = round_to_dtype(v * c, dt);
+        g[t] = v;
     }
 }
 

@@ -1060,13 +1060,21 @@ int aw4_dequantize(const aw4_moment* m, int64_t numel, float* out, void* stream)
     return AW4_OK;
 }
 
-int aw4_clip_coefficient(const aw4_tensor* tensors, int32_t count, float max_norm, float* norm_out,
-                         float* coef_out, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// The norm pass and coefficient of aw4_clip_coefficient (inv_scale null) and
+// aw4_unscale_clip_coefficient.
+int norm_prologue(const char* what, const aw4_tensor* tensors, int32_t count, const float* inv_scale,
+                  float max_norm, float* norm_out, float* coef_out, float* found_out, void* stream) {
     g_error.clear();
-    if (count <= 0 || !tensors || !norm_out || !coef_out)
-        return set_error(AW4_EINVAL, "aw4_clip_coefficient: bad arguments");
-    if (!aligned((uint64_t)norm_out, 4) || !aligned((uint64_t)coef_out, 4))
-        return set_error(AW4_EALIGN, "aw4_clip_coefficient: outputs not 4-byte aligned");
+    const bool unscale = inv_scale != nullptr;
+    if (count <= 0 || !tensors || !norm_out || !coef_out || (unscale && !found_out))
+        return set_error(AW4_EINVAL, "%s: bad arguments", what);
+    if (!aligned((uint64_t)norm_out, 4) || !aligned((uint64_t)coef_out, 4) ||
+        (unscale && (!aligned((uint64_t)inv_scale, 4) || !aligned((uint64_t)found_out, 4))))
+        return set_error(AW4_EALIGN, "%s: device floats not 4-byte aligned", what);
     int result_dtype = tensors[0].grad_dtype;
     int64_t segments = 0;
     for (int i = 0; i < count; ++i) {
@@ -1080,12 +1088,13 @@ int aw4_clip_coefficient(const aw4_tensor* tensors, int32_t count, float max_nor
         if (t.grad_dtype != result_dtype) result_dtype = AW4_F32;  // torch.stack promotes mixed dtypes
         segments += (t.numel + kNormSegment - 1) / kNormSegment;
     }
-    if (segments > 0x7fffffff) return set_error(AW4_EINVAL, "aw4_clip_coefficient: too many segments");
-    // staging: header, rows, segment starts (copied), then the partial sums and the per-gradient
-    // squared norms (device only)
+    if (segments > 0x7fffffff) return set_error(AW4_EINVAL, "%s: too many segments", what);
+    // staging: header, rows, segment starts (copied), then the partial sums, the per-gradient
+    // squared norms and (unscaling) the per-segment non-finite flags (device only)
     const size_t table = (sizeof(NormHeader) + sizeof(aw4_tensor) * count + sizeof(int64_t) * (count + 1) + 255) &
                          ~(size_t)255;
-    const size_t bytes = table + sizeof(double) * ((size_t)segments + (size_t)count);
+    const size_t bytes = table + sizeof(double) * ((size_t)segments + (size_t)count) +
+                         (unscale ? sizeof(uint32_t) * (size_t)segments : 0);
 
     std::lock_guard<std::mutex> lock(g_mutex);
     DeviceState* ds = nullptr;
@@ -1108,11 +1117,17 @@ int aw4_clip_coefficient(const aw4_tensor* tensors, int32_t count, float max_nor
     h->count = count;
     h->result_dtype = result_dtype;
     h->max_norm = max_norm;
+    h->unscale = unscale ? 1 : 0;
     h->total_segments = segments;
     h->partials = (uint64_t)slot->dev + table;
     h->norm_sq = h->partials + sizeof(double) * (uint64_t)segments;
     h->norm_out = (uint64_t)norm_out;
     h->coef_out = (uint64_t)coef_out;
+    if (unscale) {
+        h->inv_scale = (uint64_t)inv_scale;
+        h->nonfinite = h->norm_sq + sizeof(double) * (uint64_t)count;
+        h->found_out = (uint64_t)found_out;
+    }
     hipStream_t s = (hipStream_t)stream;
     rc = upload_slot(*slot, table, s);
     if (rc) return rc;
@@ -1126,6 +1141,23 @@ int aw4_clip_coefficient(const aw4_tensor* tensors, int32_t count, float max_nor
     AW4_HIP_CHECK(hipEventRecord(slot->done, s));
     slot->pending = true;
     return AW4_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int aw4_clip_coefficient(const aw4_tensor* tensors, int32_t count, float max_norm, float* norm_out,
+                         float* coef_out, void* stream) {
+    return norm_prologue("aw4_clip_coefficient", tensors, count, nullptr, max_norm, norm_out, coef_out, nullptr,
+                         stream);
+}
+
+int aw4_unscale_clip_coefficient(const aw4_tensor* tensors, int32_t count, const float* inv_scale, float max_norm,
+                                 float* norm_out, float* coef_out, float* found_inf_out, void* stream) {
+    if (!inv_scale) return set_error(AW4_EINVAL, "aw4_unscale_clip_coefficient: null inv_scale");
+    return norm_prologue("aw4_unscale_clip_coefficient", tensors, count, inv_scale, max_norm, norm_out, coef_out,
+                         found_inf_out, stream);
 }
 
 int aw4_uniforms(uint64_t seed, uint64_t offset, int64_t n, float* out, void* stream) {

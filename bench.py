@@ -158,6 +158,12 @@ def cpu_leg(seconds_target: float) -> dict:
     return out
 
 
+def _protocol_minutes(legs) -> float:
+    """Minutes that 110 steps (10 warmup + 100 timed) of each 4096x4096 recipe would take in every
+    leg, at the measured step times."""
+    return sum(110 * sum(leg["ms_per_step"].values()) for leg in legs) / 6e4
+
+
 def cpu_baseline(seconds_target: float = 20.0):
     """The CPU baseline: the same sample timed in two fresh child processes, on all host threads
     and at OMP_NUM_THREADS=2 (the reference's CI setting, .github/workflows/ci.yml:17).  `value`
@@ -197,8 +203,12 @@ def cpu_baseline(seconds_target: float = 20.0):
                        for leg in legs)
     return {"value": rate(main_leg), "unit": "Gelem/s", "cores": main_leg["threads"], "kind": "port",
             "sample": f"oracle eager chunk update (the reference's CPU path), one fp32 4096x4096 tensor "
-                      f"(16.8M values) per recipe, ZE-EDEN + ZIP-SR, median step times, in child processes "
-                      f"off the GPU; {detail}; {cpu}, ATen {torch.backends.cpu.get_cpu_capability()}, "
+                      f"(16.8M values) per recipe, ZE-EDEN + ZIP-SR, in child processes off the GPU: the median "
+                      f"of the steps that fit in about {seconds_target / 2 / len(CPU_RECIPES):.0f} s after one "
+                      f"untimed step (not the median of 100 steps after 10 warmup steps, which would take "
+                      f"about {_protocol_minutes(legs):.0f} min on these threads); the 1024x1024 ZE-EDEN leg "
+                      f"(legs[].zeeden_1024x1024_ms_per_step) is the median of 100 steps after 10 warmup "
+                      f"steps; {detail}; {cpu}, ATen {torch.backends.cpu.get_cpu_capability()}, "
                       f"os.cpu_count {os.cpu_count()}",
             "legs": [{"threads": leg["threads"], "omp_num_threads": leg["omp_num_threads"],
                       "ms_per_step": {k: round(v, 2) for k, v in leg["ms_per_step"].items()},
@@ -318,6 +328,40 @@ def time_launches(recipes, steps: int, warmup: int, clip, stream):
     return {name: [a.elapsed_time(b) for a, b in ev] for name, ev in events.items()}, wall, norm_events
 
 
+def time_grad_scaler(recipes, steps: int, warmup: int, clip, stream, fused: bool) -> dict:
+    """A trainer with loss scaling (torch.amp.GradScaler, scale 1.0 so the gradients keep their
+    values when torch unscales them in place): per iteration the unscale and clip, then
+    ``scaler.step`` (which reads found_inf on the host) and ``scaler.update``.  fused: the unscale
+    folded into the fused clip's read of the gradients (``clip_grad_norm_(max_norm,
+    grad_scaler=scaler)``); else torch's ``scaler.unscale_`` (a read and a write of every gradient)
+    followed by the fused clip.  Returns the mean ms per iteration per recipe (HIP events around
+    the whole iteration on the launch stream)."""
+    import torch
+
+    out = {}
+    for name, opt, _ in recipes:
+        scaler = torch.amp.GradScaler("cuda", init_scale=1.0, growth_interval=1 << 30)
+        loss = torch.ones((), device=stream.device)
+        ev = []
+        for k in range(warmup + steps):
+            scaler.scale(loss)
+            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            if fused:
+                opt.clip_grad_norm_(clip, grad_scaler=scaler)
+            else:
+                scaler.unscale_(opt)
+                opt.clip_grad_norm_(clip)
+            scaler.step(opt)
+            stop.record(stream)
+            scaler.update()
+            if k >= warmup:
+                ev.append((start, stop))
+        torch.cuda.synchronize()
+        out[name] = statistics.mean(a.elapsed_time(b) for a, b in ev)
+    return out
+
+
 def time_blocks(recipes, steps: int, warmup: int, stream) -> dict:
     """Per recipe: ``warmup`` untimed steps, then ``steps`` steps back to back between one pair of
     HIP events on the launch stream; ms per step."""
@@ -423,6 +467,9 @@ def main():
     ap.add_argument("--clip-grad-norm", type=float, default=None, metavar="MAX_NORM",
                     help="clip the gradients to this global 2-norm before every step, fused into the step "
                          "(QuantizedAdamW.clip_grad_norm_), and also time torch.nn.utils.clip_grad_norm_ + step")
+    ap.add_argument("--grad-scaler", action="store_true",
+                    help="with --clip-grad-norm: also time a GradScaler loop, the loss-scale unscaling fused into "
+                         "the clip (clip_grad_norm_(..., grad_scaler=)) against torch's scaler.unscale_ + fused clip")
     ap.add_argument("--copy-probe-gb", type=float, default=0.0,
                     help="also run plain device copies of this many GB (calibrates HBM byte counters)")
     args = ap.parse_args()
@@ -468,6 +515,14 @@ def main():
     if clip is not None:
         norm_ms = statistics.mean(a.elapsed_time(b) for a, b in norm_events)
         unfused = time_unfused(recipes, params, args.steps, args.warmup, clip, stream)
+        scaled = None
+        if args.grad_scaler:
+            scaled = {
+                "fused_unscale_clip_step_ms": {k: round(v, 4) for k, v in time_grad_scaler(
+                    recipes, args.steps, args.warmup, clip, stream, fused=True).items()},
+                "torch_unscale_then_fused_clip_step_ms": {k: round(v, 4) for k, v in time_grad_scaler(
+                    recipes, args.steps, args.warmup, clip, stream, fused=False).items()},
+            }
         prologue = {
             "max_grad_norm": clip,
             "fused_clip_and_step_ms": {k: round(statistics.mean(v), 4) for k, v in launch_ms.items()},
@@ -475,6 +530,7 @@ def main():
             "norm_pass_ms": round(norm_ms, 4),
             "norm_pass_gb": round(grad_bytes / 1e9, 3),
             "norm_pass_gb_s": round(grad_bytes / (norm_ms * 1e-3) / 1e9, 1),
+            **({"grad_scaler": scaled} if scaled else {}),
         }
         print(f"[bench] clip prologue: {prologue}", file=sys.stderr, flush=True)
     per_recipe = {name: statistics.mean(v) for name, v in launch_ms.items()}

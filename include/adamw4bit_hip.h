@@ -99,10 +99,14 @@ extern "C" {
 #define AW4_TENSOR_LERP1_LARGE 0x1 /* lerp weight 1-beta1 >= 0.5: m1 = fma(w-1, g-m1, g) */
 #define AW4_TENSOR_LERP2_LARGE 0x2 /* same for m2 with g*g */
 #define AW4_TENSOR_VEC_ALIGNED 0x4 /* param and grad allow 4-element vector access */
-/* Every gradient value g is read as grad_dtype(fp32(g * c)), c = the fp32 at device address
- * `grad_scale` (the gradient clipping of torch.nn.utils.clip_grad_norm_, whose
- * _foreach_mul_ rounds each product to the gradient's dtype; see aw4_clip_coefficient) */
+/* `grad_scale` is the device address of a float pair {u, c}.  With AW4_TENSOR_GRAD_UNSCALE
+ * every gradient value g is first read as grad_dtype(fp32(g * u)) (the unscaling of
+ * GradScaler.unscale_, u its fp32 inverse loss scale; see aw4_unscale_clip_coefficient); with
+ * AW4_TENSOR_GRAD_SCALE it is then read as grad_dtype(fp32(g * c)) (the gradient clipping of
+ * torch.nn.utils.clip_grad_norm_, whose _foreach_mul_ rounds each product to the gradient's
+ * dtype; see aw4_clip_coefficient).  The gradients in memory are not changed. */
 #define AW4_TENSOR_GRAD_SCALE 0x8
+#define AW4_TENSOR_GRAD_UNSCALE 0x10
 
 /*
  * One moment (m1 or m2) of one parameter.  For a quantized moment, `codes`
@@ -144,7 +148,8 @@ typedef struct aw4_moment {
 typedef struct aw4_tensor {
     uint64_t param;      /* device address, contiguous, param_dtype[numel]; updated in place */
     uint64_t grad;       /* device address, contiguous, grad_dtype[numel] */
-    uint64_t grad_scale; /* device address of one float (AW4_TENSOR_GRAD_SCALE) or 0 */
+    uint64_t grad_scale; /* device address of the float pair {u, c} (AW4_TENSOR_GRAD_UNSCALE /
+                            AW4_TENSOR_GRAD_SCALE) or 0 */
     int64_t numel;
     int32_t param_dtype; /* AW4_F32 / AW4_BF16 / AW4_F16 */
     int32_t grad_dtype;
@@ -238,13 +243,29 @@ int aw4_uniforms(uint64_t seed, uint64_t offset, int64_t n, float* out, void* st
  *            (clip_grad.py: max_norm / (total_norm + 1e-6) is reciprocal then multiply).
  * Sums of squares are taken in float64 in a fixed order (the result does not depend on
  * the launch shape).  Writes the fp32 values of total to norm_out[0] and of coef to
- * coef_out[0] (device addresses) without a host synchronisation.  Pass coef_out as the
- * rows' grad_scale (AW4_TENSOR_GRAD_SCALE) of the next aw4_fused_step: the step then
- * reads the clipped gradients the in-place _foreach_mul_ would have written, and the
- * gradients themselves stay unscaled in memory (no extra pass over them).
+ * coef_out[0] (device addresses) without a host synchronisation.  Put coef in the second
+ * float of the rows' grad_scale pair (AW4_TENSOR_GRAD_SCALE) of the next aw4_fused_step: the
+ * step then reads the clipped gradients the in-place _foreach_mul_ would have written, and
+ * the gradients themselves stay unscaled in memory (no extra pass over them).
  */
 int aw4_clip_coefficient(const aw4_tensor* tensors, int32_t count, float max_norm, float* norm_out,
                          float* coef_out, void* stream);
+
+/*
+ * The same pass over gradients that a GradScaler has scaled: GradScaler.unscale_
+ * (torch/amp/grad_scaler.py, _amp_foreach_non_finite_check_and_unscale_) followed by
+ * aw4_clip_coefficient, fused.  Each value is read once as g' = grad_dtype(fp32(g * u)),
+ * u = the fp32 at device address inv_scale (GradScaler's fp32 1 / scale); the norm and
+ * coefficient are those of aw4_clip_coefficient over the g', and found_inf_out[0] (device)
+ * receives 1.0 if any g is not finite, else 0.0, torch's found_inf.  Nothing is written to
+ * the gradients: put u and coef in the rows' grad_scale pair of the next aw4_fused_step with
+ * AW4_TENSOR_GRAD_UNSCALE (and AW4_TENSOR_GRAD_SCALE to clip).  With max_norm = +inf it is
+ * the unscaling and inf check alone (coef 1 for finite norms).  No counterpart in the
+ * reference, whose examples scale no loss; its trainer's GradScaler path
+ * (examples/train_gpt_small.py:214-215 via the HF Trainer) runs these as torch ops.
+ */
+int aw4_unscale_clip_coefficient(const aw4_tensor* tensors, int32_t count, const float* inv_scale, float max_norm,
+                                 float* norm_out, float* coef_out, float* found_inf_out, void* stream);
 
 /*
  * Host-only: copy the encode lookup tables the kernels use into `out`

@@ -119,15 +119,22 @@ def bits(t: torch.Tensor) -> torch.Tensor:
 
 # Parameter bars.  The kernel's parameter update is faithful (hardware square root and reciprocal)
 # and the reference's CPU square root is faithful too, so an update term may differ from the
-# oracle's by a few of its own ulps, and a parameter by one rounding of the sum:
+# oracle's by a few of its own ulps, and a parameter by one rounding of the sum.  Measured over
+# every comparison of the GPU suite (2,242 tensors) before these bars were set:
 # * 16-bit parameters: every value within one storage ulp per step of the oracle's (the ulp
-#   distance of the bit patterns), and at most F16_NOT_EXACT of them not bit-exact per step;
-# * fp32 parameters: every value within 1e-6 of the parameter scale, |got - expect| <= 1e-6 *
-#   (|expect| + rms(expect)) (a value that drifted close to zero keeps the few-ulp difference of
-#   an update term of the tensor's typical size), and at most FP32_BEYOND_REL of them beyond a
-#   pure 1e-6 relative error |got - expect| <= 1e-6 |expect|.
-F16_NOT_EXACT = 1e-4
-FP32_BEYOND_REL = 1e-3
+#   distance of the bit patterns), or within one storage ulp of the tensor's rms magnitude: where
+#   the update nearly cancels a parameter, or the value is small enough for fine ulps, a few ulps
+#   of the update term are many ulps of the result (measured: at most 5.6e-4 * rms, for fp16,
+#   whose ulp at the rms is 9.8e-4 * rms).  At most F16_NOT_EXACT per step (plus one) of them
+#   not bit-exact (measured at most 9.8e-4 per step; 0 in most tensors);
+# * fp32 parameters: every value within FP32_SCALE_RTOL of the parameter scale, |got - expect| <=
+#   5e-7 * (|expect| + rms(expect)) (measured at most 4.02e-7), and at most FP32_BEYOND_REL (plus
+#   three) of them beyond a pure 1e-6 relative error |got - expect| <= 1e-6 |expect| (values near
+#   zero, where the update term's last bits are a larger share; measured at most 5.5%, median
+#   0.24%, more where the step size is large against the parameters).
+F16_NOT_EXACT = 2e-3
+FP32_SCALE_RTOL = 5e-7
+FP32_BEYOND_REL = 0.05
 # Relative size of one storage ulp of 16-bit values (7 / 10 explicit mantissa bits).
 ULP16 = {torch.bfloat16: 2.0 ** -7, torch.float16: 2.0 ** -10}
 
@@ -138,6 +145,12 @@ def ulp_distance16(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
         v = bits(t).to(torch.int32)  # sign-extended bit patterns
         return torch.where(v < 0, -(v & 0x7FFF), v)
     return (ordered(a) - ordered(b)).abs()
+
+
+# AW4_PARAM_STATS=path appends each comparison's statistics to path (JSON lines); with
+# AW4_PARAM_STATS_COLLECT=1 as well, only the per-value bars are asserted (a run that measures the
+# budgets' statistics over every test).
+_COLLECT = bool(os.environ.get("AW4_PARAM_STATS_COLLECT"))
 
 
 def _record(what: str, stats: dict) -> None:
@@ -162,24 +175,40 @@ def assert_params_close(got: torch.Tensor, expect: torch.Tensor, what: str, rtol
     if got.dtype in (torch.bfloat16, torch.float16):
         d = ulp_distance16(got, expect)[keep]
         stats.update(max_ulps=int(d.max()) if n else 0, not_exact=int((d > 0).sum()))
+        far = d > steps
+        if bool(far.any()):
+            e = expect.double()[keep]
+            err = (got.double()[keep] - e).abs()
+            rms = float(e.pow(2).mean().sqrt())
+            stats.update(far=int(far.sum()), far_err_rms=float(err[far].max()) / rms,
+                         far_abs_rms=float(e[far].abs().max()) / rms,
+                         far_d_le8=int((d[far] <= 8).sum()))
         _record(what, stats)
-        assert int(d.max() if n else 0) <= steps, (f"{what}: {int((d > steps).sum())} of {n} values more than "
-                                                   f"{steps} ulp(s) from the oracle (worst {int(d.max())})")
-        assert stats["not_exact"] <= F16_NOT_EXACT * steps * n, (
+        if _COLLECT:
+            return exact
+        if n:
+            e = expect.double()[keep]
+            err = (got.double()[keep] - e).abs()
+            bad = (d > steps) & (err > ULP16[got.dtype] * float(e.pow(2).mean().sqrt()))
+            assert not bool(bad.any()), (f"{what}: {int(bad.sum())} of {n} values more than {steps} ulp(s) and one "
+                                         f"storage ulp of the rms from the oracle (worst {int(d.max())} ulps)")
+        assert stats["not_exact"] <= F16_NOT_EXACT * steps * n + 1, (
             f"{what}: {stats['not_exact']} of {n} values not bit-exact (budget {F16_NOT_EXACT} per step)")
         return exact
     g = got.double()
     e = expect.double()
     err = (g - e).abs()
     scale = e.abs() + e.pow(2).mean().sqrt()
-    bad = (err > rtol * scale) & keep
+    bad = (err > FP32_SCALE_RTOL * scale) & keep
     beyond = int(((err > rtol * e.abs()) & keep).sum())
     stats.update(beyond_rel=beyond, worst_scale=float((err / (rtol * scale))[keep].max()) if n else 0.0)
     _record(what, stats)
-    assert not bool(bad.any()), (f"{what}: {int(bad.sum())} of {n} values exceed the tolerance; worst error "
-                                 f"{stats['worst_scale']:.3g} x tolerance; bit-exact {exact:.6f}")
-    assert beyond <= FP32_BEYOND_REL * n, (f"{what}: {beyond} of {n} values beyond a 1e-6 relative error "
-                                           f"(budget {FP32_BEYOND_REL}); bit-exact {exact:.6f}")
+    assert not bool(bad.any()), (f"{what}: {int(bad.sum())} of {n} values beyond {FP32_SCALE_RTOL} of the scale; "
+                                 f"worst {stats['worst_scale']:.3g} x 1e-6 of it; bit-exact {exact:.6f}")
+    if _COLLECT:
+        return exact
+    assert beyond <= FP32_BEYOND_REL * n + 3, (f"{what}: {beyond} of {n} values beyond a 1e-6 relative error "
+                                               f"(budget {FP32_BEYOND_REL}); bit-exact {exact:.6f}")
     return exact
 
 

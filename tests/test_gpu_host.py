@@ -482,6 +482,124 @@ def test_grad_scaler_unscales_and_skips_steps():
     assert all(oa.state[a]["step"] == 3 for a in pa)
 
 
+def _scaled_grads(params, gs, scale, k):
+    for p, g in zip(params, gs):
+        p.grad = (g * scale).to(p.dtype).to(H.DEVICE)
+    if k == 2:  # an overflowed iteration
+        params[0].grad.view(-1)[7] = float("inf")
+    if k == 3:  # a NaN
+        params[-1].grad.view(-1)[5] = float("nan")
+
+
+@pytest.mark.parametrize("clip", [True, False])
+def test_fused_unscale_matches_grad_scaler_unscale(clip):
+    """The loss-scale unscaling fused into the clip's read of the gradients
+    (``clip_grad_norm_(max_norm, grad_scaler=...)``, or ``unscale_grads_`` without a clip) against
+    torch's ``scaler.unscale_(opt)`` writing the unscaled gradients, then the same clip and
+    ``scaler.step`` / ``scaler.update``: the total norm, found_inf, the scale's trajectory, and
+    parameters and moment state after every step bit-identical, over five iterations with a
+    scale that is not a power of two (so unscaling rounds) and an overflowed (inf) and a NaN
+    iteration, whose steps both skip.  The fused path leaves the gradients scaled in memory.
+    (torch's unscale_ takes fp32 gradients only on this device: it refuses fp16, and its kernel
+    has no bf16 instance; bf16 is the next test.)"""
+    log(f"fused GradScaler unscale ({'with' if clip else 'without'} clip)")
+    gen = torch.Generator().manual_seed(43)
+    shapes = [(128, 256), (512,), (64, 256)]
+    init = [torch.randn(s, generator=gen) * 0.02 for s in shapes]
+    pa = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
+    pb = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
+    oa = aw.ZIPSRAdamW4Bit(pa, optimized=True, quant_rng_seed=4, **ARGS)
+    ob = aw.ZIPSRAdamW4Bit(pb, optimized=True, quant_rng_seed=4, **ARGS)
+    sa = torch.amp.GradScaler("cuda", init_scale=3.0 * 2 ** 10, growth_interval=2)
+    sb = torch.amp.GradScaler("cuda", init_scale=3.0 * 2 ** 10, growth_interval=2)
+    skipped = 0
+    for k in range(5):
+        gs = [H.heavy_tailed(s, gen) for s in shapes]
+        sa.scale(torch.ones((), device=H.DEVICE))  # the loss a trainer would scale
+        sb.scale(torch.ones((), device=H.DEVICE))
+        scale = sa.get_scale()
+        assert scale == sb.get_scale()
+        _scaled_grads(pa, gs, scale, k)
+        _scaled_grads(pb, gs, scale, k)
+        scaled = [a.grad.clone() for a in pa]
+        if clip:
+            ta = oa.clip_grad_norm_(1.0, grad_scaler=sa)
+            sb.unscale_(ob)
+            tb = ob.clip_grad_norm_(1.0)
+            assert ta.dtype == tb.dtype
+            assert torch.equal(H.bits(ta), H.bits(tb)) or (bool(ta.isnan()) and bool(tb.isnan())), (k, ta, tb)
+        else:
+            oa.unscale_grads_(sa)
+            sb.unscale_(ob)
+        fa = sum(float(v) for v in sa._per_optimizer_states[id(oa)]["found_inf_per_device"].values())
+        fb = sum(float(v) for v in sb._per_optimizer_states[id(ob)]["found_inf_per_device"].values())
+        assert fa == fb == (1.0 if k in (2, 3) else 0.0), (k, fa, fb)
+        with pytest.raises(RuntimeError, match="already been called"):
+            sa.unscale_(oa)
+        sa.step(oa)
+        sb.step(ob)
+        sa.update()
+        sb.update()
+        assert sa.get_scale() == sb.get_scale()
+        for a, g in zip(pa, scaled):
+            assert torch.equal(H.bits(a.grad), H.bits(g)), k  # still scaled in memory
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(pa, pb)):
+            same_state(oa, a, ob, b, (k, i))
+        skipped += int(k in (2, 3))
+        oa.zero_grad()  # drops the pending unscale/clip of a skipped step
+        ob.zero_grad()
+    assert all(oa.state[a]["step"] == 5 - skipped for a in pa)
+    # torch's unscale_ refuses fp16 gradients, and so does the fused one
+    ph = torch.nn.Parameter(torch.zeros(4096, dtype=torch.float16, device=H.DEVICE))
+    oh = aw.ZIPSRAdamW4Bit([ph], optimized=True, quant_rng_seed=4, **ARGS)
+    ph.grad = torch.ones_like(ph)
+    sh = torch.amp.GradScaler("cuda")
+    sh.scale(torch.ones((), device=H.DEVICE))
+    with pytest.raises(ValueError, match="FP16"):
+        oh.clip_grad_norm_(1.0, grad_scaler=sh)
+
+
+def test_fused_unscale_of_bf16_gradients():
+    """bf16 gradients, which torch's unscale_ kernel does not take here: the fused unscale reads
+    each value as bf16(fp32(g) * inv_scale), the functor torch applies to its dtypes, so the
+    result equals torch ops that unscale in place the same way (found_inf: any value not finite,
+    the step skipped), followed by the fused clip and the step, bit for bit."""
+    log("fused GradScaler unscale, bf16 gradients")
+    gen = torch.Generator().manual_seed(47)
+    shapes = [(128, 256), (64, 256)]
+    init = [(torch.randn(s, generator=gen) * 0.02).to(torch.bfloat16) for s in shapes]
+    pa = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
+    pb = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
+    oa = aw.ZIPSRAdamW4Bit(pa, optimized=True, quant_rng_seed=6, **ARGS)
+    ob = aw.ZIPSRAdamW4Bit(pb, optimized=True, quant_rng_seed=6, **ARGS)
+    sa = torch.amp.GradScaler("cuda", init_scale=3.0 * 2 ** 10, growth_interval=2)
+    for k in range(5):
+        gs = [H.heavy_tailed(s, gen) for s in shapes]
+        sa.scale(torch.ones((), device=H.DEVICE))
+        scale = sa.get_scale()
+        _scaled_grads(pa, gs, scale, k)
+        _scaled_grads(pb, gs, scale, k)
+        inv = sa._scale.double().reciprocal().float()
+        found = any(not bool(torch.isfinite(b.grad).all()) for b in pb)
+        for b in pb:
+            b.grad = (b.grad.float() * inv).to(torch.bfloat16)
+        ta = oa.clip_grad_norm_(1.0, grad_scaler=sa)
+        tb = ob.clip_grad_norm_(1.0)
+        assert torch.equal(H.bits(ta), H.bits(tb)) or (bool(ta.isnan()) and bool(tb.isnan())), (k, ta, tb)
+        fa = sum(float(v) for v in sa._per_optimizer_states[id(oa)]["found_inf_per_device"].values())
+        assert fa == float(found) == (1.0 if k in (2, 3) else 0.0), k
+        sa.step(oa)
+        sa.update()
+        if not found:
+            ob.step()
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(pa, pb)):
+            same_state(oa, a, ob, b, (k, i))
+        oa.zero_grad()
+        ob.zero_grad()
+
+
 # ---------------------------------------------------------------------------
 # torch.compile: the launch is the custom operator
 # ---------------------------------------------------------------------------

@@ -407,7 +407,7 @@ def test_fused_clip_matches_torch_clip(kind):
         for p, g in zip(params, grads):
             p.grad = g.to(H.DEVICE)
         total = opt.clip_grad_norm_(max_norm)
-        coef = opt._grad_clip[1].cpu().reshape(())
+        coef = opt._grad_clip[1][1].cpu().reshape(())
         with pytest.raises(RuntimeError, match="already pending"):
             opt.clip_grad_norm_(max_norm)
         if step == 0:  # a skipped step: zero_grad() drops the pending clip with the gradients
@@ -416,7 +416,7 @@ def test_fused_clip_matches_torch_clip(kind):
             for p, g in zip(params, grads):
                 p.grad = g.to(H.DEVICE)
             total = opt.clip_grad_norm_(max_norm)
-            coef = opt._grad_clip[1].cpu().reshape(())
+            coef = opt._grad_clip[1][1].cpu().reshape(())
         expect_total, _ = ref.clip_grad_norm_f64(grads, max_norm)
         torch_total, _ = ref.clip_grad_norm(grads, max_norm)
         assert total.dtype == expect_total.dtype == torch_total.dtype and total.shape == ()
