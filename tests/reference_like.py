@@ -9,6 +9,8 @@ from __future__ import annotations
 
 import torch
 
+from adamw4bit_amd.quantization import QuantState  # stands in for the reference's QuantState
+
 MIN_QUANT_NUMEL = 4096
 
 
@@ -61,6 +63,40 @@ class ReferenceLikeOptimizer(torch.optim.Optimizer):
         for m, gens in states.items():
             for key, state in gens.items():
                 self._quant_generator(m, torch.device(key)).set_state(state)
+
+    def state_dict(self):
+        """torch's state dict with each moment's scale metadata as a plain dict (adamw.py:326-336)."""
+        out = super().state_dict()
+        out["state"] = {index: {k: (vars(v).copy() if isinstance(v, QuantState) else v) for k, v in st.items()}
+                        for index, st in out["state"].items()}
+        return out
+
+    def load_state_dict(self, state_dict):
+        """torch's load casts every tensor of a parameter's state to the parameter's dtype; as the
+        reference does (adamw.py:364-425), a post-hook that runs before any other puts back the
+        saved fp32 moments and uint8 codes and rebuilds the scale metadata objects."""
+        def restore(_optimizer):
+            for group, saved_group in zip(self.param_groups, state_dict["param_groups"]):
+                for p, index in zip(group["params"], saved_group["params"]):
+                    saved = state_dict["state"].get(index, {})
+                    state = self.state[p]
+                    for key in ("m1", "m2", "lookahead_pending_exp_avg_sq", "m2_read_preconditioner"):
+                        if key in saved:
+                            state[key] = saved[key].to(device=p.device, dtype=torch.float32)
+                    for key in ("m1_code", "m2_code"):
+                        if key in saved:
+                            state[key] = saved[key].to(device=p.device, dtype=torch.uint8)
+                    for key in ("m1_quant_state", "m2_quant_state"):
+                        if key in saved:
+                            fields = dict(saved[key])
+                            fields["absmax"] = fields["absmax"].to(device=p.device, dtype=torch.float32)
+                            state[key] = QuantState(**fields)
+
+        hook = self.register_load_state_dict_post_hook(restore, prepend=True)
+        try:
+            return super().load_state_dict(state_dict)
+        finally:
+            hook.remove()
 
     @torch.no_grad()
     def step(self, closure=None):

@@ -7,7 +7,7 @@ parameters the kernels do not take going to the reference's own backend, and the
 import pytest
 import torch
 
-from adamw4bit_amd.adamw import QuantizedAdamW
+from adamw4bit_amd.adamw import _FALLBACK_KEY, QuantizedAdamW
 from adamw4bit_amd.backend import HipOptimizedBackend
 from adamw4bit_amd.quantization import QuantState
 
@@ -62,8 +62,8 @@ def test_declining_settings_change_nothing_and_draw_nothing(setting):
 
 @pytest.mark.parametrize("answer", [True, False])
 def test_parameters_the_kernels_do_not_take_go_to_the_reference_backend(answer):
-    """CPU parameters (and float64 ones) are the reference backend's: its answer is the answer."""
-    ps = [with_grad(64, 128), with_grad(4096, dtype=torch.float64)]
+    """CPU parameters (and complex ones) are the reference backend's: its answer is the answer."""
+    ps = [with_grad(64, 128), with_grad(4096, dtype=torch.complex64)]
     opt, stub = make(ps, answer=answer)
     opt.step()
     assert stub.calls == ps
@@ -75,3 +75,29 @@ def test_the_backend_belongs_to_its_optimizer():
     other, _ = make([with_grad(4096)])
     with pytest.raises(ValueError, match="another optimizer"):
         opt._optimized_backend.try_step_parameter(other, other.param_groups[0]["params"][0], other.param_groups[0])
+
+
+def test_checkpoint_load_restores_codes_before_the_aliasing_hook():
+    """torch's load casts a parameter's state tensors to its dtype; the reference's loader (and the
+    stand-in) puts the uint8 codes and fp32 scales back in a post-hook that runs first, so the
+    backend's aliased-state hook sees the restored state and marks nothing."""
+    p = torch.nn.Parameter(torch.zeros(64, 128, dtype=torch.bfloat16))
+    opt, _ = make([p])
+    codes = torch.arange(64 * 128 // 2, dtype=torch.uint8)
+    opt.state[p].update(step=3, m1_code=codes, m2_code=codes.flip(0).clone(),
+                        m1_quant_state=QuantState(torch.rand(64), shape=p.shape, dtype=torch.float32, blocksize=128,
+                                                  packed=True),
+                        m2_quant_state=QuantState(torch.rand(64), shape=p.shape, dtype=torch.float32, blocksize=128,
+                                                  packed=True))
+    saved = opt.state_dict()
+    seen = {}
+    q = torch.nn.Parameter(torch.zeros(64, 128, dtype=torch.bfloat16))
+    resumed, _ = make([q])
+    resumed.register_load_state_dict_post_hook(lambda o: seen.update(dtype=o.state[q]["m1_code"].dtype))
+    resumed.load_state_dict(saved)
+    st = resumed.state[q]
+    assert seen["dtype"] == torch.uint8
+    assert st["m1_code"].dtype == torch.uint8 and torch.equal(st["m1_code"], codes)
+    assert isinstance(st["m2_quant_state"], QuantState) and st["m2_quant_state"].absmax.dtype == torch.float32
+    assert torch.equal(st["m2_quant_state"].absmax, opt.state[p]["m2_quant_state"].absmax)
+    assert _FALLBACK_KEY not in st and st["step"] == 3
