@@ -17,7 +17,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIBRARY = os.path.join(HERE, "libadamw4bit_hip.so")
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 BLOCK = 128
 
 # Error codes
@@ -28,7 +28,7 @@ CB_NF4, CB_SDYN4, CB_DYN4, CB_LIN4, CB_LIN4_NZ = 0, 1, 2, 3, 4
 ROUND_FP32, ROUND_RTN, ROUND_STATE_SR, ROUND_UPDATE_SR, ROUND_LOOKAHEAD_SR = 0, 1, 2, 3, 4
 MOMENT_ZERO_FLOOR, MOMENT_EDEN, MOMENT_GUARDS, MOMENT_EXT_DRAWS = 0x1, 0x2, 0x4, 0x8
 MOMENT_SAMPLED_READ, MOMENT_READ_RAW_SCALE, MOMENT_FRESH_PROXY, MOMENT_PENDING = 0x10, 0x20, 0x40, 0x80
-F32, BF16, F16 = 0, 1, 2
+F32, BF16, F16, F64 = 0, 1, 2, 3
 TENSOR_LERP1_LARGE, TENSOR_LERP2_LARGE, TENSOR_VEC_ALIGNED, TENSOR_GRAD_SCALE = 0x1, 0x2, 0x4, 0x8
 TENSOR_GRAD_UNSCALE = 0x10
 
@@ -49,8 +49,9 @@ TENSOR = np.dtype([
     ("w1", "<f4"), ("w2", "<f4"), ("decay", "<f4"), ("step_coef", "<f4"),
     ("bc2_sqrt", "<f4"), ("bc2_sqrt_rcp", "<f4"), ("eps", "<f4"),
     ("m1", MOMENT), ("m2", MOMENT),
+    ("decay_f64", "<f8"), ("step_coef_f64", "<f8"),
 ])
-assert MOMENT.itemsize == 104 and TENSOR.itemsize == 280
+assert MOMENT.itemsize == 104 and TENSOR.itemsize == 296
 
 # Every function the header declares, with its ctypes signature.
 SIGNATURES = {
@@ -112,10 +113,30 @@ def check(rc: int, what: str) -> int:
     return rc
 
 
+class Rows(np.ndarray):
+    """Launch-table rows (dtype :data:`TENSOR`, C-contiguous) with their host address resolved
+    once (``ptr``; numpy's ``ctypes.data`` costs about half a microsecond per call): a launch
+    plan hands the same rows to every step.  Views and copies do not keep the address."""
+
+    def __array_finalize__(self, obj) -> None:
+        self.ptr = None
+
+
+def rows_of(table: np.ndarray) -> Rows:
+    """``table`` as :class:`Rows` (the same memory)."""
+    assert table.dtype == TENSOR and table.flags.c_contiguous
+    rows = table.view(Rows)
+    rows.ptr = rows.ctypes.data
+    return rows
+
+
 def fused_step(table: np.ndarray, stream: int) -> None:
     """Launch one fused step over the rows of ``table`` (dtype :data:`TENSOR`)."""
-    assert table.dtype == TENSOR and table.flags.c_contiguous
-    check(library().aw4_fused_step(table.ctypes.data, len(table), stream), "aw4_fused_step")
+    ptr = table.ptr if type(table) is Rows else None
+    if ptr is None:
+        assert table.dtype == TENSOR and table.flags.c_contiguous
+        ptr = table.ctypes.data
+    check(library().aw4_fused_step(ptr, len(table), stream), "aw4_fused_step")
 
 
 def fused_step_noalloc(table: np.ndarray, stream: int) -> None:

@@ -7,7 +7,7 @@ which tensors it writes (parameters and moment states, updated in place) and whi
 (gradients, the clip coefficient, caller-provided draws), and it runs on the current stream of
 the parameters' device.
 
-``table`` is a CPU uint8 tensor of ``aw4_tensor`` rows (280 bytes each) holding everything but
+``table`` is a CPU uint8 tensor of ``aw4_tensor`` rows (296 bytes each) holding everything but
 device addresses; ``refs`` (CPU int64, one row per table row, :data:`ADDRESS_FIELDS` columns)
 says which tensor each address field points into: an index into ``params + states + inputs``,
 or -1 for "no buffer".  The operator reads the addresses from the tensors it receives at call

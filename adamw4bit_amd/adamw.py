@@ -32,6 +32,7 @@ from __future__ import annotations
 import array
 import bisect
 import functools
+import itertools
 import math
 import operator
 import struct
@@ -85,7 +86,8 @@ _OPT_M2_SCHEMES = {
     "fp32", "lin4", "lin4_sr", "lin4_nz", "dyn4", "dyn4_sr", "dyn4_nz",
     "lin4_upd_sr_fp32read", "dyn4_upd_sr_fp32read", "dyn4_lookahead_sr", "dyn4_upd_sr_fp32read_nextbc",
 }
-_DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
+_DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16, torch.float64: _lib.F64}
+_CLIP_DTYPES = (torch.float32, torch.bfloat16, torch.float16)  # gradients the fused clip and unscale read
 _UNSUPPORTED_SCHEMES = {"linear": "8-bit linear state", "dynamic": "8-bit dynamic state"}
 _SR_ROUNDINGS = (ROUND_STATE_SR, ROUND_UPDATE_SR, ROUND_LOOKAHEAD_SR)  # roundings that draw uniforms
 
@@ -103,12 +105,17 @@ def _rcp32(x: float) -> float:
     return array.array("f", (1.0 / x,)).tolist()[0]
 
 
+def _rcp32s(*values: float) -> list:
+    """``_rcp32`` of each fp32 value, with one rounding call."""
+    return array.array("f", [1.0 / x if x != 0.0 else math.copysign(math.inf, x) for x in values]).tolist()
+
+
 def _step_fields() -> np.dtype:
     """View of a launch-table row holding only what a reused plan rewrites each step: the
     gradient address and scale pointer, the flags word with the seven fp32 step constants
-    after it (``words``, 8 x 32 bits), the m2 update-SR constants (``m2_sr``, 3 x 32 bits)
-    and both random-stream keys and positions (a stream drawn from torch's generator takes
-    that generator's current seed)."""
+    after it (``words``, 8 x 32 bits), the m2 update-SR constants (``m2_sr``, 3 x 32 bits),
+    both random-stream keys and positions (a stream drawn from torch's generator takes
+    that generator's current seed) and the float64 constants of float64 parameters (``f64``)."""
     T = _lib.TENSOR
     m1, m2 = T.fields["m1"][1], T.fields["m2"][1]
     M = T.fields["m2"][0]
@@ -116,17 +123,30 @@ def _step_fields() -> np.dtype:
     assert [T.fields[k][1] for k in words] == [T.fields["flags"][1] + 4 * i for i in range(8)]
     assert [M.fields[k][1] for k in ("sr_bias", "sr_bias_rcp", "sr_eps")] == [M.fields["sr_bias"][1] + 4 * i
                                                                             for i in range(3)]
+    assert T.fields["step_coef_f64"][1] == T.fields["decay_f64"][1] + 8
     return np.dtype({"names": ["grad", "grad_scale", "words", "m2_sr", "m1_rng_seed", "m2_rng_seed",
-                               "m1_rng_offset", "m2_rng_offset"],
-                     "formats": ["<u8", "<u8", ("<u4", 8), ("<u4", 3), "<u8", "<u8", "<u8", "<u8"],
+                               "m1_rng_offset", "m2_rng_offset", "f64"],
+                     "formats": ["<u8", "<u8", ("<u4", 8), ("<u4", 3), "<u8", "<u8", "<u8", "<u8", ("<f8", 2)],
                      "offsets": [T.fields["grad"][1], T.fields["grad_scale"][1], T.fields["flags"][1],
                                  m2 + M.fields["sr_bias"][1], m1 + M.fields["rng_seed"][1],
                                  m2 + M.fields["rng_seed"][1], m1 + M.fields["rng_offset"][1],
-                                 m2 + M.fields["rng_offset"][1]],
+                                 m2 + M.fields["rng_offset"][1], T.fields["decay_f64"][1]],
                      "itemsize": T.itemsize})
 
 
 _STEP_FIELDS = _step_fields()
+# The same per-step fields as byte offsets within a row, for small plans, which pack them in place.
+_OFF_WORDS = _lib.TENSOR.fields["flags"][1]
+_OFF_GRAD = _lib.TENSOR.fields["grad"][1]
+_OFF_M2_SR = _lib.TENSOR.fields["m2"][1] + _lib.MOMENT.fields["sr_bias"][1]
+_OFF_F64 = _lib.TENSOR.fields["decay_f64"][1]
+_OFF_RNG = {m: _lib.TENSOR.fields[m][1] + _lib.MOMENT.fields["rng_seed"][1] for m in ("m1", "m2")}
+assert _lib.MOMENT.fields["rng_offset"][1] == _lib.MOMENT.fields["rng_seed"][1] + 8
+_PACK_WORDS = struct.Struct("<i7f").pack_into    # flags word and the seven fp32 step constants
+_PACK_U64 = struct.Struct("<Q").pack_into
+_PACK_M2_SR = struct.Struct("<3f").pack_into     # update-SR bias, its reciprocal, eps
+_PACK_F64 = struct.Struct("<2d").pack_into       # decay_f64, step_coef_f64
+_PACK_RNG = struct.Struct("<QQ").pack_into       # rng_seed, rng_offset
 _STEP_WORDS = np.dtype([("flags", "<i4")] + [(k, "<f4") for k in ("w1", "w2", "decay", "step_coef", "bc2_sqrt",
                                                                    "bc2_sqrt_rcp", "eps")])
 
@@ -192,15 +212,21 @@ class _StepConstants:
     the m2 update-SR bias, its reciprocal and eps)."""
 
     __slots__ = ("lerp_flags", "w1", "w2", "decay", "step_coef", "bc2_sqrt", "bc2_sqrt_rcp", "eps", "storage_bias",
-                 "_words", "_m2_sr")
+                 "decay_f64", "step_coef_f64", "_words", "_m2_sr", "_m2_vals")
 
     def __init__(self, group, step: int, m2_scheme: str):
         beta1, beta2 = group["betas"]
         lr, wd, eps = group["lr"], group["weight_decay"], group["eps"]
         bias1, bias2 = 1 - beta1 ** step, 1 - beta2 ** step
         self.storage_bias = 1 - beta2 ** (step + 1) if m2_scheme in NEXT_BIAS_SCHEMES else bias2
-        w1, w2, self.decay, self.step_coef, self.bc2_sqrt, self.eps = _f32s(
-            1 - beta1, 1 - beta2, 1 - lr * wd, -lr / bias1, math.sqrt(bias2), eps)
+        # a float64 parameter is decayed and updated with the float64 values (_optimized.py:221-222)
+        self.decay_f64, self.step_coef_f64 = float(1 - lr * wd), float(-lr / bias1)
+        # one fp32 rounding of everything, then of the two reciprocals (the update-SR bias is
+        # floored at 1e-12 before its rounding, _optimized_quantization.py:66-67)
+        w1, w2, self.decay, self.step_coef, self.bc2_sqrt, self.eps, sr_bias = _f32s(
+            1 - beta1, 1 - beta2, 1 - lr * wd, -lr / bias1, math.sqrt(bias2), eps, max(float(self.storage_bias), 1e-12))
+        self.bc2_sqrt_rcp, sr_bias_rcp = _rcp32s(self.bc2_sqrt, sr_bias)
+        self._m2_vals = (sr_bias, sr_bias_rcp, self.eps)
         flags = 0
         if not abs(w1) < 0.5:  # ATen lerp switches formulas at |weight| >= 0.5
             flags |= _lib.TENSOR_LERP1_LARGE
@@ -210,7 +236,6 @@ class _StepConstants:
             w2 = w2 - 1.0
         self.lerp_flags = flags
         self.w1, self.w2 = w1, w2
-        self.bc2_sqrt_rcp = _rcp32(self.bc2_sqrt)
         self._words = self._m2_sr = None
 
     def words(self) -> np.ndarray:
@@ -220,10 +245,13 @@ class _StepConstants:
                                         dtype=np.uint32)
         return self._words
 
+    def m2_sr_values(self) -> tuple:
+        """fp32 update-SR storage bias max(c, 1e-12), its correctly rounded reciprocal, and eps."""
+        return self._m2_vals
+
     def m2_sr(self) -> np.ndarray:
         if self._m2_sr is None:
-            bias = _f32(max(float(self.storage_bias), 1e-12))
-            self._m2_sr = np.frombuffer(struct.pack("<3f", bias, _rcp32(bias), self.eps), dtype=np.uint32)
+            self._m2_sr = np.frombuffer(struct.pack("<3f", *self.m2_sr_values()), dtype=np.uint32)
         return self._m2_sr
 
 
@@ -242,7 +270,7 @@ def _table_tensor(table: np.ndarray) -> torch.Tensor:
     """The rows of a launch table as the CPU uint8 tensor a launch record carries; the tensor also
     keeps the rows for the eager launch (``_aw4_rows``)."""
     t = torch.from_numpy(table.view(np.uint8))
-    t._aw4_rows = table
+    t._aw4_rows = _lib.rows_of(table)
     return t
 
 
@@ -785,8 +813,8 @@ class QuantizedAdamW(Optimizer):
         grads = []
         for p in params:
             g = p.grad
-            if g.layout != torch.strided or g.dtype not in _DTYPES:
-                raise NotImplementedError("gradients must be dense float32/bfloat16/float16 tensors")
+            if g.layout != torch.strided or g.dtype not in _CLIP_DTYPES:
+                raise NotImplementedError("the fused clip reads dense float32/bfloat16/float16 gradients")
             grads.append(g if g.is_contiguous() else g.contiguous())
         table = np.zeros(len(grads), dtype=_lib.TENSOR)
         table["grad"] = [g.data_ptr() for g in grads]
@@ -822,7 +850,6 @@ class QuantizedAdamW(Optimizer):
     # The step
     # ------------------------------------------------------------------
     @_lean_step
-    @torch.no_grad()
     def step(self, closure=None):  # type: ignore[override]
         """One fused launch per device over every parameter with a gradient (``adamw.py:472-502``).
 
@@ -831,9 +858,34 @@ class QuantizedAdamW(Optimizer):
         the custom operator ``adamw4bit_hip::fused_step_`` when compiled and a direct library call
         otherwise.  A step changes nothing unless it launches: every parameter is checked before
         any state changes, and a failed launch restores step counts, moment state and random
-        stream positions."""
+        stream positions.  Like the reference's, the step runs under ``torch.no_grad()``, except
+        an eager step without closure that reuses the last step's launch tables: it runs no torch
+        operation (a library call and version-counter bumps), so it skips the grad-mode switch."""
         if self._inconsistent is not None:
             raise RuntimeError(self._inconsistent)
+        plan = self._launch_plan
+        if closure is None and plan is not None and not torch.compiler.is_compiling():
+            prepared = plan.prepare(self, records=False)
+            if prepared is not None:
+                self._pending_finish = prepared[1]
+                done = 0
+                incomplete = False
+                try:
+                    for dev in plan.devices:
+                        try:
+                            dev.launch_eager()
+                        except _lib.HipLaunchIncomplete:
+                            incomplete = True
+                            raise
+                        done += 1
+                finally:
+                    self._finish_launches(done, len(plan.devices), incomplete)
+                return None
+            self._launch_plan = None  # stale: the full path rebuilds it
+        return self._step_full(closure)
+
+    @torch.no_grad()
+    def _step_full(self, closure):
         loss = None
         if closure is not None:
             with torch.enable_grad():
@@ -855,6 +907,9 @@ class QuantizedAdamW(Optimizer):
 
     @torch.compiler.disable
     def _finish_step(self, done: int, total: int, incomplete: bool = False) -> None:
+        self._finish_launches(done, total, incomplete)
+
+    def _finish_launches(self, done: int, total: int, incomplete: bool = False) -> None:
         """Commit the prepared step after its launches (``done == total``), or undo it if no step
         kernel was enqueued.  A step that failed after enqueuing some of its kernels (a launch that
         failed part way, or one device's launch after another's) cannot be undone: the tensors may
@@ -969,12 +1024,13 @@ class QuantizedAdamW(Optimizer):
         if not p.is_cuda:
             raise NotImplementedError("the fused 4-bit step runs on HIP devices only; move the parameters to the GPU")
         if p.dtype not in _DTYPES:
-            raise NotImplementedError(f"parameter dtype {p.dtype} (supported: float32, bfloat16, float16)")
+            raise NotImplementedError(f"parameter dtype {p.dtype} (supported: float32, bfloat16, float16, float64)")
         if p.layout != torch.strided:
             raise NotImplementedError("the fused step updates dense (strided) parameters in place")
         grad = p.grad
         if grad.layout != torch.strided or grad.dtype not in _DTYPES or grad.device != p.device:
-            raise NotImplementedError("gradients must be dense float32/bfloat16/float16 tensors on the parameter's device")
+            raise NotImplementedError("gradients must be dense float32/bfloat16/float16/float64 tensors on the "
+                                      "parameter's device")
         if grad.shape != p.shape:
             raise ValueError(f"gradient shape {tuple(grad.shape)} does not match parameter shape {tuple(p.shape)}")
         state = self.state[p]
@@ -1074,7 +1130,8 @@ class QuantizedAdamW(Optimizer):
             if schemes[1] in SAMPLED_READ_SCHEMES:
                 m2 = m2[:8] + (m2[8] | _lib.MOMENT_SAMPLED_READ,) + m2[9:]
         batch.rows.append((0, 0, 0, n, _DTYPES[p.dtype], _DTYPES[grad.dtype], flags, c_.w1, c_.w2, c_.decay,
-                           c_.step_coef, c_.bc2_sqrt, c_.bc2_sqrt_rcp, c_.eps, m1, m2))
+                           c_.step_coef, c_.bc2_sqrt, c_.bc2_sqrt_rcp, c_.eps, m1, m2, c_.decay_f64,
+                           c_.step_coef_f64))
         batch.refs.append(refs)
         pre = state.get("m2_read_preconditioner")
         for t in [target] + _moment_tensors(state) + ([pre] if isinstance(pre, torch.Tensor) else []):
@@ -1266,6 +1323,7 @@ class _StepUndo:
 # Plans of at most this many rows per device check and refresh their rows in Python loops,
 # larger ones with numpy (whose fixed cost per operation is about a microsecond).
 _SMALL_PLAN = 16
+_REPEAT_STEP, _REPEAT_INT = itertools.repeat("step"), itertools.repeat(int)
 
 
 class _PlanDevice:
@@ -1273,9 +1331,10 @@ class _PlanDevice:
     the views and per-row facts its per-step refresh needs."""
 
     __slots__ = ("table", "params", "written", "entries", "states", "device", "small", "lo", "hi", "ranges",
-                 "pptr", "gbytes", "gbytes_list", "pvec", "pvec_list", "gvec", "gvec_list", "fields", "words",
+                 "gbytes", "gbytes_list", "pvec", "pvec_list", "gvec", "gvec_list", "fields", "words",
                  "m2_sr", "seed_cols", "offset_cols", "grad_col", "qrows", "qsel", "qrows_any", "la_rows", "la_next",
-                 "refs", "table_t", "refs_t", "scale_ptr", "scale_ref")
+                 "f64", "f64_rows", "refs", "table_t", "refs_t", "scale_ptr", "scale_ref", "buf", "row_plans",
+                 "rows", "index", "bump", "gchecked")
 
     def __init__(self, table: np.ndarray, params, written, entries, lo, hi, ranges, refs: np.ndarray):
         n = len(params)
@@ -1288,7 +1347,6 @@ class _PlanDevice:
         self.small = n <= _SMALL_PLAN
         self.lo, self.hi = lo, hi
         self.ranges = ranges  # per row: the (start, end) byte ranges a gradient may not overlap
-        self.pptr = [p.data_ptr() for p in params]
         self.gbytes_list = [p.numel() * p.element_size() for p in params]
         self.gbytes = np.array(self.gbytes_list, dtype=np.int64)
         self.pvec_list = [p.data_ptr() % (4 * p.element_size()) == 0 for p in params]
@@ -1309,10 +1367,33 @@ class _PlanDevice:
         # step too (the pending form's bias is bias_c2 of the step, the proxies' that of the next)
         self.la_rows = np.flatnonzero(table["m2"]["rounding"] == _lib.ROUND_LOOKAHEAD_SR)
         self.la_next = (table["m2"]["flags"][self.la_rows] & _lib.MOMENT_PENDING) == 0
+        # float64 parameters: their float64 decay and step coefficient are per step too
+        self.f64 = self.fields["f64"]
+        self.f64_rows = np.flatnonzero(table["param_dtype"] == _lib.F64)
         self.refs = refs
         self.table_t = _table_tensor(table)
+        self.rows = self.table_t._aw4_rows
         self.refs_t = torch.from_numpy(refs)
         self.scale_ptr = self.scale_ref = None  # what the grad_scale fields hold (unknown: rewrite)
+        self.index = self.device.index
+        self.bump = self.params + self.written  # what an eager launch writes in place
+        self.gchecked = None  # the gradient addresses whose overlap check last passed
+        # small plans write each row's per-step fields in place (struct.pack_into at the row's
+        # offsets): per row whether m2 takes the update-SR constants, is float64, is lookahead
+        self.buf = memoryview(table.view(np.uint8)).cast("B")
+        rounding, pdtype = table["m2"]["rounding"], table["param_dtype"]
+        self.row_plans = [(i * _lib.TENSOR.itemsize, bool(rounding[i] != _lib.ROUND_FP32),
+                           bool(pdtype[i] == _lib.F64)) for i in range(n)] if self.small else None
+
+    def launch_eager(self) -> None:
+        """The eager launch of a refreshed plan (as ``_launch`` for its record)."""
+        index = self.index
+        if torch.cuda.current_device() != index:
+            with torch.cuda.device(index):
+                _lib.fused_step(self.rows, _raw_stream(index))
+        else:
+            _lib.fused_step(self.rows, _raw_stream(index))
+        torch.autograd.graph.increment_version(self.bump)
 
 
 class _LaunchPlan:
@@ -1336,8 +1417,10 @@ class _LaunchPlan:
         self.groups: list = []     # (group, structure, parameter count)
         self.streams: list = []    # the random streams the planned rows draw from
         self.params: List[torch.Tensor] = []
-        self.pdtypes: list = []    # each parameter's dtype, numel at build time
+        self.pdtypes: list = []    # each parameter's dtype, numel and data address at build time
         self.pnumel: list = []
+        self.pptr: list = []
+        self.one_small = False
         self.devices: list = []    # per device: see build
         # what the tables were built from, checked by identity each step, as parallel lists:
         # (params, their state dicts), (state dict, key, value) for every state key,
@@ -1420,6 +1503,8 @@ class _LaunchPlan:
             plan.params.extend(params)
             plan.pdtypes.extend(p.dtype for p in params)
             plan.pnumel.extend(p.numel() for p in params)
+            plan.pptr.extend(p.data_ptr() for p in params)
+        plan.one_small = len(plan.devices) == 1 and plan.devices[0].small
         return plan
 
     def _valid(self, opt: "QuantizedAdamW"):
@@ -1428,32 +1513,41 @@ class _LaunchPlan:
             return None
         params = self.params
         dtypes = self.pdtypes
+        one = self.one_small  # one device with few rows: its storage checks join the first loop
+        numels, pptrs, gptrs = self.pnumel, self.pptr, []
         i = 0
         n = len(params)
         strided = torch.strided
         for (group, structure, count), current in zip(self.groups, opt.param_groups):
             if current is not group or len(group["params"]) != count:
                 return None
-            if tuple(group.get(k) for k in self._STRUCTURE_KEYS) != structure:
+            if tuple(map(group.get, self._STRUCTURE_KEYS)) != structure:
                 return None
             for p in group["params"]:
                 g = p.grad
                 if g is None:
                     continue
-                if (i >= n or p is not params[i] or p.dtype is not dtypes[i] or g.layout != strided
+                if (i >= n or p is not params[i] or p.dtype is not dtypes[i] or g.layout is not strided
                         or not g.is_contiguous() or not p.is_contiguous()):
                     return None
+                if one:
+                    # the parameter's size and storage are still what the tables hold (p.data
+                    # can be swapped without changing the Parameter object)
+                    if p.numel() != numels[i] or p.data_ptr() != pptrs[i]:
+                        return None
+                    gptrs.append(g.data_ptr())
                 i += 1
         if i != n:
             return None
-        if list(map(torch.Tensor.numel, params)) != self.pnumel:
+        if not one and (list(map(torch.Tensor.numel, params)) != numels
+                        or list(map(torch.Tensor.data_ptr, params)) != pptrs):
             return None
         # identity checks in C-level loops (map/all): about 1,300 of them for 148 parameters
         state_map = opt.state
         owners, states = self.owners
         if not all(map(operator.is_, map(state_map.get, owners), states)):
             return None
-        if not all(type(state.get("step")) is int for state in states):
+        if not all(map(operator.is_, map(type, map(dict.get, states, _REPEAT_STEP)), _REPEAT_INT)):
             return None
         ref_states, ref_keys, ref_values = self.state_refs
         if not all(map(operator.is_, map(dict.get, ref_states, ref_keys), ref_values)):
@@ -1463,18 +1557,17 @@ class _LaunchPlan:
             return None
         out = []
         for dev in self.devices:
-            dparams = dev.params
-            # the parameters' storage is still where the tables point (p.data can be swapped
-            # without changing the Parameter object)
-            if list(map(torch.Tensor.data_ptr, dparams)) != dev.pptr:
-                return None
-            g0 = [p.grad.data_ptr() for p in dparams]
+            g0 = gptrs if one else [p.grad.data_ptr() for p in dev.params]
             if dev.small:
-                for g, nbytes, ranges in zip(g0, dev.gbytes_list, dev.ranges):
-                    g1 = g + nbytes
-                    for a, b in ranges:
-                        if a < g1 and g < b:
-                            return None
+                # a gradient may not overlap its row's tensors (the plan's ranges); a gradient at
+                # the address checked last step passes again
+                if g0 != dev.gchecked:
+                    for g, nbytes, ranges in zip(g0, dev.gbytes_list, dev.ranges):
+                        g1 = g + nbytes
+                        for a, b in ranges:
+                            if a < g1 and g < b:
+                                return None
+                    dev.gchecked = g0
             else:
                 g0 = np.array(g0, dtype=np.int64)
                 g1 = g0 + dev.gbytes
@@ -1483,9 +1576,10 @@ class _LaunchPlan:
             out.append(g0)
         return out
 
-    def prepare(self, opt: "QuantizedAdamW"):
+    def prepare(self, opt: "QuantizedAdamW", records: bool = True):
         """Launch records and ``finish`` of the step from the cached tables (as
-        ``QuantizedAdamW._prepare_launches``), or None (nothing changed) if the plan is stale."""
+        ``QuantizedAdamW._prepare_launches``), or None (nothing changed) if the plan is stale.
+        Without ``records`` the launches are the devices' ``launch_eager`` (the list is None)."""
         grads = self._valid(opt)
         if grads is None:
             return None
@@ -1496,45 +1590,66 @@ class _LaunchPlan:
         constants: Dict[Tuple[int, int, str], int] = {}
         consts: List[_StepConstants] = []
         launches = []
+
+        def constants_of(gi: int, step: int, m2_scheme: str) -> int:
+            k = constants.get((gi, step, m2_scheme))
+            if k is None:
+                k = constants[(gi, step, m2_scheme)] = len(consts)
+                consts.append(_StepConstants(self.groups[gi][0], step, m2_scheme))
+            return k
+
         for dev, g0 in zip(self.devices, grads):
             entries = dev.entries
-            ks = []  # constants index of each row
-            seeds, offsets = dev.seed_cols, dev.offset_cols
-            for i, (state, gi, m2_scheme, sr, numel) in enumerate(entries):
-                step = state["step"] + 1
-                state["step"] = step
-                k = constants.get((gi, step, m2_scheme))
-                if k is None:
-                    k = constants[(gi, step, m2_scheme)] = len(consts)
-                    consts.append(_StepConstants(self.groups[gi][0], step, m2_scheme))
-                ks.append(k)
-                for moment, stream in sr:
-                    seeds[moment][i] = stream.seed
-                    offsets[moment][i] = stream.take(numel)
-            # the flags word and the seven fp32 step constants (bit patterns), and the m2
-            # update-SR constants of the rows whose m2 is quantized
-            one = ks.count(ks[0]) == len(ks)
-            if one:
-                dev.words[:] = consts[ks[0]].words()
-            else:
-                index = np.array(ks, dtype=np.intp)
-                dev.words[:] = np.stack([c.words() for c in consts])[index]
             clip = opt._take_grad_clip(dev.device)
             coef, extra = clip if clip is not None else (None, 0)
             if dev.small:
-                flags = dev.words[:, 0]
-                for i, (g, pvec, gvec) in enumerate(zip(g0, dev.pvec_list, dev.gvec_list)):
-                    f = extra | (_lib.TENSOR_VEC_ALIGNED if pvec and g % gvec == 0 else 0)
-                    if f:
-                        flags[i] |= f
+                # each row's per-step fields packed in place at its offsets
+                buf = dev.buf
+                for (state, gi, m2_scheme, sr, numel), (off, q2, f64), g, pvec, gvec in zip(
+                        entries, dev.row_plans, g0, dev.pvec_list, dev.gvec_list):
+                    step = state["step"] + 1
+                    state["step"] = step
+                    c = consts[constants_of(gi, step, m2_scheme)]
+                    flags = c.lerp_flags | extra | (_lib.TENSOR_VEC_ALIGNED if pvec and g % gvec == 0 else 0)
+                    _PACK_WORDS(buf, off + _OFF_WORDS, flags, c.w1, c.w2, c.decay, c.step_coef, c.bc2_sqrt,
+                                c.bc2_sqrt_rcp, c.eps)
+                    _PACK_U64(buf, off + _OFF_GRAD, g)
+                    if q2:
+                        _PACK_M2_SR(buf, off + _OFF_M2_SR, *c.m2_sr_values())
+                    if f64:
+                        _PACK_F64(buf, off + _OFF_F64, c.decay_f64, c.step_coef_f64)
+                    for moment, stream in sr:
+                        _PACK_RNG(buf, off + _OFF_RNG[moment], stream.seed, stream.take(numel))
+                ks = None
             else:
+                ks = []  # constants index of each row
+                seeds, offsets = dev.seed_cols, dev.offset_cols
+                for i, (state, gi, m2_scheme, sr, numel) in enumerate(entries):
+                    step = state["step"] + 1
+                    state["step"] = step
+                    ks.append(constants_of(gi, step, m2_scheme))
+                    for moment, stream in sr:
+                        seeds[moment][i] = stream.seed
+                        offsets[moment][i] = stream.take(numel)
+                # the flags word and the seven fp32 step constants (bit patterns), and the m2
+                # update-SR constants of the rows whose m2 is quantized
+                one = ks.count(ks[0]) == len(ks)
+                if one:
+                    dev.words[:] = consts[ks[0]].words()
+                else:
+                    index = np.array(ks, dtype=np.intp)
+                    dev.words[:] = np.stack([c.words() for c in consts])[index]
                 dev.words[:, 0] |= (np.where(dev.pvec & (g0 % dev.gvec == 0), _lib.TENSOR_VEC_ALIGNED, 0)
                                     | extra).astype(np.uint32)
-            if dev.qrows_any:
-                if one:
-                    dev.m2_sr[dev.qsel] = consts[ks[0]].m2_sr()
-                else:
-                    dev.m2_sr[dev.qrows] = np.stack([c.m2_sr() for c in consts])[index[dev.qrows]]
+                if dev.qrows_any:
+                    if one:
+                        dev.m2_sr[dev.qsel] = consts[ks[0]].m2_sr()
+                    else:
+                        dev.m2_sr[dev.qrows] = np.stack([c.m2_sr() for c in consts])[index[dev.qrows]]
+                if len(dev.f64_rows):
+                    dev.f64[dev.f64_rows] = [(consts[ks[i]].decay_f64, consts[ks[i]].step_coef_f64)
+                                             for i in dev.f64_rows.tolist()]
+                dev.grad_col[:] = g0
             if len(dev.la_rows):
                 # the lookahead fields, by the full path's arithmetic (Python floats)
                 la = []
@@ -1547,12 +1662,9 @@ class _LaunchPlan:
                 m2 = dev.table["m2"]
                 for k, name in enumerate(("la_beta2", "la_fresh_weight", "la_bias", "la_eps")):
                     m2[name][dev.la_rows] = [v[k] for v in la]
-            dev.grad_col[:] = g0
             params, written = dev.params, dev.written
-            read = [p.grad for p in params]
             scale_ref = -1
             if coef is not None:
-                read.append(coef)
                 scale_ref = len(params) + len(written) + len(params)
             scale_ptr = 0 if coef is None else coef.data_ptr()
             if scale_ptr != dev.scale_ptr:
@@ -1561,7 +1673,11 @@ class _LaunchPlan:
             if scale_ref != dev.scale_ref:
                 dev.refs[:, _COL["grad_scale"]] = scale_ref
                 dev.scale_ref = scale_ref
-            launches.append((params, written, read, dev.table_t, dev.refs_t, []))
+            if records:
+                read = [p.grad for p in params]
+                if coef is not None:
+                    read.append(coef)
+                launches.append((params, written, read, dev.table_t, dev.refs_t, []))
 
         def finish(done: int, total: int) -> None:
             if done == total:
@@ -1572,7 +1688,7 @@ class _LaunchPlan:
                 for s, offset in saved_streams:
                     s.offset = offset
 
-        return launches, finish
+        return (launches if records else None), finish
 
 
 class AdamW8bit(QuantizedAdamW):

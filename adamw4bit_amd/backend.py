@@ -20,8 +20,9 @@ This class keeps that contract with this package's launch preparation and HIP ke
   its positions from, and advances, the generator's offset, so the reference's checkpoint of its
   generators resumes the stream exactly.  The draws equal those of this package's own
   ``QuantizedAdamW`` with the same seed;
-* parameters the kernels do not take (on the CPU, float64, gradients of other dtypes) go to the
-  reference's own ``OptimizedBackend``, whose answer is returned.
+* parameters the kernels do not take (on the CPU, of a dtype other than float32, bfloat16, float16
+  and float64, with a gradient of another dtype) go to the reference's own ``OptimizedBackend``,
+  whose answer is returned.
 
 Each accepted parameter is launched at once (``deferred=False``), or, with ``deferred=True``, the
 accepted parameters of a step are prepared one by one and launched together by ``flush(optimizer)``

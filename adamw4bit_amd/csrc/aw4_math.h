@@ -23,6 +23,7 @@ namespace aw4 {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef double f64x2 __attribute__((ext_vector_type(2)));
 
 template <class T>
 using gptr = __attribute__((address_space(1))) T*;

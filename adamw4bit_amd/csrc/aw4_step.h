@@ -14,8 +14,9 @@ constexpr int kTilesPerWave = 4;                    // consecutive wave tiles on
 constexpr int kThreads = 256;
 constexpr int kWavesPerGroup = kThreads / 64;
 
-// Parameter/gradient storage kinds (AW4_F32 / AW4_BF16 / AW4_F16) and "any" (run time).
-enum : int { D_F32 = AW4_F32, D_BF16 = AW4_BF16, D_F16 = AW4_F16, D_ANY = 7 };
+// Parameter/gradient storage kinds (AW4_F32 / AW4_BF16 / AW4_F16 / AW4_F64) and "any" (run
+// time).  Specialised kernels take the first three; float64 runs the generic kernels only.
+enum : int { D_F32 = AW4_F32, D_BF16 = AW4_BF16, D_F16 = AW4_F16, D_F64 = AW4_F64, D_ANY = 7 };
 
 // Launch table staged in device memory: header, tensors[count], tile_start[count + 1].
 struct StepHeader {
@@ -129,12 +130,45 @@ __device__ __forceinline__ void clip_grads(const aw4_tensor& T, float* g, int n)
     }
 }
 
-// Run-time dtype dispatch for the generic kernel (D_ANY): loads convert to fp32 words.
+// float64 values: 4 at element e (vec: two 16-byte accesses).
+__device__ __forceinline__ void load_f64x4(uint64_t base, int64_t e, bool vec, double (&d)[4]) {
+    const gptr<const double> p = gaddr<const double>(base) + e;
+    if (vec) {
+        const f64x2 a = __builtin_nontemporal_load((gptr<const f64x2>)p);
+        const f64x2 b = __builtin_nontemporal_load((gptr<const f64x2>)(p + 2));
+        d[0] = a.x; d[1] = a.y; d[2] = b.x; d[3] = b.y;
+    } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) d[t] = p[t];
+    }
+}
+
+__device__ __forceinline__ void store_f64x4(uint64_t base, int64_t e, bool vec, const double (&d)[4]) {
+    const gptr<double> p = gaddr<double>(base) + e;
+    if (vec) {
+        __builtin_nontemporal_store(f64x2{d[0], d[1]}, (gptr<f64x2>)p);
+        __builtin_nontemporal_store(f64x2{d[2], d[3]}, (gptr<f64x2>)(p + 2));
+    } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) p[t] = d[t];
+    }
+}
+
+// Run-time dtype dispatch for the generic kernel (D_ANY): loads convert to fp32 words (a
+// float64 gradient rounded to nearest, as gradient.to(float32)).  A float64 parameter is not
+// loaded here: its update reads it in float64 (update_quarter).
 __device__ __forceinline__ void load_words_any(int dtype, uint64_t base, int64_t e, bool vec, uint32_t* w) {
     uint32_t r[4];
     float f[4];
     if (dtype == D_F32) {
         load_words<D_F32>(base, e, vec, w);
+        return;
+    }
+    if (dtype == D_F64) {
+        double d[4];
+        load_f64x4(base, e, vec, d);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) w[t] = f2u((float)d[t]);
         return;
     }
     if (dtype == D_BF16) {
@@ -176,6 +210,22 @@ __device__ __forceinline__ float param_apply(const aw4_tensor& T, float p1, floa
 template <int D>
 __device__ __forceinline__ float param_update(const aw4_tensor& T, float p, float m1, float m2) {
     return param_apply(T, round_to_storage<D>(p * T.decay), m1, m2);
+}
+
+// A float64 parameter (AW4_F64; the reference's eager chunk update, _optimized.py:219-222): the
+// fp32 denominator fp32(sqrt(m2)) / fp32(sqrt(bc2)) + fp32(eps) (a true division, as ATen's
+// div_ by a Python scalar), then p = p * (1 - lr*wd) and p = p + ((-lr/bc1) * m1) / den with
+// m1 and den widened, every operation rounded to float64 (ATen's CPU addcdiv order; hipcc
+// contracts nothing and divides float64 correctly rounded).  The root is the correctly rounded
+// one, which ATen's CPU root also gives on all but a few percent of inputs (1 ulp below it
+// there); v_sqrt_f32 alone is off by an ulp far more often, and a float64 parameter shows it.
+__device__ __forceinline__ float denominator_f64_param(const aw4_tensor& T, float m2) {
+    return div_cr(sqrt_cr(m2), T.bc2_sqrt) + T.eps;
+}
+
+__device__ __forceinline__ double param_update_f64(const aw4_tensor& T, double p, float m1, float den) {
+    const double p1 = p * T.decay_f64;
+    return p1 + (T.step_coef_f64 * (double)m1) / (double)den;
 }
 
 // The decayed parameters p * (1 - lr*wd) of 4 values, rounded to storage (bf16: one conversion
@@ -279,7 +329,7 @@ __device__ __forceinline__ void load_tile(const aw4_tensor& T, const TileLane& t
         if constexpr (D == D_ANY) {
             const int64_t e = tl.blk0 * kBlock + off;
             load_words_any(T.grad_dtype, T.grad, e, vec, &in.g[4 * q]);
-            load_words_any(T.param_dtype, T.param, e, vec, &in.p[4 * q]);
+            if (T.param_dtype != D_F64) load_words_any(T.param_dtype, T.param, e, vec, &in.p[4 * q]);
         } else {
             load_words<D>(tile_values<D>(T.grad, tl.blk0), off, true, &in.g[In::kW * q]);
             load_words<D>(tile_values<D>(T.param, tl.blk0), off, true, &in.p[In::kW * q]);
@@ -360,10 +410,11 @@ __device__ __forceinline__ void update_quarter(const aw4_tensor& T, int q, const
                                                float (&m1)[16], M2Sink& m2, float* p1, const float* la_prior) {
     using In = TileInputs<M1K, M2K, D>;
     constexpr int DC = D == D_ANY ? D_F32 : D;  // generic loads are already fp32 words
+    constexpr bool kF64 = DP == D_F64;  // the parameter is read, updated and stored in float64 below
     float g[4], p[4], a[4], b[4];
     words_to_f32<DC>(&in.g[In::kW * q], g);
     clip_grads<D>(T, g, 4);
-    words_to_f32<DC>(&in.p[In::kW * q], p);
+    if constexpr (!kF64) words_to_f32<DC>(&in.p[In::kW * q], p);
     if (moment_quantized<M1K>(T.m1)) {
         if constexpr (In::kQ1) decode4(L1.dec, in.c1[q >> 1] >> (16 * (q & 1)), in.s1, a);
     } else {
@@ -382,7 +433,7 @@ __device__ __forceinline__ void update_quarter(const aw4_tensor& T, int q, const
     }
     const bool large1 = (T.flags & AW4_TENSOR_LERP1_LARGE) != 0, large2 = (T.flags & AW4_TENSOR_LERP2_LARGE) != 0;
     float pd[4];
-    decay4<DP>(T, p, pd);
+    if constexpr (!kF64) decay4<DP>(T, p, pd);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
         if constexpr (kGenericLerp) {
@@ -394,14 +445,28 @@ __device__ __forceinline__ void update_quarter(const aw4_tensor& T, int q, const
         }
         if (la_prior)
             b[t] = __builtin_fmaf((float)T.m2.la_fresh_weight * g[t], g[t], la_prior[4 * q + t] * (float)T.m2.la_beta2);
-        if constexpr (kDefer) p1[4 * q + t] = pd[t];
-        else p[t] = param_apply(T, pd[t], a[t], b[t]);
+        if constexpr (kF64) {
+            if constexpr (!kDefer) p[t] = denominator_f64_param(T, b[t]);  // the update follows the store of m2
+        } else if constexpr (kDefer) {
+            p1[4 * q + t] = pd[t];
+        } else {
+            p[t] = param_apply(T, pd[t], a[t], b[t]);
+        }
         m1[4 * q + t] = a[t];
     }
     m2.put(q, b);
     if (!kDefer && tl.active) {
         const uint32_t off = tl.voff + 32u * q;
-        if constexpr (D == D_ANY) {
+        if constexpr (kF64) {
+            // (the generic kernel: D_ANY) p holds the denominators
+            const bool vec = (T.flags & AW4_TENSOR_VEC_ALIGNED) != 0;
+            const int64_t e = tl.blk0 * kBlock + off;
+            double v[4];
+            load_f64x4(T.param, e, vec, v);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) v[t] = param_update_f64(T, v[t], a[t], p[t]);
+            store_f64x4(T.param, e, vec, v);
+        } else if constexpr (D == D_ANY) {
             const bool vec = (T.flags & AW4_TENSOR_VEC_ALIGNED) != 0;
             const int64_t e = tl.blk0 * kBlock + off;
             if (T.param_dtype == D_F32) store_f32<D_F32>(T.param, e, vec, p);
@@ -438,7 +503,9 @@ __device__ __forceinline__ void update_tile_any(const aw4_tensor& T, const TileL
         if (T.param_dtype == D_F32) update_tile<M1K, M2K, D, D_F32, kDefer>(T, in, L1, L2, tl, m1, m2, p1, la_prior);
         else if (T.param_dtype == D_BF16)
             update_tile<M1K, M2K, D, D_BF16, kDefer>(T, in, L1, L2, tl, m1, m2, p1, la_prior);
-        else update_tile<M1K, M2K, D, D_F16, kDefer>(T, in, L1, L2, tl, m1, m2, p1, la_prior);
+        else if (T.param_dtype == D_F16)
+            update_tile<M1K, M2K, D, D_F16, kDefer>(T, in, L1, L2, tl, m1, m2, p1, la_prior);
+        else update_tile<M1K, M2K, D, D_F64, kDefer>(T, in, L1, L2, tl, m1, m2, p1, la_prior);
     } else {
         update_tile<M1K, M2K, D, D, kDefer>(T, in, L1, L2, tl, m1, m2, p1, la_prior);
     }
@@ -464,7 +531,8 @@ __device__ __forceinline__ void tile_grads(const aw4_tensor& T, const TileInputs
 // block's LDS stage (scale: the stored one, or with AW4_MOMENT_READ_RAW_SCALE the one before
 // EDEN, adamw.py:615-635), d = sqrt(v) / sqrt(bc2) + eps, p = p1 + (step_coef * m1) / d
 // (correctly rounded divisions, as the reference's), and 1 / d to M.values when it is set
-// (m2_read_preconditioner, adamw.py:632).
+// (m2_read_preconditioner, adamw.py:632).  A float64 parameter (DP = D_F64; p1 is not used) is
+// read here and updated in float64 (param_update_f64).
 template <int DP>
 __device__ __forceinline__ void sampled_read_update(const aw4_tensor& T, const TileLane& tl, const MomentTables& L2,
                                                     BlockScratch sc, BlockScales bs, const float (&m1)[16],
@@ -473,19 +541,28 @@ __device__ __forceinline__ void sampled_read_update(const aw4_tensor& T, const T
     const float scale = (T.m2.flags & AW4_MOMENT_READ_RAW_SCALE) ? bs.raw : stored;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        float v[4], p[4], pre[4];
+        float v[4], p[4], pre[4], den[4];
         decode4(L2.dec, sc.stage[8 * q + tl.j], scale, v);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            const float sq = sqrt_faithful(v[t]);
+            const float sq = DP == D_F64 ? sqrt_cr(v[t]) : sqrt_faithful(v[t]);  // see denominator_f64_param
             const float d = __builtin_amdgcn_div_fixupf(div_by_rcp(sq, T.bc2_sqrt, T.bc2_sqrt_rcp), T.bc2_sqrt, sq) + T.eps;
-            p[t] = p1[4 * q + t] + div_cr(T.step_coef * m1[4 * q + t], d);
+            if constexpr (DP != D_F64) p[t] = p1[4 * q + t] + div_cr(T.step_coef * m1[4 * q + t], d);
+            den[t] = d;
             pre[t] = div_cr(1.0f, d);
         }
         if (tl.active) {
             const uint32_t off = tl.voff + 32u * q;
             const bool vec = (T.flags & AW4_TENSOR_VEC_ALIGNED) != 0;
-            store_f32<DP>(T.param, tl.blk0 * kBlock + off, vec, p);
+            if constexpr (DP == D_F64) {
+                double w[4];
+                load_f64x4(T.param, tl.blk0 * kBlock + off, vec, w);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) w[t] = param_update_f64(T, w[t], m1[4 * q + t], den[t]);
+                store_f64x4(T.param, tl.blk0 * kBlock + off, vec, w);
+            } else {
+                store_f32<DP>(T.param, tl.blk0 * kBlock + off, vec, p);
+            }
             if (T.m2.values)
                 *(gptr<f32x4>)(gaddr<float>(T.m2.values) + tl.blk0 * kBlock + off) = f32x4{pre[0], pre[1], pre[2], pre[3]};
         }
@@ -518,6 +595,7 @@ template <int D>
 __device__ __forceinline__ float load_value(const aw4_tensor& T, uint64_t base, int dtype, int64_t k) {
     const int dt = D == D_ANY ? dtype : D;
     if (dt == D_F32) return gaddr<const float>(base)[k];
+    if (D == D_ANY && dt == D_F64) return (float)gaddr<const double>(base)[k];
     const uint32_t h = gaddr<const uint16_t>(base)[k];
     return dt == D_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
 }
@@ -528,15 +606,18 @@ __device__ __forceinline__ void step_values_one(const aw4_tensor& T, int64_t k) 
     const gptr<float> v2 = gaddr<float>(T.m2.values);
     float g = load_value<D>(T, T.grad, T.grad_dtype, k);
     clip_grads<D>(T, &g, 1);
-    float p = load_value<D>(T, T.param, T.param_dtype, k);
+    const int dt = D == D_ANY ? T.param_dtype : D;
+    float p = dt == D_F64 ? 0.0f : load_value<D>(T, T.param, T.param_dtype, k);
     float a = v1[k], b = v2[k];
     const int lf = T.flags & (AW4_TENSOR_LERP1_LARGE | AW4_TENSOR_LERP2_LARGE);
     if (lf == 0) moments_update<false, false>(T, g, a, b);
     else if (lf == AW4_TENSOR_LERP1_LARGE) moments_update<true, false>(T, g, a, b);
     else if (lf == AW4_TENSOR_LERP2_LARGE) moments_update<false, true>(T, g, a, b);
     else moments_update<true, true>(T, g, a, b);
-    const int dt = D == D_ANY ? T.param_dtype : D;
-    if (dt == D_F32) {
+    if (D == D_ANY && dt == D_F64) {
+        const gptr<double> pp = gaddr<double>(T.param);
+        pp[k] = param_update_f64(T, pp[k], a, denominator_f64_param(T, b));
+    } else if (dt == D_F32) {
         p = param_update<D_F32>(T, p, a, b);
         gaddr<float>(T.param)[k] = p;
     } else if (dt == D_BF16) {
@@ -690,10 +771,11 @@ __device__ __forceinline__ void run_tiles(const StepHeader* hdr, const LdsT& lds
                     finish_moment<M1K, false>(T.m1, L1, tl, RegValues{m1}, ws);
                     prefetch();
                     const BlockScales bs = finish_moment<M2K, true>(T.m2, L2, tl, m2.values(), ws);
-                    if (T.param_dtype == D_F32) sampled_read_update<D_F32>(T, tl, L2, ws.block(tl.grp), bs, m1, p1);
-                    else if (T.param_dtype == D_BF16)
-                        sampled_read_update<D_BF16>(T, tl, L2, ws.block(tl.grp), bs, m1, p1);
-                    else sampled_read_update<D_F16>(T, tl, L2, ws.block(tl.grp), bs, m1, p1);
+                    const int dp = D == D_ANY ? T.param_dtype : D;  // a specialised kernel's own dtype
+                    if (dp == D_F32) sampled_read_update<D_F32>(T, tl, L2, ws.block(tl.grp), bs, m1, p1);
+                    else if (dp == D_BF16) sampled_read_update<D_BF16>(T, tl, L2, ws.block(tl.grp), bs, m1, p1);
+                    else if (dp == D_F16) sampled_read_update<D_F16>(T, tl, L2, ws.block(tl.grp), bs, m1, p1);
+                    else if (D == D_ANY) sampled_read_update<D_F64>(T, tl, L2, ws.block(tl.grp), bs, m1, p1);
                   }
                 }
                 if constexpr (kind_of(M2K) == K_ANY || kind_of(M2K) == K_LA) {

@@ -58,7 +58,7 @@ namespace {
 using namespace aw4;
 
 static_assert(sizeof(aw4_moment) == 104, "aw4_moment layout");
-static_assert(sizeof(aw4_tensor) == 280, "aw4_tensor layout");
+static_assert(sizeof(aw4_tensor) == 296, "aw4_tensor layout");
 
 // Codebooks as fp32 bit patterns (ascending; code = index).  Values of the reference's
 // closed forms: NF4 table (quantization.py:401-422), signed and unsigned dynamic maps
@@ -607,15 +607,20 @@ int check_tensor(const aw4_tensor& t, int index) {
     if (!t.param || !t.grad) return set_error(AW4_EINVAL, "tensor %d: null param or grad", index);
     if (t.numel <= 0) return set_error(AW4_EINVAL, "tensor %d: numel %lld", index, (long long)t.numel);
     for (int dt : {t.param_dtype, t.grad_dtype})
-        if (dt != AW4_F32 && dt != AW4_BF16 && dt != AW4_F16)
+        if (dt != AW4_F32 && dt != AW4_BF16 && dt != AW4_F16 && dt != AW4_F64)
             return set_error(AW4_EINVAL, "tensor %d: dtype %d", index, dt);
     if (t.flags & AW4_TENSOR_VEC_ALIGNED) {
-        const uint64_t pa = t.param_dtype == AW4_F32 ? 16 : 8, ga = t.grad_dtype == AW4_F32 ? 16 : 8;
+        // 4-value vector access: 16 bytes (fp32, and float64 as two 16-byte halves) or 8 bytes
+        const uint64_t pa = t.param_dtype == AW4_F32 || t.param_dtype == AW4_F64 ? 16 : 8;
+        const uint64_t ga = t.grad_dtype == AW4_F32 || t.grad_dtype == AW4_F64 ? 16 : 8;
         if (!aligned(t.param, pa) || !aligned(t.grad, ga))
             return set_error(AW4_EALIGN, "tensor %d: VEC_ALIGNED but param/grad misaligned", index);
     }
-    if ((t.flags & AW4_TENSOR_GRAD_SCALE) && (!t.grad_scale || !aligned(t.grad_scale, 4)))
-        return set_error(AW4_EINVAL, "tensor %d: GRAD_SCALE without a 4-byte aligned grad_scale", index);
+    const bool scaled = (t.flags & (AW4_TENSOR_GRAD_SCALE | AW4_TENSOR_GRAD_UNSCALE)) != 0;
+    if (scaled && (!t.grad_scale || !aligned(t.grad_scale, 4)))
+        return set_error(AW4_EINVAL, "tensor %d: GRAD_SCALE/GRAD_UNSCALE without a 4-byte aligned grad_scale", index);
+    if (scaled && t.grad_dtype == AW4_F64)
+        return set_error(AW4_EINVAL, "tensor %d: GRAD_SCALE/GRAD_UNSCALE with a float64 gradient", index);
     int rc = check_moment(t.m1, t.numel, index, "m1");
     if (rc) return rc;
     return check_moment(t.m2, t.numel, index, "m2");

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define AW4_ABI_VERSION 6
+#define AW4_ABI_VERSION 7
 #define AW4_BLOCK 128 /* values per block scale (quantization.py:694-703, 4-bit default) */
 
 /* Error codes. */
@@ -94,6 +94,11 @@ extern "C" {
 #define AW4_F32 0
 #define AW4_BF16 1
 #define AW4_F16 2
+/* float64 (the reference's optimized backend takes float64 parameters, _optimized.py:99): the
+ * gradient is read as fp32(g) (gradient.to(float32), _optimized.py:215), the moments and the
+ * denominator are fp32 as for every dtype, and the parameter is updated in float64 with
+ * decay_f64 and step_coef_f64.  Not with AW4_TENSOR_GRAD_SCALE / AW4_TENSOR_GRAD_UNSCALE. */
+#define AW4_F64 3
 
 /* aw4_tensor.flags */
 #define AW4_TENSOR_LERP1_LARGE 0x1 /* lerp weight 1-beta1 >= 0.5: m1 = fma(w-1, g-m1, g) */
@@ -143,7 +148,10 @@ typedef struct aw4_moment {
  * ATen kernels see (_optimized.py:168-173, :215-222):
  *   w1 = fp32(1-beta1) (or fp32(1-beta1) - 1 with LERP1_LARGE), w2 likewise,
  *   decay = fp32(1 - lr*wd), step_coef = fp32(-lr/bc1),
- *   bc2_sqrt = fp32(sqrt(bc2)), bc2_sqrt_rcp = RN(1/bc2_sqrt), eps = fp32(eps).
+ *   bc2_sqrt = fp32(sqrt(bc2)), bc2_sqrt_rcp = RN(1/bc2_sqrt), eps = fp32(eps);
+ * and for an AW4_F64 parameter the float64 values themselves:
+ *   decay_f64 = 1 - lr*wd, step_coef_f64 = -lr/bc1
+ * (p = p * decay_f64, then p = p + (step_coef_f64 * m1) / den in float64, _optimized.py:221-222).
  */
 typedef struct aw4_tensor {
     uint64_t param;      /* device address, contiguous, param_dtype[numel]; updated in place */
@@ -151,13 +159,14 @@ typedef struct aw4_tensor {
     uint64_t grad_scale; /* device address of the float pair {u, c} (AW4_TENSOR_GRAD_UNSCALE /
                             AW4_TENSOR_GRAD_SCALE) or 0 */
     int64_t numel;
-    int32_t param_dtype; /* AW4_F32 / AW4_BF16 / AW4_F16 */
+    int32_t param_dtype; /* AW4_F32 / AW4_BF16 / AW4_F16 / AW4_F64 */
     int32_t grad_dtype;
     int32_t flags;       /* AW4_TENSOR_* */
     float w1, w2, decay, step_coef, bc2_sqrt, bc2_sqrt_rcp, eps;
     aw4_moment m1;
     aw4_moment m2;
-} aw4_tensor; /* 280 bytes */
+    double decay_f64, step_coef_f64; /* AW4_F64 parameters (else unused) */
+} aw4_tensor; /* 296 bytes */
 
 /* Library ABI version (AW4_ABI_VERSION of the build). */
 int aw4_abi_version(void);
@@ -169,7 +178,7 @@ const char* aw4_last_error(void);
  * One fused AdamW step over `count` parameters on `stream` (a hipStream_t;
  * 0 = legacy default stream): one kernel launch per group of parameters that
  * share a kernel (one launch for a recipe's parameters).  `tensors` is a host
- * array: a group of up to 12 parameters on the ZE-EDEN or ZIP-SR kernels
+ * array: a group of up to 11 parameters on the ZE-EDEN or ZIP-SR kernels
  * receives its rows in its launch's arguments, any other step's rows are
  * staged to device memory by the library (the call returns before the step
  * completes, stream-ordered like any HIP launch).
@@ -186,7 +195,7 @@ int aw4_fused_step(const aw4_tensor* tensors, int32_t count, void* stream);
  * tables (the step's only device memory besides the caller's tensors) go to a fixed area of
  * AW4_NOALLOC_TABLE_BYTES that the library holds in a file-scope device array on each GPU
  * until the process ends, and reach it through the arguments of small copy kernels on
- * `stream`.  A call whose tables exceed that area (about 3,700 tensors) fails with AW4_EINVAL.
+ * `stream`.  A call whose tables exceed that area (about 3,400 tensors) fails with AW4_EINVAL.
  * The first call on a device (of any entry point) copies the codebook tables to it once,
  * synchronously.  Every call on one GPU uses the same area: calls on one stream are ordered,
  * calls that overlap on different streams of one GPU race.

@@ -123,7 +123,7 @@ int main(void) {
   P(aw4_tensor, param) P(aw4_tensor, grad) P(aw4_tensor, grad_scale) P(aw4_tensor, numel) P(aw4_tensor, param_dtype)
   P(aw4_tensor, grad_dtype) P(aw4_tensor, flags) P(aw4_tensor, w1) P(aw4_tensor, w2) P(aw4_tensor, decay)
   P(aw4_tensor, step_coef) P(aw4_tensor, bc2_sqrt) P(aw4_tensor, bc2_sqrt_rcp) P(aw4_tensor, eps)
-  P(aw4_tensor, m1) P(aw4_tensor, m2)
+  P(aw4_tensor, m1) P(aw4_tensor, m2) P(aw4_tensor, decay_f64) P(aw4_tensor, step_coef_f64)
   return 0;
 }
 """
@@ -370,7 +370,7 @@ def test_plan_step_view_covers_exactly_the_per_step_fields():
     from adamw4bit_amd import _lib
     from adamw4bit_amd.adamw import _STEP_FIELDS, _STEP_WORDS
     T = _lib.TENSOR
-    assert _STEP_FIELDS.itemsize == T.itemsize == 280 and _STEP_WORDS.itemsize == 32
+    assert _STEP_FIELDS.itemsize == T.itemsize == 296 and _STEP_WORDS.itemsize == 32
     row = np.zeros(2, dtype=T)
     raw = row.view(np.uint8).reshape(2, -1)
     raw[:] = 0xA5
@@ -385,7 +385,9 @@ def test_plan_step_view_covers_exactly_the_per_step_fields():
     view["m2_rng_seed"] = [33, 34]
     view["m1_rng_offset"] = [21, 22]
     view["m2_rng_offset"] = [23, 24]
+    view["f64"] = [(0.999, -2.5e-4), (0.998, -3.5e-4)]
     assert list(row["grad"]) == [11, 12] and list(row["grad_scale"]) == [13, 14]
+    assert list(row["decay_f64"]) == [0.999, 0.998] and list(row["step_coef_f64"]) == [-2.5e-4, -3.5e-4]
     assert list(row["flags"]) == [3, 3]
     for name, value in zip(("w1", "w2", "decay", "step_coef", "bc2_sqrt", "bc2_sqrt_rcp", "eps"),
                            (0.5, 0.25, 0.75, -1e-3, 0.125, 8.0, 1e-8)):
@@ -399,7 +401,7 @@ def test_plan_step_view_covers_exactly_the_per_step_fields():
     for name in _STEP_FIELDS.names:
         dt, off = _STEP_FIELDS.fields[name][:2]
         written[off:off + dt.itemsize] = True
-    assert written.sum() == 8 + 8 + 32 + 12 + 4 * 8
+    assert written.sum() == 8 + 8 + 32 + 12 + 4 * 8 + 16
     assert np.array_equal(raw[:, ~written], before[:, ~written])
 
 
@@ -418,3 +420,23 @@ def test_noalloc_step_rejects_tables_beyond_its_area():
     rows["numel"][7] = 0
     assert lib.aw4_fused_step_noalloc(rows.ctypes.data, len(rows), None) == _lib.EINVAL
     assert b"tensor 7: numel 0" in lib.aw4_last_error()
+
+
+def test_step_rejects_unknown_dtypes_and_scaled_float64_gradients():
+    """Rows are checked before any device work (no GPU needed): a dtype code outside
+    AW4_F32/BF16/F16/F64 fails, and so does a float64 gradient with GRAD_SCALE or GRAD_UNSCALE (the
+    prologue's coefficients are fp32 products of fp32/bf16/fp16 gradients)."""
+    lib = _lib.library()
+    rows = np.zeros(1, dtype=_lib.TENSOR)
+    rows["param"], rows["grad"], rows["numel"], rows["grad_scale"] = 1 << 20, 2 << 20, 256, 5 << 20
+    rows["param_dtype"] = rows["grad_dtype"] = _lib.F64
+    rows["m1"]["values"], rows["m2"]["values"] = 3 << 20, 4 << 20
+    rows["m1"]["rounding"] = rows["m2"]["rounding"] = _lib.ROUND_FP32
+    for flag in (_lib.TENSOR_GRAD_SCALE, _lib.TENSOR_GRAD_UNSCALE):
+        rows["flags"] = flag
+        assert lib.aw4_fused_step(rows.ctypes.data, 1, None) == _lib.EINVAL
+        assert b"tensor 0: GRAD_SCALE/GRAD_UNSCALE with a float64 gradient" in lib.aw4_last_error()
+    rows["flags"] = 0
+    rows["param_dtype"] = 4
+    assert lib.aw4_fused_step(rows.ctypes.data, 1, None) == _lib.EINVAL
+    assert b"tensor 0: dtype 4" in lib.aw4_last_error()

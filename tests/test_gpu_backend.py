@@ -25,8 +25,8 @@ from tests.test_backend_host import StubReferenceBackend
 pytestmark = pytest.mark.gpu
 
 HYPER = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
-SHAPES = [(256, 512), (768,), (64, 4096), (1000,)]
-DTYPES = [torch.float32, torch.float32, torch.bfloat16, torch.float32]
+SHAPES = [(256, 512), (768,), (64, 4096), (1000,), (128, 256)]
+DTYPES = [torch.float32, torch.float64, torch.bfloat16, torch.float32, torch.float64]
 
 
 def same(oa, pa, ob, pb, what):
@@ -90,6 +90,7 @@ def test_reference_optimizer_steps_like_the_package_optimizer(deferred):
         own.step()
         resumed.step()
         torch.cuda.synchronize()
+        assert resumed.declined == []
         for i, (a, b, c) in enumerate(zip(pa, pb, pc)):
             same(ref, a, own, b, ("continued", k, i))
             same(ref, a, resumed, c, ("resumed", k, i))

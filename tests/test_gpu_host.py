@@ -251,16 +251,16 @@ def test_aliased_state_after_load_takes_reference_step(tmp_path):
 # ---------------------------------------------------------------------------
 
 def test_rejected_parameter_leaves_every_state_untouched():
-    """A parameter the step cannot take (float64), listed after one it can, raises before any
+    """A parameter the step cannot take (complex64), listed after one it can, raises before any
     state changes: the first parameter is not initialised, no stream moved."""
     log("rejected parameter: no state change")
     good = torch.nn.Parameter(torch.randn(64, 128, device=H.DEVICE) * 0.02)
-    bad = torch.nn.Parameter(torch.randn(64, 128, device=H.DEVICE, dtype=torch.float64))
+    bad = torch.nn.Parameter(torch.randn(64, 128, device=H.DEVICE, dtype=torch.complex64))
     opt = aw.ZIPSRAdamW4Bit([good, bad], optimized=True, quant_rng_seed=1, **ARGS)
     good.grad = torch.randn_like(good) * 1e-3
     bad.grad = torch.randn_like(bad) * 1e-3
     before = good.detach().clone()
-    with pytest.raises(NotImplementedError, match="float64"):
+    with pytest.raises(NotImplementedError, match="complex64"):
         opt.step()
     torch.cuda.synchronize()
     assert len(opt.state[good]) == 0
@@ -419,8 +419,8 @@ def test_unseeded_draws_follow_torch_generator(monkeypatch):
     from adamw4bit_amd.adamw import _LaunchPlan
     prepare, planned = _LaunchPlan.prepare, []
 
-    def counting(self, opt):
-        out = prepare(self, opt)
+    def counting(self, opt, records=True):
+        out = prepare(self, opt, records)
         planned.append(out is not None)
         return out
 
@@ -598,6 +598,29 @@ def test_fused_unscale_of_bf16_gradients():
             same_state(oa, a, ob, b, (k, i))
         oa.zero_grad()
         ob.zero_grad()
+
+
+def test_fused_clip_refuses_float64_gradients():
+    """The fused clip and unscale read fp32/bf16/fp16 gradients; with a float64 gradient they
+    raise before any device work, nothing is left pending, and the step still takes the float64
+    parameter (unclipped)."""
+    log("fused clip with a float64 gradient")
+    p = torch.nn.Parameter(torch.randn(64, 256, device=H.DEVICE, dtype=torch.float64) * 0.02)
+    q = torch.nn.Parameter(torch.randn(64, 256, device=H.DEVICE) * 0.02)
+    opt = aw.ZIPSRAdamW4Bit([p, q], optimized=True, quant_rng_seed=2, **ARGS)
+    p.grad = torch.randn_like(p) * 1e-3
+    q.grad = torch.randn_like(q) * 1e-3
+    scaler = torch.amp.GradScaler("cuda", init_scale=4.0)
+    scaler.scale(torch.ones((), device=H.DEVICE))
+    for call in (lambda: opt.clip_grad_norm_(1.0), lambda: opt.clip_grad_norm_(1.0, grad_scaler=scaler),
+                 lambda: opt.unscale_grads_(scaler)):
+        with pytest.raises(NotImplementedError, match="float32/bfloat16/float16 gradients"):
+            call()
+        assert opt._grad_clip is None
+    before = p.detach().clone()
+    opt.step()
+    torch.cuda.synchronize()
+    assert opt.state[p]["step"] == 1 and not torch.equal(p.detach(), before)
 
 
 # ---------------------------------------------------------------------------
