@@ -831,11 +831,14 @@ int fill_step_tables(const aw4_tensor* tensors, StepLaunch& sl, int num_cus, voi
             acc += (rows[k].numel + kWaveTile - 1) / kWaveTile;
         }
         starts[n] = acc;
-        // Small launches take fewer tiles per wave so that their waves still spread over every
-        // CU: 3 or 4 tiles per wave from 128 tiles per CU, 2 from 8, else 1 (measured on one
-        // 4096^2 and one 1024^2 tensor, and the GPT-2-small list).
+        // Smaller launches take fewer tiles per wave so that their waves still spread over every
+        // CU: from 128 tiles per CU 3 or 4; below, one per 16 tiles per CU (16 waves per CU, the
+        // four 256-thread workgroups the recipe kernels keep resident: one round of waves), at
+        // least 1.  Measured on one 4096^2 ZIP-SR tensor (64 tiles per CU): 4 tiles per wave
+        // 52.1-52.2 us, 2 52.7-52.9, 3 56.4-56.6, 1 57.1-57.3; one 1024^2 tensor (4 per CU): 1.
         const int64_t per_cu = acc / (int64_t)num_cus;
-        const int tiles_per_wave = per_cu >= 128 ? large_tiles_per_wave(lg.variant) : per_cu >= 8 ? 2 : 1;
+        const int tiles_per_wave = per_cu >= 128 ? large_tiles_per_wave(lg.variant)
+                                                 : (int)std::max<int64_t>(1, std::min<int64_t>(4, per_cu / 16));
         const int64_t waves = (acc + tiles_per_wave - 1) / tiles_per_wave;
         sl.grid[g] = (waves + kWavesPerGroup - 1) / kWavesPerGroup;
         if (sl.grid[g] > 0x7fffffff)

@@ -383,12 +383,14 @@ def time_blocks(recipes, steps: int, warmup: int, stream) -> dict:
 
 
 def time_single_tensors(device, stream) -> dict:
-    """The two single-tensor workloads, each timed through ``step()`` after 10 untimed steps:
-    ZE-EDEN on one fp32 1024x1024 parameter with fresh seeded N(0, 1e-3) gradients each step
-    (100 timed steps), and ZIP-SR (quant_rng_seed=0) on one fp32 4096x4096 parameter with the
-    heavy-tailed gradients (20 timed steps).  The timed steps run back to back between one pair of
-    HIP events on the launch stream (host time shows where it exceeds the kernel's; events between
-    the steps would add their own work to them) and the wall clock; per step: their time / steps."""
+    """The two single-tensor workloads, each timed through ``step()``: ZE-EDEN on one fp32
+    1024x1024 parameter with fresh seeded N(0, 1e-3) gradients each step (100 timed steps after
+    10 untimed ones, the reference's protocol for it), and ZIP-SR (quant_rng_seed=0) on one fp32
+    4096x4096 parameter with the heavy-tailed gradients (100 timed steps after 100 untimed ones:
+    its first tens of steps after a launch of another size run up to 10% slower).  The timed
+    steps run back to back between one pair of HIP events on the launch stream (host time shows
+    where it exceeds the kernel's; events between the steps would add their own work to them)
+    and the wall clock; per step: their time / steps."""
     import torch
 
     import adamw4bit_amd as aw
@@ -396,20 +398,21 @@ def time_single_tensors(device, stream) -> dict:
     hyper = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True)
     out = {}
     gen = torch.Generator(device=device).manual_seed(7)
-    for name, shape, make, steps, fresh in (
-            ("zeeden_1024x1024", SMALL_SHAPE, lambda ps: aw.ZEEDENAdamW4Bit(ps, **hyper), SMALL_STEPS, True),
-            ("zipsr_4096x4096", (4096, 4096), lambda ps: aw.ZIPSRAdamW4Bit(ps, quant_rng_seed=0, **hyper), 20,
+    for name, shape, make, warmup, steps, fresh in (
+            ("zeeden_1024x1024", SMALL_SHAPE, lambda ps: aw.ZEEDENAdamW4Bit(ps, **hyper), SMALL_WARMUP, SMALL_STEPS,
+             True),
+            ("zipsr_4096x4096", (4096, 4096), lambda ps: aw.ZIPSRAdamW4Bit(ps, quant_rng_seed=0, **hyper), 100, 100,
              False)):
         p = torch.nn.Parameter(torch.randn(shape, generator=gen, device=device) * 0.02)
         opt = make([p])
         if fresh:
-            grads = [torch.randn(shape, generator=gen, device=device) * 1e-3 for _ in range(SMALL_WARMUP + steps)]
+            grads = [torch.randn(shape, generator=gen, device=device) * 1e-3 for _ in range(warmup + steps)]
         else:
-            grads = make_grads([shape], device, seed=11) * (SMALL_WARMUP + steps)
+            grads = make_grads([shape], device, seed=11) * (warmup + steps)
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         for k, g in enumerate(grads):
-            if k == SMALL_WARMUP:
+            if k == warmup:
                 torch.cuda.synchronize()
                 t0 = time.perf_counter()
                 a.record(stream)
@@ -420,7 +423,7 @@ def time_single_tensors(device, stream) -> dict:
         wall = (time.perf_counter() - t0) / steps
         ms = a.elapsed_time(b) / steps
         algo = math.prod(shape) * bytes_per_value(math.prod(shape))
-        out[name] = {"steps": steps, "warmup": SMALL_WARMUP, "event_ms_per_step": round(ms, 4),
+        out[name] = {"steps": steps, "warmup": warmup, "event_ms_per_step": round(ms, 4),
                      "wall_ms_per_step": round(wall * 1e3, 4),
                      "hbm_frac": round(algo / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         del opt, p, grads
