@@ -550,18 +550,21 @@ __device__ __forceinline__ void la_draws_quarter(const aw4_moment& M, int64_t bl
 }
 
 // Quick lookahead decision in fp32.  With r = sqrt(n), E = r / sqrt(bias) + eps, the rule's
-// P = (p(z) - p(q_hi)) / (p(q_lo) - p(q_hi)) is exactly
-//   (q_hi - z) (r_hi + r_lo) E_lo / ((q_hi - q_lo) (r_hi + r_z) E_z),
-// a quotient of positive factors without cancellation, which fp32 evaluates within about
-// 2^-18.5 of P.  The reference's float64 P itself is off by a few 2^-53 M, where
-// M = max(p_lo, 1) / (p_lo - p_hi) = (r_hi + r_lo) E_hi max(E_lo, 1) / (beta2 (q_hi - q_lo) / sqrt(bias)).
-// The decision u < P is sure outside the band 2^-16 max(P, 1) + 2^-46 M; values inside it, or
-// with M >= 2^36 (near the reference's switch to its value-linear form at 1e12), or with
-// n_lo below 2^-100 (where fp32 loses the small terms, and where p_lo = +inf makes the
-// reference's flat test true) take la_prob_lo.  rb = 1 / sqrt(bias) within 3 ulps; fresh within
-// 3 ulps of the reference's float64 term.
+// P = (p(z) - p(q_hi)) / (p(q_lo) - p(q_hi)) is exactly N / D with
+//   N = (q_hi - z) (r_hi + r_lo) E_lo,  D = (q_hi - q_lo) (r_hi + r_z) E_z,
+// positive factors without cancellation, which fp32 evaluates within about 2^-19 each.  The
+// decision u < P is taken without a division as the sign of T = u D - N (one fused rounding),
+// within about 2^-17.9 max(N, D) of D (u - P).  The reference's float64 P itself is off by a
+// few 2^-53 M, where M = max(p_lo, 1) / (p_lo - p_hi) and
+//   M D = (r_hi + r_lo) E_hi max(E_lo, 1) (r_hi + r_z) E_z sqrt(bias) / beta2
+// (the interval width cancels).  The decision is sure outside the band
+// |T| > 2^-16 max(N, D) + 2^-46 M D (that is, |u - P| > 2^-16 max(P, 1) + 2^-46 M); values
+// inside it, or with M >= 2^36 (near the reference's switch to its value-linear form at 1e12),
+// or with n_lo below 2^-100 (where fp32 loses the small terms, and where p_lo = +inf makes the
+// reference's flat test true) take la_prob_lo.  rb = 1 / sqrt(bias) and sb = sqrt(bias) / beta2
+// within a few ulps; fresh within 3 ulps of the reference's float64 term.
 struct LaQuick {
-    float beta2, rb, eps;
+    float beta2, rb, eps, sb;
 };
 __device__ __forceinline__ void la_quick(const LaQuick& k, float z, float a, float b, float s, float fresh, float U,
                                          bool& lower, bool& sure) {
@@ -575,16 +578,16 @@ __device__ __forceinline__ void la_quick(const LaQuick& k, float z, float a, flo
     const float e_z = __builtin_fmaf(r_z, k.rb, k.eps);
     const float d_hi = __builtin_fmaf(s, b, -z);
     const float w = s * (b - a);
-    const float s_lo = r_hi + r_lo;
+    const float s_lo = r_hi + r_lo, s_z = r_hi + r_z;
     const float num = (d_hi * s_lo) * e_lo;
-    const float den = (w * (r_hi + r_z)) * e_z;
-    const float p = num * rcp_faithful(den);
-    const float m = (s_lo * e_hi) * __builtin_fmaxf(e_lo, 1.0f) * rcp_faithful((k.beta2 * w) * k.rb);
-    const float band = __builtin_fmaf(0x1p-16f, __builtin_fmaxf(p, 1.0f), 0x1p-46f * m);
+    const float den = (w * s_z) * e_z;
+    const float md = (((s_lo * e_hi) * __builtin_fmaxf(e_lo, 1.0f)) * (s_z * e_z)) * k.sb;
     const float u = U * 0x1p-24f;
-    lower = u < p;
-    // comparisons with NaN are false: a NaN P or M is never sure
-    sure = (__builtin_fabsf(u - p) > band) & (m < 0x1p36f) & (n_lo >= 0x1p-100f);
+    const float t = __builtin_fmaf(u, den, -num);
+    const float band = __builtin_fmaf(0x1p-16f, __builtin_fmaxf(num, den), 0x1p-46f * md);
+    lower = t < 0.0f;
+    // comparisons with NaN are false: a NaN N, D or M D is never sure; D = 0 (M infinite) neither
+    sure = (__builtin_fabsf(t) > band) & (md < 0x1p36f * den) & (n_lo >= 0x1p-100f);
 }
 
 // Lookahead update-SR of this lane's 16 values z of block blk0 + grp (clamped at 0 first).
@@ -609,7 +612,9 @@ __device__ __forceinline__ BlockScales encode_block_la(const aw4_moment& M, cons
     const bool proxy = (M.flags & AW4_MOMENT_FRESH_PROXY) != 0;
     // the quick form needs the generator's 24-bit draws and finite, normal block scales
     const bool quick = wave_fast & ((M.flags & AW4_MOMENT_EXT_DRAWS) == 0);
-    const LaQuick lq{(float)M.la_beta2, rcp_faithful(sqrt_faithful((float)M.la_bias)), (float)M.la_eps};
+    const float sqrt_bias = sqrt_faithful((float)M.la_bias);
+    const LaQuick lq{(float)M.la_beta2, rcp_faithful(sqrt_bias), (float)M.la_eps,
+                     sqrt_bias * rcp_faithful((float)M.la_beta2)};
     const float wf = (float)M.la_fresh_weight;
     uint32_t rw[12];
     wave_lds_sync();  // the stage's previous contents have been read

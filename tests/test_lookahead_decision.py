@@ -5,17 +5,20 @@ level with probability P, computed in float64 from the pending value z, its leve
 q_lo = s*a, q_hi = s*b and the next step's second moments n(q) = beta2*q + fresh:
 P = (p(z) - p(q_hi)) / (p(q_lo) - p(q_hi)), p = 1 / (sqrt(n / bias) + eps), with a value-linear
 fallback where the interval is flat.  With r = sqrt(n) and E = r / sqrt(bias) + eps the same P
-is, exactly, (q_hi - z) (r_hi + r_lo) E_lo / ((q_hi - q_lo) (r_hi + r_z) E_z): positive factors
-without cancellation.  The kernel evaluates that form in fp32 and decides where the draw is
-farther from it than the band 2^-16 max(1, P) + 2^-46 M, M = max(p_lo, 1) / (p_lo - p_hi) (the
-reference's own float64 rounding grows with M), and sends every other value, and every value
-with M >= 2^36 (near the reference's flat switch at 1e12) or n_lo below 2^-100 (where fp32 loses
-small terms, and p_lo = +inf makes the reference's flat test true), to the float64 rule.  This
-test restates the quick form in numpy fp32 -- the fresh term as the kernel forms it,
+is, exactly, N / D with N = (q_hi - z) (r_hi + r_lo) E_lo and D = (q_hi - q_lo) (r_hi + r_z) E_z:
+positive factors without cancellation.  The kernel evaluates N and D in fp32 and, without a
+division, decides by the sign of T = u D - N where |T| exceeds the band
+2^-16 max(N, D) + 2^-46 M D (that is, |u - P| > 2^-16 max(1, P) + 2^-46 M, with
+M = max(p_lo, 1) / (p_lo - p_hi), whose product with D needs no division either: the reference's
+own float64 rounding grows with M), and sends every other value, and every value with
+M >= 2^36 (near the reference's flat switch at 1e12) or n_lo below 2^-100 (where fp32 loses small
+terms, and p_lo = +inf makes the reference's flat test true), to the float64 rule.  This test
+restates the quick form in numpy fp32 -- the fresh term as the kernel forms it,
 fp32(1 - beta2) * g * g, with gradients whose square underflows in fp32, its faithful operations
-one ulp off either way and 1/sqrt(bias) three ulps off -- and checks that wherever it is sure
-it agrees with the float64 rule; draws sit on both sides of the reference's probability, within
-4096 units of 2^-24, where a band 64 times narrower disagrees (planted below)."""
+one ulp off either way, 1/sqrt(bias) three ulps off and sqrt(bias)/beta2 four -- and checks that
+wherever it is sure it agrees with the float64 rule; draws sit on both sides of the reference's
+probability, within 4096 units of 2^-24, where a band 64 times narrower disagrees (planted
+below)."""
 
 from __future__ import annotations
 
@@ -73,18 +76,20 @@ def quick(z, a, b, s, g, beta2, bias, eps, U, rng, band_scale=1.0):
     d_hi = fma32(s, b, -z)
     w = (s * (b - a).astype(F32)).astype(F32)
     s_lo = (r_hi + r_lo).astype(F32)
+    s_z = (r_hi + r_z).astype(F32)
     num = ((d_hi * s_lo).astype(F32) * e_lo).astype(F32)
-    den = ((w * (r_hi + r_z).astype(F32)).astype(F32) * e_z).astype(F32)
-    p32 = (num * jitter((F32(1) / den).astype(F32), jit())).astype(F32)
-    # M = max(p_lo, 1) / (p_lo - p_hi) = (r_hi + r_lo) E_hi max(1, E_lo) / (beta2 w / sqrt(bias))
-    m = ((s_lo * e_hi).astype(F32) * np.maximum(e_lo, F32(1))).astype(F32) * jitter(
-        (F32(1) / ((beta32 * w).astype(F32) * rb).astype(F32)).astype(F32), jit())
-    band = (F32(2.0 ** -16 * band_scale) * np.maximum(p32, F32(1)) + F32(2.0 ** -46) * m).astype(F32)
+    den = ((w * s_z).astype(F32) * e_z).astype(F32)
+    # M D = (r_hi + r_lo) E_hi max(1, E_lo) (r_hi + r_z) E_z sqrt(bias) / beta2 (the width cancels)
+    sb = jitter(np.full(n, np.sqrt(bias) / beta2, F32), rng.integers(-4, 5, n))
+    md = ((((s_lo * e_hi).astype(F32) * np.maximum(e_lo, F32(1))).astype(F32) * (s_z * e_z).astype(F32)).astype(F32)
+          * sb).astype(F32)
     u = (U * F32(2.0 ** -24)).astype(F32)
+    t = fma32(u, den, -num)
+    band = fma32(np.full(n, 2.0 ** -16 * band_scale, F32), np.maximum(num, den), (F32(2.0 ** -46) * md).astype(F32))
     # n_lo below 2^-100 (fp32 loses small terms; p_lo = +inf when it is 0 with eps = 0, which
     # makes the reference's flat test true): the float64 rule
-    sure = (np.abs(u - p32) > band) & (m < F32(2.0 ** 36)) & (n_lo >= F32(2.0 ** -100))
-    return u < p32, sure
+    sure = (np.abs(t) > band) & (md < (F32(2.0 ** 36) * den).astype(F32)) & (n_lo >= F32(2.0 ** -100))
+    return t < 0, sure
 
 
 def sample(rng, n):
