@@ -578,10 +578,10 @@ __device__ __forceinline__ void la_quick(const LaQuick& k, float z, float a, flo
     const float e_z = __builtin_fmaf(r_z, k.rb, k.eps);
     const float d_hi = __builtin_fmaf(s, b, -z);
     const float w = s * (b - a);
-    const float s_lo = r_hi + r_lo, s_z = r_hi + r_z;
+    const float s_lo = r_hi + r_lo, sz_ez = (r_hi + r_z) * e_z;
     const float num = (d_hi * s_lo) * e_lo;
-    const float den = (w * s_z) * e_z;
-    const float md = (((s_lo * e_hi) * __builtin_fmaxf(e_lo, 1.0f)) * (s_z * e_z)) * k.sb;
+    const float den = w * sz_ez;
+    const float md = (((s_lo * e_hi) * __builtin_fmaxf(e_lo, 1.0f)) * sz_ez) * k.sb;
     const float u = U * 0x1p-24f;
     const float t = __builtin_fmaf(u, den, -num);
     const float band = __builtin_fmaf(0x1p-16f, __builtin_fmaxf(num, den), 0x1p-46f * md);

@@ -541,7 +541,7 @@ __device__ __forceinline__ void sampled_read_update(const aw4_tensor& T, const T
     const float scale = (T.m2.flags & AW4_MOMENT_READ_RAW_SCALE) ? bs.raw : stored;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        float v[4], p[4], pre[4], den[4];
+        float v[4], p[4], den[4];
         decode4(L2.dec, sc.stage[8 * q + tl.j], scale, v);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
@@ -549,7 +549,6 @@ __device__ __forceinline__ void sampled_read_update(const aw4_tensor& T, const T
             const float d = __builtin_amdgcn_div_fixupf(div_by_rcp(sq, T.bc2_sqrt, T.bc2_sqrt_rcp), T.bc2_sqrt, sq) + T.eps;
             if constexpr (DP != D_F64) p[t] = p1[4 * q + t] + div_cr(T.step_coef * m1[4 * q + t], d);
             den[t] = d;
-            pre[t] = div_cr(1.0f, d);
         }
         if (tl.active) {
             const uint32_t off = tl.voff + 32u * q;
@@ -563,8 +562,12 @@ __device__ __forceinline__ void sampled_read_update(const aw4_tensor& T, const T
             } else {
                 store_f32<DP>(T.param, tl.blk0 * kBlock + off, vec, p);
             }
-            if (T.m2.values)
+            if (T.m2.values) {  // only the read-back schemes that keep 1 / denominator
+                float pre[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) pre[t] = div_cr(1.0f, den[t]);
                 *(gptr<f32x4>)(gaddr<float>(T.m2.values) + tl.blk0 * kBlock + off) = f32x4{pre[0], pre[1], pre[2], pre[3]};
+            }
         }
     }
 }

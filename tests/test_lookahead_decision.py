@@ -76,13 +76,12 @@ def quick(z, a, b, s, g, beta2, bias, eps, U, rng, band_scale=1.0):
     d_hi = fma32(s, b, -z)
     w = (s * (b - a).astype(F32)).astype(F32)
     s_lo = (r_hi + r_lo).astype(F32)
-    s_z = (r_hi + r_z).astype(F32)
+    sz_ez = ((r_hi + r_z).astype(F32) * e_z).astype(F32)
     num = ((d_hi * s_lo).astype(F32) * e_lo).astype(F32)
-    den = ((w * s_z).astype(F32) * e_z).astype(F32)
+    den = (w * sz_ez).astype(F32)
     # M D = (r_hi + r_lo) E_hi max(1, E_lo) (r_hi + r_z) E_z sqrt(bias) / beta2 (the width cancels)
     sb = jitter(np.full(n, np.sqrt(bias) / beta2, F32), rng.integers(-4, 5, n))
-    md = ((((s_lo * e_hi).astype(F32) * np.maximum(e_lo, F32(1))).astype(F32) * (s_z * e_z).astype(F32)).astype(F32)
-          * sb).astype(F32)
+    md = ((((s_lo * e_hi).astype(F32) * np.maximum(e_lo, F32(1))).astype(F32) * sz_ez).astype(F32) * sb).astype(F32)
     u = (U * F32(2.0 ** -24)).astype(F32)
     t = fma32(u, den, -num)
     band = fma32(np.full(n, 2.0 ** -16 * band_scale, F32), np.maximum(num, den), (F32(2.0 ** -46) * md).astype(F32))
