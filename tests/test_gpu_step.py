@@ -466,17 +466,20 @@ def _same_or_both_nan(a: torch.Tensor, b: torch.Tensor) -> bool:
     return bool(torch.equal(nan, torch.isnan(b.float()))) and torch.equal(H.bits(a[~nan]), H.bits(b[~nan]))
 
 
-@pytest.mark.parametrize("recipe", ["zeeden", "zipsr", "research"])
+@pytest.mark.parametrize("recipe", ["zeeden", "zipsr", "research", "zipsr_float64"])
 def test_non_finite_gradients_match_oracle(recipe):
     """NaN, +Inf and -Inf gradient values (in quantized tensors and an fp32-state tensor) follow
     the reference: the NaN / Inf block scales, the codes of a block whose scale is not finite
     (the kernel's IEEE forms), and the propagation into moments and parameters on the next
     steps.  Codes, fp32 states and scales equal the oracle's (NaN == NaN); parameters have the
-    same NaNs and their finite values are within the usual tolerance."""
+    same NaNs and their finite values are within the usual tolerance.  fp32 parameters, and
+    float64 ones under ZIP-SR (the generic kernel's float64 update)."""
     log(f"non-finite gradients, {recipe} x 3 steps")
     shapes = [(64, 128), (4096,), (1000,)]
     gen = torch.Generator().manual_seed(13)
-    init = [torch.randn(sh, generator=gen) * 0.02 for sh in shapes]
+    dtype = torch.float64 if recipe.endswith("_float64") else torch.float32
+    recipe = recipe.replace("_float64", "")
+    init = [(torch.randn(sh, generator=gen) * 0.02).to(dtype) for sh in shapes]
     params = [torch.nn.Parameter(t.clone().to(H.DEVICE)) for t in init]
     args = dict(lr=1e-3, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, optimized=True)
     m1s = ["nf4"] * 3
@@ -504,7 +507,7 @@ def test_non_finite_gradients_match_oracle(recipe):
             grads[1][2 * 128 + 64] = float("inf")
             grads[2][5] = float("nan")          # fp32-state tensor
         for p, g in zip(params, grads):
-            p.grad = g.to(H.DEVICE)
+            p.grad = g.to(dtype).to(H.DEVICE)
         opt.step()
         oracle.step(grads)
         torch.cuda.synchronize()
