@@ -217,6 +217,28 @@ def cpu_baseline(seconds_target: float = 20.0):
             "ci_threads_value": rate(ci_leg)}
 
 
+def copy_ceiling(device, gb: float = 4.0, reps: int = 10) -> float:
+    """The streaming rate of a plain device copy (torch's copy kernel, ``gb`` GB read and written
+    per copy) on this box, GB/s: the ceiling a read-and-write stream reaches here, against which
+    the step's rate is also reported."""
+    import torch
+
+    n = int(gb * 1e9) // 4
+    src = torch.ones(n, device=device)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+    del src, dst
+    return 8 * n / (ms * 1e-3) / 1e9
+
+
 def measured_traffic(config: str):
     """HBM bytes per launch of each recipe's kernel from the committed rocprofv3 summary of
     this workload (TCC FETCH_SIZE / WRITE_SIZE, scaled by a device copy of known size);
@@ -538,6 +560,8 @@ def main():
         print(f"[bench] clip prologue: {prologue}", file=sys.stderr, flush=True)
     per_recipe = {name: statistics.mean(v) for name, v in launch_ms.items()}
     names = [n for n, _, _ in recipes]
+    ceiling = copy_ceiling(device)
+    print(f"[bench] copy ceiling {ceiling:.0f} GB/s", file=sys.stderr, flush=True)
     # The dominant kernel is the recipe with the longest launches; its roofline is reported.
     dominant = max(per_recipe, key=per_recipe.get)
     achieved = algo_bytes[dominant] / (per_recipe[dominant] * 1e-3) / 1e9
@@ -637,6 +661,8 @@ def main():
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": (round(traffic[dominant]) if traffic and dominant in traffic else None),
             "traffic_source": traffic_source,
+            "copy_ceiling_gb_s": round(ceiling, 1),
+            "frac_of_copy_ceiling": round(achieved / ceiling, 4),
         },
         "cpu_baseline": baseline,
     }
