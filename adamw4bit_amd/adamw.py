@@ -205,6 +205,36 @@ def _f32s(*values: float) -> list:
     return array.array("f", values).tolist()
 
 
+_HYPER_CACHE: Dict[tuple, tuple] = {}
+
+
+def _hyper_constants(beta1, beta2, lr, wd, eps) -> tuple:
+    """The step-independent constants of a group's hyperparameters: the lerp flags, fp32 lerp
+    weights (w - 1 with the LARGE flag), fp32 decay 1 - lr*wd and eps, and the float64 decay.
+    Cached for Python-number hyperparameters (a tensor-valued one is computed each time: its
+    value may change in place)."""
+    key = (beta1, beta2, lr, wd, eps)
+    cacheable = all(type(v) in (float, int) for v in key)
+    if cacheable:
+        hit = _HYPER_CACHE.get(key)
+        if hit is not None:
+            return hit
+    w1, w2, decay, eps32 = _f32s(1 - beta1, 1 - beta2, 1 - lr * wd, eps)
+    flags = 0
+    if not abs(w1) < 0.5:  # ATen lerp switches formulas at |weight| >= 0.5
+        flags |= _lib.TENSOR_LERP1_LARGE
+        w1 = w1 - 1.0  # exact for w1 in [0.5, 1] (and NaN stays NaN), as in fp32
+    if not abs(w2) < 0.5:
+        flags |= _lib.TENSOR_LERP2_LARGE
+        w2 = w2 - 1.0
+    out = (flags, w1, w2, decay, eps32, float(1 - lr * wd))
+    if cacheable:
+        if len(_HYPER_CACHE) >= 256:
+            _HYPER_CACHE.clear()
+        _HYPER_CACHE[key] = out
+    return out
+
+
 class _StepConstants:
     """The fp32 step constants of one (group, step), computed in float64 and rounded once to
     fp32 as the reference does (``_optimized.py:168-173``).  ``words`` and ``m2_sr`` are their
@@ -219,23 +249,16 @@ class _StepConstants:
         lr, wd, eps = group["lr"], group["weight_decay"], group["eps"]
         bias1, bias2 = 1 - beta1 ** step, 1 - beta2 ** step
         self.storage_bias = 1 - beta2 ** (step + 1) if m2_scheme in NEXT_BIAS_SCHEMES else bias2
-        # a float64 parameter is decayed and updated with the float64 values (_optimized.py:221-222)
-        self.decay_f64, self.step_coef_f64 = float(1 - lr * wd), float(-lr / bias1)
-        # one fp32 rounding of everything, then of the two reciprocals (the update-SR bias is
-        # floored at 1e-12 before its rounding, _optimized_quantization.py:66-67)
-        w1, w2, self.decay, self.step_coef, self.bc2_sqrt, self.eps, sr_bias = _f32s(
-            1 - beta1, 1 - beta2, 1 - lr * wd, -lr / bias1, math.sqrt(bias2), eps, max(float(self.storage_bias), 1e-12))
+        self.lerp_flags, self.w1, self.w2, self.decay, self.eps, self.decay_f64 = _hyper_constants(
+            beta1, beta2, lr, wd, eps)
+        # a float64 parameter is updated with the float64 coefficient (_optimized.py:221-222)
+        self.step_coef_f64 = float(-lr / bias1)
+        # one fp32 rounding of the step's values, then of the two reciprocals (the update-SR bias
+        # is floored at 1e-12 before its rounding, _optimized_quantization.py:66-67)
+        self.step_coef, self.bc2_sqrt, sr_bias = _f32s(-lr / bias1, math.sqrt(bias2),
+                                                       max(float(self.storage_bias), 1e-12))
         self.bc2_sqrt_rcp, sr_bias_rcp = _rcp32s(self.bc2_sqrt, sr_bias)
         self._m2_vals = (sr_bias, sr_bias_rcp, self.eps)
-        flags = 0
-        if not abs(w1) < 0.5:  # ATen lerp switches formulas at |weight| >= 0.5
-            flags |= _lib.TENSOR_LERP1_LARGE
-            w1 = w1 - 1.0  # exact for w1 in [0.5, 1] (and NaN stays NaN), as in fp32
-        if not abs(w2) < 0.5:
-            flags |= _lib.TENSOR_LERP2_LARGE
-            w2 = w2 - 1.0
-        self.lerp_flags = flags
-        self.w1, self.w2 = w1, w2
         self._words = self._m2_sr = None
 
     def words(self) -> np.ndarray:
