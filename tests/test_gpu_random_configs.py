@@ -11,8 +11,8 @@ one, fp32 / bf16 / fp16 parameters, tensors on the 4-bit path and on the fp32-st
 weight decay on and off, the optimized step's chunk size (its draw accounting), and gradients
 from heavy-tailed to tiny, with and without all-zero blocks.  Three steps each, so the second and
 third reuse the first step's launch plan.  Eight more cases draw tensors of up to 33.6M values,
-whose launches take 2, 3 or 4 tiles per wave.  The configuration is printed before the case
-runs."""
+whose launches take 2, 3 or 4 tiles per wave, and 16 more (8 of the resume cases) draw the same
+mixes with float64 parameters.  The configuration is printed before the case runs."""
 
 from __future__ import annotations
 
@@ -79,6 +79,13 @@ def test_random_configuration_matches_oracle(seed):
     _check_against_oracle(seed, draw_case(seed))
 
 
+@pytest.mark.parametrize("seed", range(7000, 7016))
+def test_random_float64_configuration_matches_oracle(seed):
+    """Configurations drawn the same way with float64 parameters, which the generic kernel updates
+    in float64 (gradients read as fp32, fp32 moments and denominator)."""
+    _check_against_oracle(seed, dict(draw_case(seed), dtype=torch.float64))
+
+
 @pytest.mark.parametrize("seed", range(5005, 5013))
 def test_large_random_configuration_matches_oracle(seed):
     """The same with tensors of up to 33.6M values (launches of 2-4 tiles per wave)."""
@@ -135,7 +142,16 @@ def test_random_configuration_resumes_exactly(seed, tmp_path):
     is bit-identical to five uninterrupted steps: parameters and every state entry (codes, block
     scales, fp32 and pending lookahead state, the store-EDEN denominators, step counts), which
     also pins the random streams' positions across the checkpoint."""
-    case = draw_case(1000 + seed)
+    _check_resume(seed, draw_case(1000 + seed), tmp_path)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_float64_configuration_resumes_exactly(seed, tmp_path):
+    """The same with float64 parameters."""
+    _check_resume(seed, dict(draw_case(1100 + seed), dtype=torch.float64), tmp_path)
+
+
+def _check_resume(seed: int, case: dict, tmp_path) -> None:
     log(f"resume case {seed}: {case}")
     shapes, pairs = [], []
     for g in case["groups"]:
