@@ -110,14 +110,20 @@ struct BlockScratch {
     uint16_t* stage;    // 32 code words: word 8q + j is lane j's word of quarter q
 };
 
-// LDS scratch of one wave (8 blocks).
+// Code bytes of one wave tile: 8 blocks of 64.
+constexpr int kWaveCodeBytes = kBlocksPerWave * kBlock / 2;
+
+// LDS scratch of one wave (8 blocks).  Before a tile's update its first 2 * kWaveCodeBytes bytes
+// pass the loaded code words of both moments to their lanes (codes_to_lanes).
 struct WaveScratch {
     UpdEntry upd[kBlocksPerWave][kPairs];
     float pre[kBlocksPerWave][16];
     uint16_t stage[kBlocksPerWave][32];
 
     __device__ BlockScratch block(int grp) { return BlockScratch{upd[grp], pre[grp], stage[grp]}; }
+    __device__ uint8_t* code_words() { return (uint8_t*)&upd[0][0]; }
 };
+static_assert(sizeof(WaveScratch::upd) >= 2 * kWaveCodeBytes, "code words of two moments in the update-SR tables");
 
 // Exponent and top 3 mantissa bits of x, clamped to the table's range (one med3).
 __device__ __forceinline__ int lut_field(uint32_t u) {

@@ -263,6 +263,15 @@ __device__ __forceinline__ void decay4(const aw4_tensor& T, const float (&p)[4],
 // Tiles of tensors whose numel is a multiple of 128 (block layout)
 // ---------------------------------------------------------------------------
 
+// Whether a kernel loads its code words with one 8-byte load per lane and passes them to their
+// lanes through LDS (codes_to_lanes), instead of four 2-byte loads per moment: the specialised
+// bf16 kernels of the recipes (not the read-back or lookahead m2 ones), whose loads are otherwise
+// twice as many per byte as the fp32 kernels'.
+constexpr bool codes_via_lds(int m1k, int m2k, int d) {
+    return d == D_BF16 && kind_of(m1k) != K_ANY && kind_of(m2k) != K_ANY && kind_of(m2k) != K_LA &&
+           (flags_of(m2k) & AW4_MOMENT_SAMPLED_READ) == 0;
+}
+
 // Raw inputs of one lane for one wave tile (blocks blk0 .. blk0+7; lane's block blk0 + lane/8).
 template <int M1K, int M2K, int D>
 struct TileInputs {
@@ -342,13 +351,24 @@ __device__ __forceinline__ void load_tile(const aw4_tensor& T, const TileLane& t
         if (quantized) {
             if constexpr (kQ) {
                 const gptr<const uint8_t> codes = gaddr<const uint8_t>(M.codes) + tl.blk0 * (kBlock / 2);
-                const uint32_t coff = (uint32_t)(grp * (kBlock / 2) + 2 * tl.j);
-                // two 16-bit code words per register: 4 fewer registers per tile in flight
+                if constexpr (codes_via_lds(M1K, M2K, D)) {
+                    // The tile's code bytes in memory order, one 8-byte load per lane (bytes 8 l .. 8 l + 7
+                    // of the tile: the words of one quarter for four lanes of block l / 8); codes_to_lanes
+                    // hands each lane its own four words through LDS before they are decoded.
+                    const u32x2 w = __builtin_nontemporal_load(
+                        (gptr<const u32x2>)(codes + 8u * (uint32_t)(grp * kBlocksPerWave + tl.j)));
+                    c[0] = w.x;
+                    c[1] = w.y;
+                } else {
+                    const uint32_t coff = (uint32_t)(grp * (kBlock / 2) + 2 * tl.j);
+                    // two 16-bit code words per register: 4 fewer registers per tile in flight
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const uint32_t lo = __builtin_nontemporal_load((gptr<const uint16_t>)(codes + coff + 32u * h));
-                    const uint32_t hi = __builtin_nontemporal_load((gptr<const uint16_t>)(codes + coff + 32u * h + 16u));
-                    c[h] = lo | (hi << 16);
+                    for (int h = 0; h < 2; ++h) {
+                        const uint32_t lo = __builtin_nontemporal_load((gptr<const uint16_t>)(codes + coff + 32u * h));
+                        const uint32_t hi =
+                            __builtin_nontemporal_load((gptr<const uint16_t>)(codes + coff + 32u * h + 16u));
+                        c[h] = lo | (hi << 16);
+                    }
                 }
                 s = (gaddr<const float>(M.scales) + tl.blk0)[grp];
             }
@@ -367,6 +387,42 @@ __device__ __forceinline__ void load_tile(const aw4_tensor& T, const TileLane& t
                 std::integral_constant<bool, In::kV1>());
     load_moment(T.m2, in.c2, in.s2, in.v2, std::integral_constant<bool, In::kQ2>(),
                 std::integral_constant<bool, In::kV2>());
+}
+
+// The code words of a loaded tile, from memory order to their lanes: load_tile leaves lane l
+// (block l / 8) with bytes 8 l .. 8 l + 7 of the tile's codes; lane j of block grp decodes the words
+// at bytes 64 grp + 16 q + 2 j (q = 0..3), two to a register (quarters 2h, 2h + 1).  The bytes go
+// through the wave's scratch, which no encode of this tile uses yet; lanes past a tensor's last
+// block (which loaded block 0's bytes) read block 0's words, as every other input of theirs.
+template <int M1K, int M2K, int D>
+__device__ __forceinline__ void codes_to_lanes(const aw4_tensor& T, const TileLane& tl, TileInputs<M1K, M2K, D>& in,
+                                               WaveScratch& ws) {
+    if constexpr (!codes_via_lds(M1K, M2K, D)) return;
+    using In = TileInputs<M1K, M2K, D>;
+    const bool q1 = In::kQ1 && moment_quantized<M1K>(T.m1), q2 = In::kQ2 && moment_quantized<M2K>(T.m2);
+    if (!q1 && !q2) return;
+    uint8_t* buf = ws.code_words();
+    const int lane = tl.grp * kBlocksPerWave + tl.j;
+    wave_lds_sync();  // earlier readers of the scratch are done
+    if (q1) *(u32x2*)(buf + 8 * lane) = u32x2{in.c1[0], in.c1[1]};
+    if (q2) *(u32x2*)(buf + kWaveCodeBytes + 8 * lane) = u32x2{in.c2[0], in.c2[1]};
+    wave_lds_sync();
+    const uint32_t base = (uint32_t)((tl.active ? tl.grp : 0) * (kBlock / 2) + 2 * tl.j);
+    auto words = [&](const uint8_t* b, uint32_t* c) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t lo = *(const uint16_t*)(b + base + 32u * h);
+            const uint32_t hi = *(const uint16_t*)(b + base + 32u * h + 16u);
+            c[h] = lo | (hi << 16);
+        }
+    };
+    if constexpr (In::kQ1) {
+        if (q1) words(buf, in.c1);
+    }
+    if constexpr (In::kQ2) {
+        if (q2) words(buf + kWaveCodeBytes, in.c2);
+    }
+    wave_lds_sync();  // the words are read before the scratch is written again
 }
 
 template <int MK, bool kNonNeg, class Values>
@@ -747,6 +803,7 @@ __device__ __forceinline__ void run_tiles(const StepHeader* hdr, const LdsT& lds
         } else {
             const TileLane tl = tile_lane(T, local * kBlocksPerWave, lane);
             if (!loaded) load_tile(T, tl, in);
+            codes_to_lanes(T, tl, in, ws);
             const MomentTables L1 = lds_tables.moment(T.m1, 0);
             const MomentTables L2 = lds_tables.moment(T.m2, 1);
             auto prefetch = [&]() {
