@@ -110,11 +110,13 @@ struct BlockScratch {
     uint16_t* stage;    // 32 code words: word 8q + j is lane j's word of quarter q
 };
 
-// Code bytes of one wave tile: 8 blocks of 64.
+// Code bytes of one wave tile: 8 blocks of 64; bytes of its 16-bit values: 8 blocks of 256.
 constexpr int kWaveCodeBytes = kBlocksPerWave * kBlock / 2;
+constexpr int kWaveImageBytes = kBlocksPerWave * kBlock * 2;
 
-// LDS scratch of one wave (8 blocks).  Before a tile's update its first 2 * kWaveCodeBytes bytes
-// pass the loaded code words of both moments to their lanes (codes_to_lanes).
+// LDS scratch of one wave (8 blocks).  In kernels that move tiles through LDS, its first
+// kWaveImageBytes bytes also pass the loaded code words of both moments to their lanes before a
+// tile's update, and then hold the updated 16-bit parameters until they are stored.
 struct WaveScratch {
     UpdEntry upd[kBlocksPerWave][kPairs];
     float pre[kBlocksPerWave][16];
@@ -124,6 +126,7 @@ struct WaveScratch {
     __device__ uint8_t* code_words() { return (uint8_t*)&upd[0][0]; }
 };
 static_assert(sizeof(WaveScratch::upd) >= 2 * kWaveCodeBytes, "code words of two moments in the update-SR tables");
+static_assert(sizeof(WaveScratch) >= kWaveImageBytes, "a tile's 16-bit parameters in the wave's scratch");
 
 // Exponent and top 3 mantissa bits of x, clamped to the table's range (one med3).
 __device__ __forceinline__ int lut_field(uint32_t u) {

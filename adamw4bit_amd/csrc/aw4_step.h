@@ -263,11 +263,14 @@ __device__ __forceinline__ void decay4(const aw4_tensor& T, const float (&p)[4],
 // Tiles of tensors whose numel is a multiple of 128 (block layout)
 // ---------------------------------------------------------------------------
 
-// Whether a kernel loads its code words with one 8-byte load per lane and passes them to their
-// lanes through LDS (codes_to_lanes), instead of four 2-byte loads per moment: the specialised
-// bf16 kernels of the recipes (not the read-back or lookahead m2 ones), whose loads are otherwise
-// twice as many per byte as the fp32 kernels'.
-constexpr bool codes_via_lds(int m1k, int m2k, int d) {
+// Whether a kernel moves parts of a tile between memory and its lanes through LDS: the specialised
+// bf16 kernels of the recipes (not the read-back or lookahead m2 ones).  Their lanes own 4 values
+// of a quarter, 8 bytes, so that direct accesses touch half of each 128-byte line per instruction
+// and the code words come in 2-byte loads.  Instead each lane loads one 8-byte piece of the tile's
+// codes and stores the 16-byte pieces of updated parameters 64 h + 8 j .. + 7 of its block, and
+// codes_to_lanes / params_to_memory rearrange them in LDS.  (Loading the gradients and
+// parameters the same way measured no faster, for 6 more registers.)
+constexpr bool lds_tile_io(int m1k, int m2k, int d) {
     return d == D_BF16 && kind_of(m1k) != K_ANY && kind_of(m2k) != K_ANY && kind_of(m2k) != K_LA &&
            (flags_of(m2k) & AW4_MOMENT_SAMPLED_READ) == 0;
 }
@@ -351,7 +354,7 @@ __device__ __forceinline__ void load_tile(const aw4_tensor& T, const TileLane& t
         if (quantized) {
             if constexpr (kQ) {
                 const gptr<const uint8_t> codes = gaddr<const uint8_t>(M.codes) + tl.blk0 * (kBlock / 2);
-                if constexpr (codes_via_lds(M1K, M2K, D)) {
+                if constexpr (lds_tile_io(M1K, M2K, D)) {
                     // The tile's code bytes in memory order, one 8-byte load per lane (bytes 8 l .. 8 l + 7
                     // of the tile: the words of one quarter for four lanes of block l / 8); codes_to_lanes
                     // hands each lane its own four words through LDS before they are decoded.
@@ -389,15 +392,21 @@ __device__ __forceinline__ void load_tile(const aw4_tensor& T, const TileLane& t
                 std::integral_constant<bool, In::kV2>());
 }
 
-// The code words of a loaded tile, from memory order to their lanes: load_tile leaves lane l
-// (block l / 8) with bytes 8 l .. 8 l + 7 of the tile's codes; lane j of block grp decodes the words
-// at bytes 64 grp + 16 q + 2 j (q = 0..3), two to a register (quarters 2h, 2h + 1).  The bytes go
-// through the wave's scratch, which no encode of this tile uses yet; lanes past a tensor's last
-// block (which loaded block 0's bytes) read block 0's words, as every other input of theirs.
+// Byte offset of 16-byte column c (0..15) of block grp in a tile image of 16-bit values held in
+// LDS (256 bytes per block): the column index is XORed with the block so that the 8 blocks' lanes,
+// which access the same columns of their blocks, spread over the banks.
+__device__ __forceinline__ uint32_t image_column(int grp, int c) { return (uint32_t)(grp * 256 + ((c ^ grp) << 4)); }
+
+// The code words of a loaded tile, from memory order to their lanes (lds_tile_io kernels):
+// load_tile leaves lane l (block l / 8) with bytes 8 l .. 8 l + 7 of the tile's codes; lane j of
+// block grp decodes the words at bytes 64 grp + 16 q + 2 j (q = 0..3), two to a register (quarters
+// 2h, 2h + 1).  The bytes go through the wave's scratch, which no encode of this tile uses yet;
+// lanes past a tensor's last block (which loaded block 0's bytes) read block 0's words, as every
+// other input of theirs.
 template <int M1K, int M2K, int D>
 __device__ __forceinline__ void codes_to_lanes(const aw4_tensor& T, const TileLane& tl, TileInputs<M1K, M2K, D>& in,
                                                WaveScratch& ws) {
-    if constexpr (!codes_via_lds(M1K, M2K, D)) return;
+    if constexpr (!lds_tile_io(M1K, M2K, D)) return;
     using In = TileInputs<M1K, M2K, D>;
     const bool q1 = In::kQ1 && moment_quantized<M1K>(T.m1), q2 = In::kQ2 && moment_quantized<M2K>(T.m2);
     if (!q1 && !q2) return;
@@ -423,6 +432,26 @@ __device__ __forceinline__ void codes_to_lanes(const aw4_tensor& T, const TileLa
         if (q2) words(buf + kWaveCodeBytes, in.c2);
     }
     wave_lds_sync();  // the words are read before the scratch is written again
+}
+
+// The updated parameters of a tile to memory (lds_tile_io kernels): update_quarter left each
+// lane's 8-byte pieces in a parameter image in the wave's scratch (image_column); each lane stores
+// the 16-byte pieces of values 64 h + 8 j .. + 7 of its block (the host runs these kernels only
+// where the parameter is 16-byte aligned).  Before the tile's encodes use the scratch.
+template <int M1K, int M2K, int D>
+__device__ __forceinline__ void params_to_memory(const aw4_tensor& T, const TileLane& tl, WaveScratch& ws) {
+    if constexpr (!lds_tile_io(M1K, M2K, D)) return;
+    const uint8_t* img = ws.code_words();
+    wave_lds_sync();
+    if (tl.active) {
+        const gptr<uint16_t> pt =
+            gaddr<uint16_t>(tile_values<D>(T.param, tl.blk0)) + (uint32_t)(tl.grp * kBlock + 8 * tl.j);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            __builtin_nontemporal_store(*(const u32x4*)(img + image_column(tl.grp, 8 * h + tl.j)),
+                                        (gptr<u32x4>)(pt + 64u * h));
+    }
+    wave_lds_sync();  // the pieces are read before the encodes write the scratch
 }
 
 template <int MK, bool kNonNeg, class Values>
@@ -463,7 +492,8 @@ struct M2Staged {
 template <int M1K, int M2K, int D, int DP, bool kGenericLerp, bool kDefer, class M2Sink>
 __device__ __forceinline__ void update_quarter(const aw4_tensor& T, int q, const TileInputs<M1K, M2K, D>& in,
                                                const MomentTables& L1, const MomentTables& L2, const TileLane& tl,
-                                               float (&m1)[16], M2Sink& m2, float* p1, const float* la_prior) {
+                                               float (&m1)[16], M2Sink& m2, float* p1, const float* la_prior,
+                                               uint8_t* p_img) {
     using In = TileInputs<M1K, M2K, D>;
     constexpr int DC = D == D_ANY ? D_F32 : D;  // generic loads are already fp32 words
     constexpr bool kF64 = DP == D_F64;  // the parameter is read, updated and stored in float64 below
@@ -528,6 +558,10 @@ __device__ __forceinline__ void update_quarter(const aw4_tensor& T, int q, const
             if (T.param_dtype == D_F32) store_f32<D_F32>(T.param, e, vec, p);
             else if (T.param_dtype == D_BF16) store_f32<D_BF16>(T.param, e, vec, p);
             else store_f32<D_F16>(T.param, e, vec, p);
+        } else if constexpr (lds_tile_io(M1K, M2K, D)) {
+            // the 8-byte piece into the tile's parameter image (params_to_memory stores it)
+            *(u32x2*)(p_img + image_column(tl.grp, 4 * q + (tl.j >> 1)) + 8u * (uint32_t)(tl.j & 1)) =
+                u32x2{f32x2_to_bf16x2(p[0], p[1]), f32x2_to_bf16x2(p[2], p[3])};
         } else {
             store_f32<D>(tile_values<D>(T.param, tl.blk0), off, true, p);
         }
@@ -537,15 +571,16 @@ __device__ __forceinline__ void update_quarter(const aw4_tensor& T, int q, const
 template <int M1K, int M2K, int D, int DP, bool kDefer, class M2Sink>
 __device__ __forceinline__ void update_tile(const aw4_tensor& T, const TileInputs<M1K, M2K, D>& in,
                                             const MomentTables& L1, const MomentTables& L2, const TileLane& tl,
-                                            float (&m1)[16], M2Sink& m2, float* p1, const float* la_prior) {
+                                            float (&m1)[16], M2Sink& m2, float* p1, const float* la_prior,
+                                            uint8_t* p_img) {
     if (__builtin_expect((T.flags & (AW4_TENSOR_LERP1_LARGE | AW4_TENSOR_LERP2_LARGE)) == 0, 1)) {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-            update_quarter<M1K, M2K, D, DP, false, kDefer>(T, q, in, L1, L2, tl, m1, m2, p1, la_prior);
+            update_quarter<M1K, M2K, D, DP, false, kDefer>(T, q, in, L1, L2, tl, m1, m2, p1, la_prior, p_img);
     } else {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-            update_quarter<M1K, M2K, D, DP, true, kDefer>(T, q, in, L1, L2, tl, m1, m2, p1, la_prior);
+            update_quarter<M1K, M2K, D, DP, true, kDefer>(T, q, in, L1, L2, tl, m1, m2, p1, la_prior, p_img);
     }
 }
 
@@ -554,16 +589,17 @@ template <int M1K, int M2K, int D, bool kDefer = false, class M2Sink>
 __device__ __forceinline__ void update_tile_any(const aw4_tensor& T, const TileLane& tl,
                                                 const TileInputs<M1K, M2K, D>& in, const MomentTables& L1,
                                                 const MomentTables& L2, float (&m1)[16], M2Sink& m2,
-                                                float* p1 = nullptr, const float* la_prior = nullptr) {
+                                                float* p1 = nullptr, const float* la_prior = nullptr,
+                                                uint8_t* p_img = nullptr) {
     if constexpr (D == D_ANY) {
-        if (T.param_dtype == D_F32) update_tile<M1K, M2K, D, D_F32, kDefer>(T, in, L1, L2, tl, m1, m2, p1, la_prior);
+        if (T.param_dtype == D_F32) update_tile<M1K, M2K, D, D_F32, kDefer>(T, in, L1, L2, tl, m1, m2, p1, la_prior, p_img);
         else if (T.param_dtype == D_BF16)
-            update_tile<M1K, M2K, D, D_BF16, kDefer>(T, in, L1, L2, tl, m1, m2, p1, la_prior);
+            update_tile<M1K, M2K, D, D_BF16, kDefer>(T, in, L1, L2, tl, m1, m2, p1, la_prior, p_img);
         else if (T.param_dtype == D_F16)
-            update_tile<M1K, M2K, D, D_F16, kDefer>(T, in, L1, L2, tl, m1, m2, p1, la_prior);
-        else update_tile<M1K, M2K, D, D_F64, kDefer>(T, in, L1, L2, tl, m1, m2, p1, la_prior);
+            update_tile<M1K, M2K, D, D_F16, kDefer>(T, in, L1, L2, tl, m1, m2, p1, la_prior, p_img);
+        else update_tile<M1K, M2K, D, D_F64, kDefer>(T, in, L1, L2, tl, m1, m2, p1, la_prior, p_img);
     } else {
-        update_tile<M1K, M2K, D, D, kDefer>(T, in, L1, L2, tl, m1, m2, p1, la_prior);
+        update_tile<M1K, M2K, D, D, kDefer>(T, in, L1, L2, tl, m1, m2, p1, la_prior, p_img);
     }
 }
 
@@ -878,14 +914,16 @@ __device__ __forceinline__ void run_tiles(const StepHeader* hdr, const LdsT& lds
                 }
             } else if constexpr (stage_m2(M1K, M2K, D)) {
                 M2Staged m2{m2_stage + lane, 0.0f};
-                update_tile_any(T, tl, in, L1, L2, m1, m2);
+                update_tile_any(T, tl, in, L1, L2, m1, m2, nullptr, nullptr, ws.code_words());
+                params_to_memory<M1K, M2K, D>(T, tl, ws);
                 finish_moment<M1K, false>(T.m1, L1, tl, RegValues{m1}, ws);
                 prefetch();
                 finish_moment<M2K, true>(T.m2, L2, tl, m2.values(), ws);
             } else {
                 float m2v[16];
                 M2Regs m2{m2v};
-                update_tile_any(T, tl, in, L1, L2, m1, m2);
+                update_tile_any(T, tl, in, L1, L2, m1, m2, nullptr, nullptr, ws.code_words());
+                params_to_memory<M1K, M2K, D>(T, tl, ws);
                 finish_moment<M1K, false>(T.m1, L1, tl, RegValues{m1}, ws);
                 prefetch();
                 finish_moment<M2K, true>(T.m2, L2, tl, m2.values(), ws);

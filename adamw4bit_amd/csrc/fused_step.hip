@@ -251,10 +251,10 @@ struct KernelVariant {
     {M1, M2, D, (const void*)&step_kernel_4w<M1, M2, D>, (const void*)&step_kernel_inline_4w<M1, M2, D>}
 const KernelVariant kVariants[] = {
     AW4_VARIANT_I4W(kRtn, kRtnEden, D_F32),       AW4_VARIANT_I4W(kRtn, kUsrGuarded, D_F32),
-    AW4_VARIANT_I(kRtn, kRtnEden, D_BF16),        AW4_VARIANT_I(kRtn, kUsrGuarded, D_BF16),
-    AW4_VARIANT(kSsrGuarded, kUsrGuarded, D_F32), AW4_VARIANT(kSsrGuarded, kUsrGuarded, D_BF16),
+    AW4_VARIANT_I4W(kRtn, kRtnEden, D_BF16),      AW4_VARIANT_I4W(kRtn, kUsrGuarded, D_BF16),
+    AW4_VARIANT(kSsrGuarded, kUsrGuarded, D_F32), AW4_VARIANT_4W(kSsrGuarded, kUsrGuarded, D_BF16),
     AW4_VARIANT(kRtn, kFp32, D_F32),              AW4_VARIANT(kRtn, kFp32, D_BF16),
-    AW4_VARIANT(kRtn, kUsrGuardedEden, D_F32),    AW4_VARIANT(kRtn, kUsrGuardedEden, D_BF16),
+    AW4_VARIANT(kRtn, kUsrGuardedEden, D_F32),    AW4_VARIANT_4W(kRtn, kUsrGuardedEden, D_BF16),
     AW4_VARIANT(kRtn, kUsrRead, D_F32),           AW4_VARIANT(kRtn, kUsrReadEden, D_F32),
     AW4_VARIANT(kRtn, kLaStore, D_F32),           AW4_VARIANT_3W(kRtn, kLaPending, D_F32),
     AW4_VARIANT_2W(K_ANY, kAnyResearch, D_ANY),
@@ -661,13 +661,16 @@ std::vector<LaunchGroup> plan_launches(const aw4_tensor* ts, int32_t count) {
         const bool research_tensor = research_m2(t.m2);
         const int s1 = mspec(t.m1.rounding, t.m1.flags & spec_flags_mask(t.m1.rounding));
         const int s2 = mspec(t.m2.rounding, t.m2.flags & spec_flags_mask(t.m2.rounding));
-        // Specialised kernels access parameters and gradients as 4-value vectors; a row whose
-        // addresses do not allow that (a view at an odd offset into a flat buffer) runs the
-        // generic kernel, which reads the flag at run time.
+        // Specialised kernels access parameters and gradients as 4-value vectors, and those that
+        // store parameters through LDS as 16-byte pieces; a row whose addresses do not allow that
+        // (a view at an odd offset into a flat buffer) runs the generic kernel, which reads the
+        // flag at run time.
         int v = kGenericVariant;
+        const bool vec16 = aligned(t.param, 16);
         if (t.param_dtype == t.grad_dtype && (t.flags & AW4_TENSOR_VEC_ALIGNED))
             for (int k = 0; k < kNumSpecialised; ++k)
-                if (kVariants[k].dtype == t.param_dtype && kVariants[k].m1 == s1 && kVariants[k].m2 == s2) {
+                if (kVariants[k].dtype == t.param_dtype && kVariants[k].m1 == s1 && kVariants[k].m2 == s2 &&
+                    (vec16 || !lds_tile_io(kVariants[k].m1, kVariants[k].m2, kVariants[k].dtype))) {
                     v = k;
                     break;
                 }

@@ -90,30 +90,34 @@ def test_plan_follows_swapped_parameter_storage():
 # Parameters that do not allow vector access, strided parameters
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("recipe", ["zeeden", "zipsr"])
-def test_parameter_at_odd_offset_matches_oracle(recipe):
-    """A parameter (and gradient) one element into a flat buffer: its rows cannot take 16-byte
-    vector accesses, so they run the generic kernel; results equal the oracle's."""
-    log(f"parameter at element offset 1 ({recipe})")
+@pytest.mark.parametrize("recipe,dtype,offset", [("zeeden", torch.float32, 1), ("zipsr", torch.float32, 1),
+                                                  ("zeeden", torch.bfloat16, 4), ("zipsr", torch.bfloat16, 4)])
+def test_parameter_at_odd_offset_matches_oracle(recipe, dtype, offset):
+    """A parameter (and gradient) a few elements into a flat buffer: fp32 one element in, whose
+    rows cannot take 16-byte vector accesses; bf16 four elements (8 bytes) in, whose rows allow the
+    4-value accesses but not the 16-byte parameter stores of the specialised bf16 kernels.  Both run
+    the generic kernel; results equal the oracle's and the buffer's other elements stay as they were."""
+    log(f"parameter at element offset {offset} ({recipe}, {dtype})")
     gen = torch.Generator().manual_seed(8)
     shape = (96, 256)
     n = shape[0] * shape[1]
-    init = torch.randn(shape, generator=gen) * 0.02
-    buf = torch.zeros(n + 5, device=H.DEVICE)
-    buf[1:1 + n] = init.reshape(-1).to(H.DEVICE)
-    p = torch.nn.Parameter(buf[1:1 + n].view(shape))  # contiguous, 4 bytes past an aligned address
-    assert p.is_contiguous() and p.data_ptr() % 16 == 4
+    init = (torch.randn(shape, generator=gen) * 0.02).to(dtype)
+    buf = torch.zeros(n + offset + 4, device=H.DEVICE, dtype=dtype)
+    buf[offset:offset + n] = init.reshape(-1).to(H.DEVICE)
+    p = torch.nn.Parameter(buf[offset:offset + n].view(shape))  # contiguous, off a 16-byte boundary
+    assert p.is_contiguous() and p.data_ptr() % 16 == offset * p.element_size()
     kw = dict(optimized=True, quant_rng_seed=9 if recipe == "zipsr" else None, **ARGS)
     opt = aw.ZIPSRAdamW4Bit([p], **kw) if recipe == "zipsr" else aw.ZEEDENAdamW4Bit([p], **kw)
     m2 = "dyn4_upd_sr_fp32read" if recipe == "zipsr" else "dyn4_nz"
     cpu = [init.clone()]
     oracle = ref.Oracle(cpu, ref.Hyper(), ["nf4"], [m2], [recipe == "zeeden"], seed=kw["quant_rng_seed"],
                         draw_fn=H.PhiloxMirror(opt, H.DEVICE), usr_sqrt="cr")
-    gbuf = torch.zeros(n + 3, device=H.DEVICE)
+    goff = 3 if dtype == torch.float32 else 4  # bf16: 8 bytes in, so the 4-value accesses stay allowed
+    gbuf = torch.zeros(n + goff + 4, device=H.DEVICE, dtype=dtype)
     for _ in range(3):
-        g = H.heavy_tailed(shape, gen)
-        gbuf[3:3 + n] = g.reshape(-1).to(H.DEVICE)
-        p.grad = gbuf[3:3 + n].view(shape)
+        g = H.heavy_tailed(shape, gen).to(dtype)
+        gbuf[goff:goff + n] = g.reshape(-1).to(H.DEVICE)
+        p.grad = gbuf[goff:goff + n].view(shape)
         opt.step()
         oracle.step([g])
     torch.cuda.synchronize()
@@ -126,7 +130,7 @@ def test_parameter_at_odd_offset_matches_oracle(recipe):
         else:
             assert torch.equal(H.bits(st[key]), H.bits(ost[key])), key
     H.assert_params_close(p, cpu[0], "odd offset", steps=3)
-    assert float(buf[0]) == 0.0 and bool((buf[1 + n:] == 0).all())  # neighbours untouched
+    assert bool((buf[:offset] == 0).all()) and bool((buf[offset + n:] == 0).all())  # neighbours untouched
 
 
 def test_strided_parameter_takes_reference_step():
