@@ -82,11 +82,19 @@ struct __align__(8) UpdEntry {
     float g;        // (sqrt(b) - sqrt(a)) * 2^-24 / E(a), a the lower level (0: no interval)
 };
 
+// The level-only part of the update-SR quantities of a searchsorted index i, with a = cb[lo],
+// b = cb[hi] its levels (host-computed in double, each rounded once to fp32).
+struct __align__(16) UsrPair {
+    float sqrt_lo;  // RN(sqrt(a)), 0 for a <= 0
+    float sqrt_hi;  // RN(sqrt(b)), 0 for b <= 0
+    float gap_s;    // RN(sqrt(b) - sqrt(a)) * 2^-24 (exact), 0 unless b > a >= 0
+    float b_gt_a;   // 1 where b > a (fp32 levels), else 0
+};
+
 // All tables of all codebooks, built on the host and kept in device memory.
 struct Tables {
     float codebook[AW4_NUM_CODEBOOKS][16];
-    float sqrt_level[AW4_NUM_CODEBOOKS][16];        // RN(sqrt(level)), 0 for negative levels
-    float sqrt_gap[AW4_NUM_CODEBOOKS][kPairs];      // RN(sqrt(b) - sqrt(a)) of each searchsorted index
+    UsrPair usr[AW4_NUM_CODEBOOKS][kPairs];  // per searchsorted index (update-SR)
     PairEntry pairs[AW4_NUM_CODEBOOKS][kPairs];
     float2 dec[AW4_NUM_CODEBOOKS][256];  // code byte -> (level of low nibble, level of high nibble)
     LutEntry lut[AW4_NUM_LUTS][AW4_LUT_ENTRIES];
@@ -98,15 +106,14 @@ struct MomentTables {
     const PairEntry* pairs;
     const float2* dec;
     const LutEntry* lut;
-    const float* sqrt_level;
-    const float* sqrt_gap;
+    const UsrPair* usr;
 };
 
 // LDS scratch of one block's encode: update-SR tables of the block and the staging area
 // of its 64 code bytes (written a quarter at a time, stored to memory in one piece).
 struct BlockScratch {
     UpdEntry* upd;      // kPairs entries (update-SR only)
-    float* pre;         // E(l) of each of the 16 levels (update-SR only)
+    float* pre;         // the reference's preconditioners of the 16 levels (usr_level_preconds)
     uint16_t* stage;    // 32 code words: word 8q + j is lane j's word of quarter q
 };
 
@@ -182,32 +189,28 @@ struct UsrBlock {
     float band;  // the block's decision band (+inf: decide every value exactly)
 };
 
-// The block's tables: E(l) of the 16 levels (two per lane), then the 17 UpdEntry of the
-// searchsorted indices (two per lane).
+// The block's 17 UpdEntry of the searchsorted indices (two per lane), each from its own level pair:
+// E(a) and E(b) are formed where they are used, so no lane reads another's.
 __device__ __forceinline__ UsrBlock update_sr_tables(const MomentTables& L, int j, float s, const aw4_moment& M,
-                                                     UpdEntry* upd, float* pre) {
+                                                     UpdEntry* upd) {
     const float c = sqrt_faithful(s * M.sr_bias_rcp);
     const float c_rcp = rcp_faithful(c);
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int k = j + 8 * h;
-        pre[k] = __builtin_fmaf(c, L.sqrt_level[k], M.sr_eps);
-    }
-    wave_lds_sync();
     // Entries 1..16 in two rounds of the block's 8 lanes; entry 0 (no level below x) has
     // lo == hi and no interval.
     bool certain = true;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int i = 1 + j + 8 * h;
-        const PairEntry pe = L.pairs[i];
-        const float e_lo = pre[pe.lohi & 0xffu], e_hi = pre[pe.lohi >> 8];
-        const float gap = L.sqrt_gap[i];
-        certain = certain & (!(pe.b > pe.a) | (c * gap > 0x1p-20f * e_hi));  // over the real intervals
+        const UsrPair up = L.usr[i];
+        const float e_lo = __builtin_fmaf(c, up.sqrt_lo, M.sr_eps), e_hi = __builtin_fmaf(c, up.sqrt_hi, M.sr_eps);
+        // over the real intervals: c * gap > 2^-20 * E(b), both sides scaled by 2^-24, which leaves the
+        // comparison exact: with c >= 1e-6, every codebook's real gaps >= 2^-6 and its positive levels
+        // >= 2^-9, both products of a real interval stay far above the subnormals
+        certain = certain & ((up.b_gt_a == 0.0f) | (c * up.gap_s > 0x1p-44f * e_hi));
         // E(a) = 0 (a = 0 with eps = 0): f(a) is infinite and P = 0, so g = +inf decides upper
         // (a draw of exactly 0 gives Q = NaN, which counts as sure and decides upper too)
-        const float g = e_lo > 0.0f ? gap * 0x1p-24f * rcp_faithful(e_lo) : __builtin_inff();
-        upd[i] = UpdEntry{L.sqrt_level[pe.lohi >> 8], g};
+        const float g = e_lo > 0.0f ? up.gap_s * rcp_faithful(e_lo) : __builtin_inff();
+        upd[i] = UpdEntry{up.sqrt_hi, g};
     }
     // Entry 0: no level below x (x = 0 for dyn4), where the code does not depend on the draw:
     // Q = NaN marks the value sure in every block, certain or not (an all-zero block's scale is
@@ -266,8 +269,8 @@ __device__ __forceinline__ void usr_exact(const aw4_moment& M, float s, float x,
 
 // The reference's preconditioners of the block's 16 levels, f(l) = usr_precond(s, l), into the
 // block's 16-entry table (two per lane), for usr_exact: the same function of the same inputs as
-// an evaluation per value, so the same bits.  The table reuses the slots of the quick form's
-// E(l), which update_sr_tables has finished reading.
+// an evaluation per value, so the same bits.  Built only in a block encode where some quarter
+// needs the exact form.
 __device__ __forceinline__ void usr_level_preconds(const MomentTables& L, int j, float s, const aw4_moment& M,
                                                    float* pre) {
 #pragma unroll
@@ -341,7 +344,7 @@ __device__ __forceinline__ BlockScales encode_block(const aw4_moment& M, const M
     const bool floor0 = (flags & AW4_MOMENT_ZERO_FLOOR) != 0;
     UsrBlock ub{0.0f, 0.0f};
     if constexpr (KIND == K_USR) {
-        ub = update_sr_tables(L, j, s, M, sc.upd, sc.pre);
+        ub = update_sr_tables(L, j, s, M, sc.upd);
         fast = fast && s * M.sr_bias_rcp < 0x1p127f;  // (s * x) / bias stays far from overflow
     }
     // One branch for the whole wave: the IEEE forms are exact for every block, so a wave

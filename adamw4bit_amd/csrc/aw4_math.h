@@ -215,10 +215,12 @@ __device__ __forceinline__ void philox_tile_call(uint64_t seed, uint64_t g0, int
 
 // Fields 4q .. 4q+3 of a lane's string (words 3q .. 3q+2), as exact floats in [0, 2^24):
 // the uniforms times 2^24.
+// Fields 1 and 2 straddle two words: one byte permute each (v_perm_b32; selector byte k picks
+// byte k of the result: 0-3 from the second operand, 4-7 from the first, 0x0C gives 0).
 __device__ __forceinline__ void lane_fields4(const uint32_t* w, float (&u)[4]) {
     u[0] = (float)(w[0] & 0xffffffu);
-    u[1] = (float)((w[0] >> 24) | ((w[1] & 0xffffu) << 8));
-    u[2] = (float)((w[1] >> 16) | ((w[2] & 0xffu) << 16));
+    u[1] = (float)__builtin_amdgcn_perm(w[1], w[0], 0x0C050403u);  // w0 >> 24 | (w1 & 0xffff) << 8
+    u[2] = (float)__builtin_amdgcn_perm(w[2], w[1], 0x0C040302u);  // w1 >> 16 | (w2 & 0xff) << 16
     u[3] = (float)(w[2] >> 8);
 }
 

@@ -274,6 +274,14 @@ constexpr bool lds_tile_io(int m1k, int m2k, int d) {
     return d == D_BF16 && kind_of(m1k) != K_ANY && kind_of(m2k) != K_ANY && kind_of(m2k) != K_LA &&
            (flags_of(m2k) & AW4_MOMENT_SAMPLED_READ) == 0;
 }
+// Whether a kernel loads its code bytes as one 8-byte piece per lane (codes_to_lanes): the
+// lds_tile_io kernels, and the fp32 update-SR kernels of the recipes, where it replaces eight
+// 2-byte loads per lane and tile (Llama-3-8B ZIP-SR: 20.70 -> 20.38 ms per launch).  The fp32
+// round-to-nearest kernels keep the 2-byte loads: the code words' registers made them spill.
+constexpr bool lds_code_io(int m1k, int m2k, int d) {
+    return lds_tile_io(m1k, m2k, d) ||
+           (d == D_F32 && kind_of(m1k) != K_ANY && kind_of(m2k) == K_USR && (flags_of(m2k) & AW4_MOMENT_SAMPLED_READ) == 0);
+}
 
 // Raw inputs of one lane for one wave tile (blocks blk0 .. blk0+7; lane's block blk0 + lane/8).
 template <int M1K, int M2K, int D>
@@ -354,7 +362,7 @@ __device__ __forceinline__ void load_tile(const aw4_tensor& T, const TileLane& t
         if (quantized) {
             if constexpr (kQ) {
                 const gptr<const uint8_t> codes = gaddr<const uint8_t>(M.codes) + tl.blk0 * (kBlock / 2);
-                if constexpr (lds_tile_io(M1K, M2K, D)) {
+                if constexpr (lds_code_io(M1K, M2K, D)) {
                     // The tile's code bytes in memory order, one 8-byte load per lane (bytes 8 l .. 8 l + 7
                     // of the tile: the words of one quarter for four lanes of block l / 8); codes_to_lanes
                     // hands each lane its own four words through LDS before they are decoded.
@@ -397,7 +405,7 @@ __device__ __forceinline__ void load_tile(const aw4_tensor& T, const TileLane& t
 // which access the same columns of their blocks, spread over the banks.
 __device__ __forceinline__ uint32_t image_column(int grp, int c) { return (uint32_t)(grp * 256 + ((c ^ grp) << 4)); }
 
-// The code words of a loaded tile, from memory order to their lanes (lds_tile_io kernels):
+// The code words of a loaded tile, from memory order to their lanes (lds_code_io kernels):
 // load_tile leaves lane l (block l / 8) with bytes 8 l .. 8 l + 7 of the tile's codes; lane j of
 // block grp decodes the words at bytes 64 grp + 16 q + 2 j (q = 0..3), two to a register (quarters
 // 2h, 2h + 1).  The bytes go through the wave's scratch, which no encode of this tile uses yet;
@@ -406,7 +414,7 @@ __device__ __forceinline__ uint32_t image_column(int grp, int c) { return (uint3
 template <int M1K, int M2K, int D>
 __device__ __forceinline__ void codes_to_lanes(const aw4_tensor& T, const TileLane& tl, TileInputs<M1K, M2K, D>& in,
                                                WaveScratch& ws) {
-    if constexpr (!lds_tile_io(M1K, M2K, D)) return;
+    if constexpr (!lds_code_io(M1K, M2K, D)) return;
     using In = TileInputs<M1K, M2K, D>;
     const bool q1 = In::kQ1 && moment_quantized<M1K>(T.m1), q2 = In::kQ2 && moment_quantized<M2K>(T.m2);
     if (!q1 && !q2) return;

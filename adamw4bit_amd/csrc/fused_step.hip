@@ -91,8 +91,7 @@ __host__ __device__ inline int lut_id_of(int rounding, int codebook, int flags) 
 template <bool kUpd>
 struct LdsSlots {
     float cb[2][16];
-    float sqrt_level[2][16];
-    float sqrt_gap[2][kPairs];
+    UsrPair usr[2][kPairs];
     PairEntry pairs[2][kPairs];
     float2 dec[2][256];
     LutEntry lut[2][AW4_LUT_ENTRIES];
@@ -100,7 +99,7 @@ struct LdsSlots {
     f32x4 m2_stage[kUpd ? kWavesPerGroup * 4 * 64 : 1];  // second moments of a tile (update-SR kernels)
 
     __device__ MomentTables moment(const aw4_moment&, int which) const {
-        return MomentTables{cb[which], pairs[which], dec[which], lut[which], sqrt_level[which], sqrt_gap[which]};
+        return MomentTables{cb[which], pairs[which], dec[which], lut[which], usr[which]};
     }
     __device__ f32x4* wave_m2_stage(int wslot) { return kUpd ? &m2_stage[wslot * 4 * 64] : nullptr; }
     __device__ void load(const Tables* g, const StepHeader* h) {
@@ -108,8 +107,7 @@ struct LdsSlots {
         for (int w = 0; w < 2; ++w) {
             if (cbs[w] < 0) continue;
             for (int i = threadIdx.x; i < 16; i += kThreads) cb[w][i] = g->codebook[cbs[w]][i];
-            for (int i = threadIdx.x; i < 16; i += kThreads) sqrt_level[w][i] = g->sqrt_level[cbs[w]][i];
-            for (int i = threadIdx.x; i < kPairs; i += kThreads) sqrt_gap[w][i] = g->sqrt_gap[cbs[w]][i];
+            for (int i = threadIdx.x; i < kPairs; i += kThreads) usr[w][i] = g->usr[cbs[w]][i];
             for (int i = threadIdx.x; i < kPairs; i += kThreads) pairs[w][i] = g->pairs[cbs[w]][i];
             for (int i = threadIdx.x; i < 256; i += kThreads) dec[w][i] = g->dec[cbs[w]][i];
             for (int i = threadIdx.x; i < AW4_LUT_ENTRIES; i += kThreads) lut[w][i] = g->lut[luts[w]][i];
@@ -127,7 +125,7 @@ struct LdsAll {
         const int cbid = m.rounding == AW4_ROUND_FP32 ? 0 : m.codebook;
         return MomentTables{t.codebook[cbid], t.pairs[cbid], t.dec[cbid],
                             t.lut[m.rounding == AW4_ROUND_FP32 ? 0 : lut_id_of(m.rounding, cbid, m.flags)],
-                            t.sqrt_level[cbid], t.sqrt_gap[cbid]};
+                            t.usr[cbid]};
     }
     __device__ f32x4* wave_m2_stage(int) { return nullptr; }
     __device__ void load(const Tables* g, const StepHeader*) {
@@ -460,14 +458,17 @@ const HostTables& host_tables() {
         for (int c = 0; c < AW4_NUM_CODEBOOKS; ++c) {
             for (int k = 0; k < 16; ++k) t.codebook[c][k] = host_f(kCodebookBits[c][k]);
             // square roots of the levels and of their gaps, in double, rounded once to fp32
+            float sqrt_level[16];
             for (int k = 0; k < 16; ++k) {
                 const double l = (double)t.codebook[c][k];
-                t.sqrt_level[c][k] = l > 0.0 ? (float)sqrt(l) : 0.0f;
+                sqrt_level[k] = l > 0.0 ? (float)sqrt(l) : 0.0f;
             }
             for (int i = 0; i < kPairs; ++i) {
                 const int lo = i > 0 ? i - 1 : 0, hi = i < 15 ? i : 15;
                 const double a = (double)t.codebook[c][lo], b = (double)t.codebook[c][hi];
-                t.sqrt_gap[c][i] = (a >= 0.0 && b > a) ? (float)(sqrt(b) - sqrt(a)) : 0.0f;
+                const float gap = (a >= 0.0 && b > a) ? (float)(sqrt(b) - sqrt(a)) : 0.0f;
+                t.usr[c][i] = UsrPair{sqrt_level[lo], sqrt_level[hi], ldexpf(gap, -24),
+                                      t.codebook[c][hi] > t.codebook[c][lo] ? 1.0f : 0.0f};
                 PairEntry& p = t.pairs[c][i];
                 p.a = t.codebook[c][lo];
                 p.b = t.codebook[c][hi];

@@ -152,7 +152,7 @@ def test_fixed_lane_indices_stay_in_their_arrays():
     """Indices that depend on the lane only (update_sr_tables, the code stage, decode4)."""
     j = np.arange(8)
     h = np.arange(2)[:, None]
-    pre = j + 8 * h                     # E(l) of the 16 levels, two per lane
+    pre = j + 8 * h                     # usr_level_preconds: the 16 levels, two per lane
     entry = 1 + j + 8 * h               # update-SR entries 1..16, two per lane (entry 0: lane 0)
     assert pre.min() == 0 and pre.max() == N_LEVELS - 1 and len(np.unique(pre)) == N_LEVELS
     assert entry.min() == 1 and entry.max() == N_PAIRS - 1 and len(np.unique(entry)) == N_PAIRS - 1
