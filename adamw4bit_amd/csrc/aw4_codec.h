@@ -176,17 +176,20 @@ __device__ __forceinline__ void wave_lds_sync() {
 // and Q here is rounded too; the two decisions provably agree when
 //   |Q| > 2^-19 * (E(b) / c + sqrt(b))
 // (32 units of 2^-24: the bound, first order in 2^-24, is 20.05 units times E(b) / c for the
-// reference's rounding and 24.01 units times sqrt(b) for Q's).  For levels <= 1 this is at most
-// the block's band 2^-19 * (2 + eps / c).  Values inside it (a few in 10^5, where f(a) and f(b)
-// are close) take usr_exact, the reference's own operations.  The interval is valid when b > a
+// reference's rounding and 24.01 units times sqrt(b) for Q's).  The band is taken per value as
+// 2^-18 * sqrt(b) + 2^-19 * eps / c (E(b) / c = sqrt(b) + eps / c; the computed band is within a
+// few ulps of that, far inside the slack of 32 units against 20.05 and 24.01): most values sit
+// on the small levels of their block, where it is several times narrower than the bound for
+// b = 1.  Values inside it (about 1 in 10^5 on heavy-tailed second moments) take usr_exact,
+// the reference's own operations.  The interval is valid when b > a
 // and fp32 f(a) > f(b); the latter is certain when c * (sqrt(b) - sqrt(a)) > 2^-20 * E(b) (the
 // true relative gap of f(a) and f(b) against their 5-ulp rounding); a block where it is not
 // (c tiny against eps) decides every value with usr_exact.
 constexpr float kUsrBand = 0x1p-19f;
 
 struct UsrBlock {
-    float c;     // sqrt(s / bias), within 3 ulps
-    float band;  // the block's decision band (+inf: decide every value exactly)
+    float c;      // sqrt(s / bias), within 3 ulps
+    float band0;  // the block's part of the band, 2^-19 * eps / c (+inf: decide every value exactly)
 };
 
 // The block's 17 UpdEntry of the searchsorted indices (two per lane), each from its own level pair:
@@ -222,8 +225,8 @@ __device__ __forceinline__ UsrBlock update_sr_tables(const MomentTables& L, int 
     all = min(all, dpp_u32<kQuadXor2>(all));
     all = min(all, dpp_u32<kHalfRowMirror>(all));
     wave_lds_sync();
-    const float band = kUsrBand * __builtin_fmaf(M.sr_eps, c_rcp, 2.0f);
-    return UsrBlock{c, all ? band : __builtin_inff()};
+    const float band0 = kUsrBand * (M.sr_eps * c_rcp);
+    return UsrBlock{c, all ? band0 : __builtin_inff()};
 }
 
 // Uniforms of this lane's 4 values of quarter q in its block (block blk0 + grp of one write
@@ -235,7 +238,7 @@ __device__ __forceinline__ UsrBlock update_sr_tables(const MomentTables& L, int 
 // quarter q reads words 3q .. 3q+2.  The loop over q must be unrolled (constant indices).
 __device__ __forceinline__ void draws_quarter(const aw4_moment& M, int64_t blk0, int grp, int j, int q, bool active,
                                               uint32_t (&rw)[12], float (&u)[4]) {
-    if (M.flags & AW4_MOMENT_EXT_DRAWS) {
+    if (__builtin_expect((M.flags & AW4_MOMENT_EXT_DRAWS) != 0, 0)) {
         f32x4 v = {0.f, 0.f, 0.f, 0.f};
         if (active)
             v = *(gptr<const f32x4>)(gaddr<const float>(M.draws) + (blk0 + grp) * kBlock + 32 * q + 4 * j);
@@ -279,13 +282,14 @@ __device__ __forceinline__ void usr_level_preconds(const MomentTables& L, int j,
 }
 
 // The quick decision (see update_sr_tables): returns Q, where Q > 0 means lower; `sure` is false
-// inside the band.  U = u * 2^24.
+// inside the value's band 2^-18 * sqrt(b) + band0.  U = u * 2^24.
 __device__ __forceinline__ float usr_quick(const UpdEntry& ue, const UsrBlock& ub, float eps, float x, float U,
                                            bool& sure) {
     const float w = sqrt_faithful(x);
     const float ex = __builtin_fmaf(ub.c, w, eps);
     const float q = __builtin_fmaf(-U, ue.g * ex, ue.sqrt_hi - w);
-    sure = !(__builtin_fabsf(q) <= ub.band);  // NaN: sure (entry 0, or a zero draw with g = +inf)
+    // NaN: sure (entry 0, whose sqrt_hi is NaN, or a zero draw with g = +inf)
+    sure = !(__builtin_fabsf(q) <= __builtin_fmaf(ue.sqrt_hi, 2.0f * kUsrBand, ub.band0));
     return q;
 }
 
@@ -436,7 +440,7 @@ __device__ __forceinline__ BlockScales encode_block(const aw4_moment& M, const M
                 // that slot open; the quarter's branch is uniform).  Where the quick test was sure
                 // the two agree.  It leaves code = idx - lower with idx in [0, 15], the clamps folded
                 // into lower and idx.
-                if (unsure != 0) {
+                if (__builtin_expect(unsure != 0, 0)) {  // laid out after the loop (cold)
                     // the levels' preconditioners once per block encode, when a quarter first needs them
                     if (!level_preconds) {
                         usr_level_preconds(L, j, s, M, sc.pre);

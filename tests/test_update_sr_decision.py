@@ -4,8 +4,8 @@ Update-SR (``_compiled_quantization.py:74-109``) picks the lower level with prob
 P = (f(x) - f(b)) / (f(a) - f(b)), f(l) = 1 / (sqrt((s * l) / bias) + eps), every step rounded
 in fp32.  The kernel decides most values with a rounded form of the exact identity
 u < P  <=>  Q = (sqrt(b) - sqrt(x)) - u * g * E(x) > 0,  E(l) = c * sqrt(l) + eps,
-c = sqrt(s / bias), g = (sqrt(b) - sqrt(a)) / E(a), and sends every value with |Q| inside the
-block's band 2^-19 * (2 + eps / c) to the reference's own operations.  This test restates
+c = sqrt(s / bias), g = (sqrt(b) - sqrt(a)) / E(a), and sends every value with |Q| inside its
+band 2^-18 * sqrt(b) + 2^-19 * eps / c to the reference's own operations.  This test restates
 that quick test in numpy fp32 -- with the hardware's faithful square roots and reciprocals
 taken one ulp off in either direction -- and checks on random blocks, intervals, values and
 draws that wherever it is sure, its decision equals the reference's, whether the host's
@@ -75,7 +75,9 @@ def quick(s, bias, eps, a_idx, b_idx, x, U, cb, rng, band_scale=1.0):
     w = ulp_shift(sqrt_cr(x), jit() * (x > 0))
     ex = fma32(c, w, eps)
     qv = fma32(-U, (g * ex).astype(F32), (sq[b_idx] - w).astype(F32))
-    band = (F32(2.0 ** -19 * band_scale) * fma32(eps, c_rcp, np.full(n, 2, F32))).astype(F32)
+    # the value's band: 2^-18 sqrt(b) + 2^-19 eps / c (the kernel's per-value form)
+    band0 = (F32(2.0 ** -19 * band_scale) * (eps * c_rcp).astype(F32)).astype(F32)
+    band = fma32(sq[b_idx], np.full(n, 2.0 ** -18 * band_scale, F32), band0)
     # a NaN Q counts as sure: a zero draw where g = +inf (E(a) = 0), whose P is 0
     # the block's intervals are all certain when c * gap > 2^-20 * E(b) for each; here the
     # value's own interval stands in (a block where any is uncertain decides exactly anyway)
