@@ -10,7 +10,11 @@ Flags that are part of the numerical contract:
                       explicitly (lerp) and nothing else.
   (defaults kept)     correctly rounded fp32 division and sqrt, fp32 denormals on.
   -Xclang -target-feature -Xclang -packed-fp32-ops
-                      keep scalar fp32 VALU ops (no packed fp32 instructions).
+                      keep scalar fp32 VALU ops (no packed fp32 instructions).  The
+                      host pass prints that it does not know the feature and ignores
+                      it: clang's -Xarch_device forwards no -Xclang option, so the flag
+                      reaches both passes (tests/test_device_code_rules.py checks that
+                      the device code has no packed fp32 instruction).
 """
 
 from __future__ import annotations
