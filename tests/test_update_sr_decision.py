@@ -162,3 +162,24 @@ def test_a_value_at_its_upper_level_is_never_decided_lower(codebook):
             U = np.where(rng.random(len(x)) < 0.1, F32(0), U).astype(F32)  # zero draws too
             lower, sure, certain = quick(s, bias, eps, a_idx, b_idx, b.copy(), U, cb, rng)
         assert not (sure & certain & lower).any(), codebook
+
+
+def test_certainty_products_stay_normal_for_every_codebook():
+    """The update-SR table build compares c * gap * 2^-24 with 2^-44 * E(b) instead of c * gap with
+    2^-20 * E(b).  Scaling both sides by 2^-24 leaves the comparison exact only while neither
+    product is subnormal: for every codebook's real intervals (b > a >= 0) and the smallest block
+    factor c = sqrt(1e-12 / bias) >= 1e-6, both stay normal."""
+    tiny = np.finfo(F32).tiny
+    c = F32(1e-6)
+    for cbid in q.CODEBOOK_VALUES:
+        cb = np.array(q.CODEBOOK_VALUES[cbid], dtype=F32)
+        a, b = cb[:-1], cb[1:]
+        real = (a >= 0) & (b > a)
+        if not real.any():
+            continue
+        gap = (np.sqrt(b[real].astype(np.float64)) - np.sqrt(a[real].astype(np.float64))).astype(F32)
+        gap_s = (gap * F32(2.0 ** -24)).astype(F32)
+        assert (gap_s.astype(np.float64) == gap.astype(np.float64) * 2.0 ** -24).all(), cbid  # exact scaling
+        assert (c * gap_s >= tiny).all(), cbid
+        e_hi = (c * np.sqrt(b[real].astype(np.float64)).astype(F32)).astype(F32)  # E(b) >= c * sqrt(b) (eps >= 0)
+        assert ((F32(2.0 ** -44) * e_hi).astype(F32) >= tiny).all(), cbid
