@@ -799,14 +799,21 @@ int prepare_step(const aw4_tensor* tensors, int32_t count, StepLaunch& sl) {
     return AW4_OK;
 }
 
-// Tiles per wave of a large launch: three for the kernels that take their tiles in grid order
-// (round to nearest, bound by memory), four for the others.  Measured on the Llama-3-8B fp32
-// set, in-process A/B on two boxes: three took ZE-EDEN from 20.33 to 20.15 ms and from 20.44
-// to 20.26 ms, and ZIP-SR from 21.11 to 21.19 ms (so it keeps four); five cost ZE-EDEN 2%.
-int large_tiles_per_wave(int variant) {
+// Tiles per wave of a large launch (per_cu: tiles per CU, at least 128): three for the kernels
+// that take their tiles in grid order (round to nearest, bound by memory), four for the others,
+// except the bf16 update-SR kernels, which are bound by their instruction issue and gain from
+// loading their workgroup's tables for more tiles: up to twelve, while a launch keeps at least
+// 128 tiles per CU for each tile of a wave (several rounds of workgroups, so the last round is a
+// small share).  Measured on the Llama-3-8B fp32 set, in-process A/B on two boxes: three took
+// ZE-EDEN from 20.33 to 20.15 ms and from 20.44 to 20.26 ms, and ZIP-SR from 21.11 to 21.19 ms
+// (so it keeps four; six and eight cost it 2-3%); five cost ZE-EDEN 2%.  The bf16 mixed set
+// (alternating processes, one box): 2 tiles 17.87 ms, 4 16.98-17.07, 6 16.80-16.83, 8
+// 16.44-16.65, 12 16.35-16.37, 16 16.28-16.38.
+int large_tiles_per_wave(int variant, int64_t per_cu) {
     if (variant < kNumSpecialised) {
         const KernelVariant& kv = kVariants[variant];
         if (tile_order_grid(kv.m1, kv.m2, kv.dtype)) return 3;
+        if (kv.dtype == AW4_BF16) return (int)std::max<int64_t>(kTilesPerWave, std::min<int64_t>(12, per_cu / 128));
     }
     return kTilesPerWave;
 }
@@ -841,7 +848,7 @@ int fill_step_tables(const aw4_tensor* tensors, StepLaunch& sl, int num_cus, voi
         // least 1.  Measured on one 4096^2 ZIP-SR tensor (64 tiles per CU): 4 tiles per wave
         // 52.1-52.2 us, 2 52.7-52.9, 3 56.4-56.6, 1 57.1-57.3; one 1024^2 tensor (4 per CU): 1.
         const int64_t per_cu = acc / (int64_t)num_cus;
-        const int tiles_per_wave = per_cu >= 128 ? large_tiles_per_wave(lg.variant)
+        const int tiles_per_wave = per_cu >= 128 ? large_tiles_per_wave(lg.variant, per_cu)
                                                  : (int)std::max<int64_t>(1, std::min<int64_t>(4, per_cu / 16));
         const int64_t waves = (acc + tiles_per_wave - 1) / tiles_per_wave;
         sl.grid[g] = (waves + kWavesPerGroup - 1) / kWavesPerGroup;
