@@ -808,7 +808,11 @@ int prepare_step(const aw4_tensor* tensors, int32_t count, StepLaunch& sl) {
 // ZE-EDEN from 20.33 to 20.15 ms and from 20.44 to 20.26 ms, and ZIP-SR from 21.11 to 21.19 ms
 // (so it keeps four; six and eight cost it 2-3%); five cost ZE-EDEN 2%.  The bf16 mixed set
 // (alternating processes, one box): 2 tiles 17.87 ms, 4 16.98-17.07, 6 16.80-16.83, 8
-// 16.44-16.65, 12 16.35-16.37, 16 16.28-16.38.
+// 16.44-16.65, 12 16.35-16.37, 16 16.28-16.38.  The fp32 update-SR kernel keeps four consecutive
+// tiles although grid order at 8-24 tiles ran it 3% faster in processes after a first one on
+// their box: as the first process on a fresh box, where the Llama-3-8B set streams slower, the
+// same change cost it 2.5% (21.37 -> 21.90 ms, two boxes each), and 8 or 12 consecutive tiles
+// 2.5-3% (21.91, 22.00 ms); ZE-EDEN lost 4% with four consecutive tiles there (20.4 -> 21.15 ms).
 int large_tiles_per_wave(int variant, int64_t per_cu) {
     if (variant < kNumSpecialised) {
         const KernelVariant& kv = kVariants[variant];
