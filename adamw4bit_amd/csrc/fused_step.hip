@@ -801,10 +801,13 @@ int prepare_step(const aw4_tensor* tensors, int32_t count, StepLaunch& sl) {
 
 // Tiles per wave of a large launch (per_cu: tiles per CU, at least 128): three for the kernels
 // that take their tiles in grid order (round to nearest, bound by memory), four for the others,
-// except the bf16 update-SR kernels, which are bound by their instruction issue and gain from
-// loading their workgroup's tables for more tiles: up to twelve, while a launch keeps at least
-// 128 tiles per CU for each tile of a wave (several rounds of workgroups, so the last round is a
-// small share).  Measured on the Llama-3-8B fp32 set, in-process A/B on two boxes: three took
+// except the bf16 update-SR kernels and the research m2 kernels, which are bound by their
+// instruction issue and gain from loading their workgroup's tables for more tiles: up to twelve,
+// while a launch keeps at least 128 tiles per CU for each tile of a wave (several rounds of
+// workgroups, so the last round is a small share).  The research kernels on the Llama-3-8B fp32
+// set, as the first process on a fresh box (two boxes each), four -> twelve tiles: proxy
+// lookahead 28.4-28.5 -> 27.2-27.4 ms, v-proxy 28.0-28.3 -> 27.4-27.5, pending lookahead
+// 33.5-33.6 -> 32.6-32.7, read-back 23.5-23.7 -> 22.6, store-EDEN 28.0 -> 26.4.  Measured on the Llama-3-8B fp32 set, in-process A/B on two boxes: three took
 // ZE-EDEN from 20.33 to 20.15 ms and from 20.44 to 20.26 ms, and ZIP-SR from 21.11 to 21.19 ms
 // (so it keeps four; six and eight cost it 2-3%); five cost ZE-EDEN 2%.  The bf16 mixed set
 // (alternating processes, one box): 2 tiles 17.87 ms, 4 16.98-17.07, 6 16.80-16.83, 8
@@ -817,7 +820,8 @@ int large_tiles_per_wave(int variant, int64_t per_cu) {
     if (variant < kNumSpecialised) {
         const KernelVariant& kv = kVariants[variant];
         if (tile_order_grid(kv.m1, kv.m2, kv.dtype)) return 3;
-        if (kv.dtype == AW4_BF16) return (int)std::max<int64_t>(kTilesPerWave, std::min<int64_t>(12, per_cu / 128));
+        if (kv.dtype == AW4_BF16 || research_kernel(kv.m2))
+            return (int)std::max<int64_t>(kTilesPerWave, std::min<int64_t>(12, per_cu / 128));
     }
     return kTilesPerWave;
 }
