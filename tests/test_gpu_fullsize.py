@@ -1,8 +1,9 @@
 """The benchmark workloads at full size on the GPU: the Llama-3-8B parameter set (291 tensors,
 8,030,261,248 values) in fp32 under ZE-EDEN and ZIP-SR, and in bf16 under the mixed-scheme
 stress case (ZIP-SR everywhere, the LM head's first moment nf4_sr, every tenth tensor an
-fp32-m2 or EDEN-m2 ablation, 1% zero gradient blocks).  Each step is one launch over all
-tensors, as the benchmark runs it.
+fp32-m2 or EDEN-m2 ablation, 1% zero gradient blocks); and the fp32 set under the reference
+step's research m2 schemes (read-back, store-EDEN, lookahead proxy and pending lookahead).  Each
+step is one launch over all tensors, as the benchmark runs it.
 
 Checked two ways, every step:
 * every tensor, at full size, against what the step guarantees whatever the inputs: finite
@@ -97,6 +98,9 @@ def check_invariants(opt, params, schemes, step):
         if not bool(torch.isfinite(p).all()):
             bad.append((i, "param not finite"))
         for m, scheme, is_eden in (("m1", m1, False), ("m2", m2, eden)):
+            if m == "m2" and "lookahead_pending_exp_avg_sq" in st:  # pending lookahead: fp32 state
+                assert bool(torch.isfinite(st["lookahead_pending_exp_avg_sq"]).all()), (i, m)
+                continue
             if f"{m}_code" not in st:
                 assert bool(torch.isfinite(st[m]).all()), (i, m)
                 continue
@@ -130,6 +134,10 @@ def compare(opt, p, oracle, cpu_param, parted, what, dtype):
             else:
                 assert flips == 0, f"{what} {m} ({ms.scheme}): {flips} flips"
                 assert torch.equal(H.bits(st[f"{m}_scale"]), H.bits(ost[f"{m}_scale"])), (what, m)
+        elif f"{m}_pending" in ost:  # a pending lookahead m2: its sampled fp32 state, bit-exact
+            same = torch.equal(H.bits(st[f"{m}_pending"].reshape(-1)), H.bits(ost[f"{m}_pending"].reshape(-1)))
+            assert same, (what, m)
+            log(f"  {what} {m} ({ms.scheme}): pending state bit-exact")
         else:
             assert torch.equal(H.bits(st[f"{m}_fp32"].reshape(-1)), H.bits(ost[f"{m}_fp32"])), (what, m)
     exact = H.assert_params_close(p, cpu_param, what, steps=STEPS if dtype != torch.float32 else 1,
@@ -139,7 +147,9 @@ def compare(opt, p, oracle, cpu_param, parted, what, dtype):
     return n_parted, stochastic
 
 
-def run_full(monkeypatch, make_opt, schemes, dtype, zero_blocks, sampled, seed):
+def run_full(monkeypatch, make_opt, schemes, dtype, zero_blocks, sampled, seed, init_draws=True):
+    """init_draws: the first step's zero-state encode of a stochastic moment asks for draws (the
+    lookahead schemes store their zero state without any)."""
     shapes = bench.llama3_8b_shapes()
     assert sum(math.prod(s) for s in shapes) == 8_030_261_248 and len(shapes) == 291
     gen = torch.Generator(device=H.DEVICE).manual_seed(seed)
@@ -169,7 +179,7 @@ def run_full(monkeypatch, make_opt, schemes, dtype, zero_blocks, sampled, seed):
             row = tables[k][i]
             offsets = {m: int(row[m]["rng_offset"]) for m, s in (("m1", schemes[i][0]), ("m2", schemes[i][1]))
                        if s != "fp32" and ref.is_stochastic(s)}
-            draws[i].start(offsets, first=(k == 0))
+            draws[i].start(offsets, first=(k == 0 and init_draws))
             oracles[i].step([params[i].grad.cpu()])
             st = H.state_of(opt, params[i])
             for m, ms in (("m1", oracles[i].states[0].m1), ("m2", oracles[i].states[0].m2)):
@@ -217,3 +227,18 @@ def test_llama3_8b_bf16_mixed_full_size(monkeypatch):
     assert schemes[5][1] == "fp32" and schemes[15][2] and schemes[HEAD][0] == "nf4_sr"
     sampled = [0] + LAYER0 + [15, FINAL_NORM, HEAD]  # 5: fp32-m2 ablation, 15: EDEN-m2 ablation
     run_full(monkeypatch, make, schemes, torch.bfloat16, 0.01, sampled, seed=43)
+
+
+@pytest.mark.parametrize("m2", ["dyn4_upd_sr", "dyn4_upd_sr_store_eden", "dyn4_proxy_la_upd_sr", "dyn4_la_upd_sr"])
+def test_llama3_8b_research_m2_full_size(monkeypatch, m2):
+    """The reference step's research m2 schemes over the whole Llama-3-8B fp32 set (one launch of
+    their specialised kernel, twelve tiles per wave at this size), NF4 m1: invariants on every
+    tensor, and the oracle on the first layer's small tensors and the norms (codes, scales and the
+    pending lookahead state bit-exact; store-EDEN's kept 1 / denominator is checked at smaller
+    sizes by test_gpu_step.py)."""
+    log(f"Llama-3-8B fp32 at full size, nf4 + {m2}, {STEPS} steps")
+    make = lambda ps: aw.QuantizedAdamW(ps, m1_quant_scheme="nf4", m2_quant_scheme=m2,  # noqa: E731
+                                        optimized=True, quant_rng_seed=0)
+    schemes = [("nf4", m2, False)] * 291
+    sampled = [2, 3, 8, 9, FINAL_NORM]  # k and v projections (1024x4096), the layer's RMSNorm vectors
+    run_full(monkeypatch, make, schemes, torch.float32, 0.0, sampled, seed=47, init_draws="la" not in m2)
