@@ -773,9 +773,10 @@ __device__ __forceinline__ bool values_only(const aw4_tensor& T) {
 // Tile order: grid order (wave w takes tiles w, w + W, ...) or consecutive tiles per wave
 // (w * K .. w * K + K - 1).  Prefetch: the next tile's loads are issued during the second
 // moment's encode.  Both keep the in-flight tiles of a memory-bound kernel adjacent and
-// its loads early; a kernel bound by its arithmetic (update-SR) pays for the prefetched
-// registers and runs the plain order.  The generic kernel (run-time kinds and dtype) has
-// the register pressure of every variant at once and loads each tile when it starts it.
+// its loads early.  The bf16 update-SR kernels, bound by their instruction issue, take
+// consecutive tiles (grid order cost them 2% at twelve tiles per wave, for its per-tile tensor
+// search).  The generic kernel (run-time kinds and dtype) has the register pressure of every
+// variant at once and loads each tile when it starts it.
 // Kernel instances for the reference step's research m2 variants: m2 read back after its
 // encode (AW4_MOMENT_SAMPLED_READ in the m2 spec's flags) and lookahead update-SR
 // (AW4_ROUND_LOOKAHEAD_SR); the generic one (any kind, marked by the flag) runs both.
@@ -788,7 +789,7 @@ constexpr bool prefetch_next_tile(int m1k, int m2k, int d) {
     return kind_of(m1k) != K_ANY && kind_of(m2k) != K_ANY && d != D_ANY && !research_kernel(m2k);
 }
 constexpr bool tile_order_grid(int m1k, int m2k, int d) {
-    return prefetch_next_tile(m1k, m2k, d) && kind_of(m2k) != K_USR;
+    return prefetch_next_tile(m1k, m2k, d) && !(kind_of(m2k) == K_USR && d == D_BF16);
 }
 // Update-SR kernels stage the new second moments in LDS (M2Staged) so that the prefetched
 // inputs fit in the registers of four waves per SIMD.

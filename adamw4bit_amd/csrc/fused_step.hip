@@ -800,27 +800,29 @@ int prepare_step(const aw4_tensor* tensors, int32_t count, StepLaunch& sl) {
 }
 
 // Tiles per wave of a large launch (per_cu: tiles per CU, at least 128): three for the kernels
-// that take their tiles in grid order (round to nearest, bound by memory), four for the others,
-// except the bf16 update-SR kernels and the research m2 kernels, which are bound by their
-// instruction issue and gain from loading their workgroup's tables for more tiles: up to twelve,
-// while a launch keeps at least 128 tiles per CU for each tile of a wave (several rounds of
-// workgroups, so the last round is a small share).  The research kernels on the Llama-3-8B fp32
-// set, as the first process on a fresh box (two boxes each), four -> twelve tiles: proxy
-// lookahead 28.4-28.5 -> 27.2-27.4 ms, v-proxy 28.0-28.3 -> 27.4-27.5, pending lookahead
-// 33.5-33.6 -> 32.6-32.7, read-back 23.5-23.7 -> 22.6, store-EDEN 28.0 -> 26.4.  Measured on the Llama-3-8B fp32 set, in-process A/B on two boxes: three took
-// ZE-EDEN from 20.33 to 20.15 ms and from 20.44 to 20.26 ms, and ZIP-SR from 21.11 to 21.19 ms
-// (so it keeps four; six and eight cost it 2-3%); five cost ZE-EDEN 2%.  The bf16 mixed set
-// (alternating processes, one box): 2 tiles 17.87 ms, 4 16.98-17.07, 6 16.80-16.83, 8
-// 16.44-16.65, 12 16.35-16.37, 16 16.28-16.38.  The fp32 update-SR kernel keeps four consecutive
-// tiles although grid order at 8-24 tiles ran it 3% faster in processes after a first one on
-// their box: as the first process on a fresh box, where the Llama-3-8B set streams slower, the
-// same change cost it 2.5% (21.37 -> 21.90 ms, two boxes each), and 8 or 12 consecutive tiles
-// 2.5-3% (21.91, 22.00 ms); ZE-EDEN lost 4% with four consecutive tiles there (20.4 -> 21.15 ms).
+// that take their tiles in grid order (all specialised ones but the bf16 update-SR and research
+// kernels; bound by memory, or memory and issue together); up to twelve for the
+// bf16 update-SR kernels and the research m2 kernels, which are bound by their instruction issue
+// and gain from loading each workgroup's tables for more tiles, while a launch keeps at least 128
+// tiles per CU for each tile of a wave (several rounds of workgroups, so the last round is a
+// small share); four for the rest.  Measured on the Llama-3-8B sets with alternating processes,
+// ranked as the first process on a fresh box (where the fp32 set streams slower; two boxes per
+// variant), which is how the benchmark runs:
+//   ZIP-SR fp32: grid order 2 tiles 21.80-22.09 ms, 3 20.83-21.01, 4 21.10-21.16, 12 21.89-21.90;
+//     consecutive tiles 2 21.47, 3 21.16-21.19, 4 21.25-21.37, 8 21.90, 12 21.99-22.00 (in later
+//     processes on a box grid order at 4-24 tiles ran 19.1-19.6 ms, consecutive 4 19.7-19.8);
+//   ZE-EDEN: grid order 2 20.24-20.44, 3 20.33-20.52, 4 20.49-20.50, 12 as 3 in later processes;
+//     consecutive 4 21.14-21.16;
+//   the bf16 mixed set (consecutive tiles, later processes): 2 tiles 17.87 ms, 4 16.98-17.07,
+//     6 16.80-16.83, 8 16.44-16.65, 12 16.35-16.37, 16 16.28-16.38; in grid order at 12, 2% slower;
+//   the research kernels (first process), four -> twelve tiles: proxy lookahead 28.4-28.5 ->
+//     27.2-27.4 ms, v-proxy 28.0-28.3 -> 27.4-27.5, pending lookahead 33.5-33.6 -> 32.6-32.7,
+//     read-back 23.5-23.7 -> 22.6, store-EDEN 28.0 -> 26.4.
 int large_tiles_per_wave(int variant, int64_t per_cu) {
     if (variant < kNumSpecialised) {
         const KernelVariant& kv = kVariants[variant];
         if (tile_order_grid(kv.m1, kv.m2, kv.dtype)) return 3;
-        if (kv.dtype == AW4_BF16 || research_kernel(kv.m2))
+        if ((kind_of(kv.m2) == K_USR && kv.dtype == AW4_BF16) || research_kernel(kv.m2))
             return (int)std::max<int64_t>(kTilesPerWave, std::min<int64_t>(12, per_cu / 128));
     }
     return kTilesPerWave;
