@@ -1,8 +1,10 @@
 """Build the HIP library ``libadamw4bit_hip.so`` in-tree for gfx950.
 
 ``python -m adamw4bit_amd.build`` compiles ``csrc/fused_step.hip`` with hipcc
-(no GPU needed: hipcc cross-compiles for ``--offload-arch=gfx950``).  The
-library lands next to this file so it travels with the source tree.
+(no GPU needed: hipcc cross-compiles for ``--offload-arch=gfx950``) twice: the
+main object, and one with ``AW4_SCHED_ILP_TU`` that holds only the four-wave
+update-SR kernels, scheduled by LLVM's max-ilp strategy; one link makes the
+library.  It lands next to this file so it travels with the source tree.
 
 Flags that are part of the numerical contract:
   -ffp-contract=off   no implicit multiply-add fusion; the kernel writes each
@@ -23,6 +25,7 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
@@ -39,26 +42,60 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
 
 
-def command(output: str = LIBRARY, extra=()) -> list:
+# The second object: the same source with AW4_SCHED_ILP_TU, which emits only the four-wave
+# update-SR kernels, scheduled by LLVM's max-ilp strategy (the source says why).
+ILP_FLAGS = ("-DAW4_SCHED_ILP_TU", "-mllvm", "-amdgpu-sched-strategy=max-ilp")
+
+
+def compile_command(output: str, ilp: bool = False, extra=()) -> list:
+    """hipcc line for one object of the library (the main one, or with ilp the second)."""
     return [
-        hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+        hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
         "-ffp-contract=off",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-Wall", "-Wno-unused-function",
-        f"-I{INCLUDE}", f"-I{os.path.dirname(SOURCE)}", SOURCE, "-o", output, *extra,
+        f"-I{INCLUDE}", f"-I{os.path.dirname(SOURCE)}", *(ILP_FLAGS if ilp else ()),
+        "-c", SOURCE, "-o", output, *extra,
     ]
 
 
+def link_command(objects, output: str) -> list:
+    return [hipcc(), "-shared", "-fPIC", *objects, "-o", output]
+
+
+def assembly_commands(directory: str) -> list:
+    """(hipcc line, output path) for the gfx950 assembly of both objects' device code."""
+    out = []
+    for ilp in (False, True):
+        path = os.path.join(directory, "fused_step_ilp.s" if ilp else "fused_step.s")
+        cmd = [a for a in compile_command(path, ilp) if a not in ("-fPIC", "-c")] + ["--cuda-device-only", "-S"]
+        out.append((cmd, path))
+    return out
+
+
+def _run(cmds, verbose: bool) -> None:
+    procs = []
+    for cmd in cmds:
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append(subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True))
+    failed = None
+    for proc in procs:
+        out, err = proc.communicate()
+        if proc.returncode != 0 and failed is None:
+            sys.stderr.write(out + err)
+            failed = proc.returncode
+    if failed is not None:
+        raise RuntimeError(f"hipcc failed with exit code {failed}")
+
+
 def build(verbose: bool = False) -> str:
-    """Compile the library (always) and return its path."""
-    tmp = LIBRARY + ".tmp"
-    cmd = command(tmp)
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    if proc.returncode != 0:
-        sys.stderr.write(proc.stdout + proc.stderr)
-        raise RuntimeError(f"hipcc failed with exit code {proc.returncode}")
+    """Compile the library (always) and return its path: two objects in parallel, then one link."""
+    with tempfile.TemporaryDirectory() as tmpdir:
+        objects = [os.path.join(tmpdir, "fused_step.o"), os.path.join(tmpdir, "fused_step_ilp.o")]
+        _run([compile_command(objects[0]), compile_command(objects[1], ilp=True)], verbose)
+        tmp = LIBRARY + ".tmp"
+        _run([link_command(objects, tmp)], verbose)
     os.replace(tmp, LIBRARY)
     return LIBRARY
 

@@ -42,16 +42,21 @@
 #include <vector>
 
 #include "adamw4bit_hip.h"
-#include "aw4_prologue.h"
+#ifndef AW4_SCHED_ILP_TU
+#include "aw4_prologue.h"  // its kernels belong to the main object only
+#endif
 #include "aw4_step.h"
 
 // Device memory the library holds without allocating it: file-scope arrays, one copy per GPU,
 // kept until the process ends.  g_tables_mem holds the codebook and lookup tables every kernel
 // reads; `scratch` holds the launch tables of aw4_fused_step_noalloc.  In host code these names
 // are stand-ins, not device addresses: the host takes each GPU's address of them with
-// hipGetSymbolAddress (device_state) and uses only that.
+// hipGetSymbolAddress (device_state) and uses only that.  (Only the main object holds them: the
+// second compile of this file, AW4_SCHED_ILP_TU below, emits kernels and nothing else.)
+#ifndef AW4_SCHED_ILP_TU
 static __device__ __align__(256) uint8_t g_tables_mem[sizeof(aw4::Tables)];
 static __device__ __align__(256) uint8_t scratch[AW4_NOALLOC_TABLE_BYTES];
+#endif
 
 namespace {
 
@@ -215,6 +220,31 @@ step_kernel_inline_4w(const InlineArgs a) {
     step_body_inline<M1K, M2K, D>(a);
 }
 
+}  // namespace
+
+// The four-wave update-SR kernels (ZIP-SR's fp32 and bf16 steps, the bf16 nf4_sr head and
+// EDEN-m2 ablation) come from a second compile of this file, with AW4_SCHED_ILP_TU defined and
+// LLVM's max-ilp machine scheduler (-mllvm -amdgpu-sched-strategy=max-ilp); that object holds
+// nothing else.  Bound by their instruction issue, they ran 1.2-1.5% faster under it (ZIP-SR on
+// the Llama-3-8B fp32 set 19.40-19.55 against 19.77-19.85 ms, the bf16 set 16.28-16.49 against
+// 16.49-16.72 ms per step; alternating processes on one box, five each), while ZE-EDEN spills
+// under it and ran 4% slower, so every other kernel keeps the default scheduler.  The main
+// object declares them and launches them through the variant table.
+namespace aw4_ilp {
+template <int M1K, int M2K, int D>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4)))
+step_kernel_4w(const aw4::StepHeader* __restrict__ hdr, const aw4::Tables* __restrict__ tables)
+#ifdef AW4_SCHED_ILP_TU
+{
+    step_body<M1K, M2K, D>(hdr, tables);
+}
+#else
+    ;
+#endif
+}  // namespace aw4_ilp
+
+namespace {
+
 // The instantiated kernels; the host groups a step's tensors by the variant whose moment
 // specs and dtype they match (optimized-path flags).  ZE-EDEN: NF4 round-to-nearest m1,
 // Dyn4 round-to-nearest m2 with EDEN.  ZIP-SR: NF4 round-to-nearest m1, Dyn4 update-SR m2
@@ -234,6 +264,18 @@ constexpr int kLaStore = mspec(K_LA);
 constexpr int kLaPending = mspec(K_LA, AW4_MOMENT_PENDING);
 // Any m2 kind of the research schemes (read-back and lookahead), any dtype.
 constexpr int kAnyResearch = mspec(K_ANY, AW4_MOMENT_SAMPLED_READ);
+
+#ifdef AW4_SCHED_ILP_TU
+}  // namespace
+
+template __global__ void aw4_ilp::step_kernel_4w<kRtn, kUsrGuarded, D_F32>(const aw4::StepHeader*, const aw4::Tables*);
+template __global__ void aw4_ilp::step_kernel_4w<kRtn, kUsrGuarded, D_BF16>(const aw4::StepHeader*, const aw4::Tables*);
+template __global__ void aw4_ilp::step_kernel_4w<kSsrGuarded, kUsrGuarded, D_BF16>(const aw4::StepHeader*,
+                                                                                   const aw4::Tables*);
+template __global__ void aw4_ilp::step_kernel_4w<kRtn, kUsrGuardedEden, D_BF16>(const aw4::StepHeader*,
+                                                                                const aw4::Tables*);
+#else
+
 struct KernelVariant {
     int m1, m2, dtype;
     const void* fn;
@@ -247,12 +289,16 @@ struct KernelVariant {
     {M1, M2, D, (const void*)&step_kernel<M1, M2, D>, (const void*)&step_kernel_inline<M1, M2, D>}
 #define AW4_VARIANT_I4W(M1, M2, D) \
     {M1, M2, D, (const void*)&step_kernel_4w<M1, M2, D>, (const void*)&step_kernel_inline_4w<M1, M2, D>}
+// the max-ilp instances of the second object (their small-step instances stay in this one)
+#define AW4_VARIANT_ILP(M1, M2, D) {M1, M2, D, (const void*)&aw4_ilp::step_kernel_4w<M1, M2, D>, nullptr}
+#define AW4_VARIANT_ILP_I4W(M1, M2, D) \
+    {M1, M2, D, (const void*)&aw4_ilp::step_kernel_4w<M1, M2, D>, (const void*)&step_kernel_inline_4w<M1, M2, D>}
 const KernelVariant kVariants[] = {
-    AW4_VARIANT_I4W(kRtn, kRtnEden, D_F32),       AW4_VARIANT_I4W(kRtn, kUsrGuarded, D_F32),
-    AW4_VARIANT_I4W(kRtn, kRtnEden, D_BF16),      AW4_VARIANT_I4W(kRtn, kUsrGuarded, D_BF16),
-    AW4_VARIANT(kSsrGuarded, kUsrGuarded, D_F32), AW4_VARIANT_4W(kSsrGuarded, kUsrGuarded, D_BF16),
+    AW4_VARIANT_I4W(kRtn, kRtnEden, D_F32),       AW4_VARIANT_ILP_I4W(kRtn, kUsrGuarded, D_F32),
+    AW4_VARIANT_I4W(kRtn, kRtnEden, D_BF16),      AW4_VARIANT_ILP_I4W(kRtn, kUsrGuarded, D_BF16),
+    AW4_VARIANT(kSsrGuarded, kUsrGuarded, D_F32), AW4_VARIANT_ILP(kSsrGuarded, kUsrGuarded, D_BF16),
     AW4_VARIANT(kRtn, kFp32, D_F32),              AW4_VARIANT(kRtn, kFp32, D_BF16),
-    AW4_VARIANT(kRtn, kUsrGuardedEden, D_F32),    AW4_VARIANT_4W(kRtn, kUsrGuardedEden, D_BF16),
+    AW4_VARIANT(kRtn, kUsrGuardedEden, D_F32),    AW4_VARIANT_ILP(kRtn, kUsrGuardedEden, D_BF16),
     AW4_VARIANT(kRtn, kUsrRead, D_F32),           AW4_VARIANT(kRtn, kUsrReadEden, D_F32),
     AW4_VARIANT(kRtn, kLaStore, D_F32),           AW4_VARIANT_3W(kRtn, kLaPending, D_F32),
     AW4_VARIANT_2W(K_ANY, kAnyResearch, D_ANY),
@@ -264,6 +310,8 @@ const KernelVariant kVariants[] = {
 #undef AW4_VARIANT_3W
 #undef AW4_VARIANT_I
 #undef AW4_VARIANT_I4W
+#undef AW4_VARIANT_ILP
+#undef AW4_VARIANT_ILP_I4W
 constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 constexpr int kGenericVariant = kNumVariants - 1;
 constexpr int kResearchVariant = kNumVariants - 2;  // generic, for read-back and lookahead m2
@@ -1203,3 +1251,5 @@ int aw4_uniforms(uint64_t seed, uint64_t offset, int64_t n, float* out, void* st
 }
 
 }  // extern "C"
+
+#endif  // AW4_SCHED_ILP_TU

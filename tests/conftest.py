@@ -32,17 +32,19 @@ def pytest_collection_modifyitems(config, items):
 
 @pytest.fixture(scope="session")
 def device_assembly():
-    """The gfx950 assembly of the library's own source, compiled here with the library's flags
-    (hipcc cross-compiles; no GPU needed).  One compile serves every test of the session."""
+    """The gfx950 assembly of the library's own source, both of its objects, compiled here with
+    the library's flags (hipcc cross-compiles; no GPU needed).  One compile serves every test of
+    the session."""
     from adamw4bit_amd import build
 
     hipcc = build.hipcc()
     if not os.path.exists(hipcc):
         pytest.skip("hipcc not available")
     with tempfile.TemporaryDirectory() as tmp:
-        out = os.path.join(tmp, "fused_step.s")
-        cmd = [a for a in build.command(out) if a not in ("-shared", "-fPIC")] + ["--cuda-device-only", "-S"]
-        proc = subprocess.run(cmd, capture_output=True, text=True)
-        assert proc.returncode == 0, proc.stderr[-2000:]
-        with open(out) as f:
-            return f.read()
+        text = []
+        for cmd, out in build.assembly_commands(tmp):
+            proc = subprocess.run(cmd, capture_output=True, text=True)
+            assert proc.returncode == 0, proc.stderr[-2000:]
+            with open(out) as f:
+                text.append(f.read())
+        return "\n".join(text)

@@ -36,10 +36,11 @@ def waves_per_simd(vgprs: int) -> int:
 
 @pytest.fixture(scope="module")
 def kernel_vgprs(device_assembly):
-    text = device_assembly
-    meta = text[text.index("amdhsa.kernels"):]
+    # one metadata section per object of the library
+    metas = device_assembly.split("amdhsa.kernels")[1:]
+    assert metas, "no kernel metadata"
     found = {}
-    for block in re.split(r"\n  - \.", meta):
+    for block in (b for meta in metas for b in re.split(r"\n  - \.", meta)):
         name = re.search(r"\.name:\s+(\S+)", block)
         if not name or "step_kernel" not in name.group(1):
             continue
