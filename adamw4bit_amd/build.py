@@ -55,6 +55,9 @@ def compile_command(output: str, ilp: bool = False, extra=()) -> list:
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-Wall", "-Wno-unused-function",
         f"-I{INCLUDE}", f"-I{os.path.dirname(SOURCE)}", *(ILP_FLAGS if ilp else ()),
+        # a fixed compile-unit id per object (clang derives one from the output path otherwise,
+        # a temporary directory's), so that a rebuild gives the same library byte for byte
+        f"-cuid=adamw4bit_{'ilp' if ilp else 'main'}",
         "-c", SOURCE, "-o", output, *extra,
     ]
 
